@@ -1,0 +1,200 @@
+"""Benchmark of the paged-attention hot path on one MI355X.
+
+Headline (the driver's JSON line): BASELINE.json's metric on configs[1], GQA paged decode
+(32 sequences x 1 token, 32 Q / 8 KV heads, hd 128, f16 KV, contexts U[512, 4096], 16-token
+pages): decode KV-read GB/s. One step = one `lmh_attend` call over the whole batch (host
+hand-off + kernels), inputs already resident in HBM. `value` = algorithmic bytes per step /
+wall time per step; `roofline` = the decode kernel's algorithmic bytes / its average duration
+from HIP events recorded on the launch stream inside the timed region.
+
+Also reported (extra keys): every other configuration's throughput and roofline fraction, and the
+CPU baseline (the C++ restatement of the reference's CPU attention, oracle/, on host cores).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
+FP32_PEAK_TFLOPS = 157.3
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
+    import torch
+
+    from llmario_amd import harness
+    from llmario_amd.workloads import Generator, config
+
+    w = config(name)
+    t_load = time.perf_counter()
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    L = w.layer
+    q = torch.from_numpy(gen.q()).cuda()
+    out = torch.empty((w.n_rows, L.n_head, L.hdv), device="cuda")
+    segs = w.segments()
+    stream = torch.cuda.current_stream()
+    log(f"[bench] {name}: loaded in {time.perf_counter() - t_load:.1f}s; warmup {warmup}")
+    for _ in range(warmup):
+        hc.attend(0, segs, q, out, w.scale, w.window, stream)
+    torch.cuda.synchronize()
+    hc.kernel_time()  # reset
+    hc.set_timing(timing_kernel)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        hc.attend(0, segs, q, out, w.scale, w.window, stream)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    hc.set_timing(False)
+    k_ms, launches = hc.kernel_time()
+    ms_step = max(wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps)
+    k_avg = k_ms / max(launches, 1)
+    res = {
+        "config": name, "kv_type": w.kv_type, "rows": w.n_rows, "ms_per_step": ms_step,
+        "kernel_ms": k_avg, "bytes": w.algorithmic_bytes(), "flops": w.flops(),
+    }
+    res["GBps"] = res["bytes"] / (ms_step * 1e-3) / 1e9
+    res["TFLOPs"] = res["flops"] / (ms_step * 1e-3) / 1e12
+    res["kernel_GBps"] = res["bytes"] / (k_avg * 1e-3) / 1e9
+    res["kernel_TFLOPs"] = res["flops"] / (k_avg * 1e-3) / 1e12
+    res["hbm_frac"] = res["kernel_GBps"] / HBM_PEAK_GBS
+    res["mfma_frac"] = res["kernel_TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
+    del hc
+    torch.cuda.empty_cache()
+    log(f"[bench] {name}: {ms_step * 1e3:.1f} us/step, kernel {k_avg * 1e3:.1f} us, "
+        f"{res['kernel_GBps']:.0f} GB/s ({res['hbm_frac']:.1%} HBM), {res['kernel_TFLOPs']:.1f} TFLOP/s")
+    return res
+
+
+def physical_cores() -> int:
+    try:
+        cores = set()
+        phys = core = None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("physical id"):
+                    phys = line.split(":")[1].strip()
+                elif line.startswith("core id"):
+                    core = line.split(":")[1].strip()
+                    cores.add((phys, core))
+        n = len(cores) or os.cpu_count() or 1
+    except OSError:
+        n = os.cpu_count() or 1
+    try:
+        n = min(n, len(os.sched_getaffinity(0)))
+    except AttributeError:
+        pass
+    return max(1, min(n, 16))
+
+
+def cpu_baseline(name: str, seconds: float, threads: int):
+    """The restated reference CPU path (oracle/, a C++ port of attend/attend_split over a
+    reference-layout page store) on this host's cores, same inputs, pages pre-touched."""
+    import oracle as O
+    from llmario_amd.workloads import Generator, config
+
+    O.build()
+    w = config(name)
+    gen = Generator(w)
+    oc = O.empty_cache_for(w)
+    for s in range(w.n_seqs):
+        k, v = gen.kv_rows(s)
+        O.fill(oc, gen.tables[s], s, k, v, w.prior[s])
+    q = gen.q()
+    segs = w.segments()
+    oc.attend(0, segs, q, w.scale, w.window, threads)  # warm-up (touches every page)
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oc.attend(0, segs, q, w.scale, w.window, threads)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or n >= 1000:
+            break
+    per = el / n
+    return {"value": w.algorithmic_bytes() / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{name} full step ({w.n_rows} decode rows, {sum(w.totals)} cached positions), "
+                      f"{n} steps in {el:.1f}s, {per * 1e3:.2f} ms/step"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w", help="other configs to report ('' = none)")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the paged-attention path is single-device here (no "
+              "collectives, no sharding); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    torch.cuda.set_device(0)
+
+    head = time_config("c2", args.steps, args.warmup)
+    extra = {}
+    for name in [x for x in args.extra.split(",") if x]:
+        extra[name] = time_config(name, max(5, min(args.steps, 20)), 3)
+
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+    roof = {"bound": "hbm", "achieved": round(head["kernel_GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(head["hbm_frac"], 4), "traffic": traffic,
+            "kernel": "decode_mfma_kernel<f16,128,128>", "kernel_us": round(head["kernel_ms"] * 1e3, 2),
+            "algorithmic_bytes": head["bytes"]}
+    cpu = None
+    if not args.no_cpu_baseline:
+        th = physical_cores()
+        log(f"[bench] cpu baseline: c2 on {th} threads")
+        cpu = cpu_baseline("c2", args.cpu_seconds, th)
+    line = {
+        "metric": "decode KV-read GB/s (GQA paged decode, configs[1])",
+        "value": round(head["GBps"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) K/V/Q rounded to f16, seeded permuted block tables)",
+        "config": {"workload": "c2: GQA paged decode, 32 seqs x 1 token, 32 Q / 8 KV heads, hd 128, "
+                               "ctx U[512,4096], page 16, f16 KV",
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in {"c2": head, **extra}.items()},
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

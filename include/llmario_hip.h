@@ -1,0 +1,178 @@
+/*
+ * llmario_hip.h — C ABI of the MI355X-native paged-KV attention backend.
+ *
+ * The drop-in boundary for the attention / KV-cache part of LLMario's `ModelBackend`
+ * (crates/engine/model/src/backend.rs:17-106). A Rust `HipBackend` binds these symbols with an
+ * `extern "C"` block. Plain C types only: fixed-width
+ * integers, plain pointers and sizes, opaque handles. Device pointers are HIP device addresses;
+ * `stream` is a `hipStream_t` passed as `void*` (NULL = the default stream).
+ *
+ * Status codes: every entry point returns int32_t LMH_* below. LMH_KV_FULL leaves all state as
+ * it was and reports `needed`/`free` blocks through out-parameters. No C++ exception crosses this
+ * boundary. A handle is single-threaded (the reference's `ModelBackend: Send`, not `Sync`), and
+ * the device work of one handle must be stream-ordered: issue it on one stream, or order the
+ * streams yourself.
+ *
+ * Page layout: blocks of `block_tokens` positions (a multiple of 16), each holding every layer's
+ * K then V for those positions, as the reference's block does (kv.rs:286-324, 402-497); inside a
+ * block each (layer, KV head) owns a contiguous region whose bytes are in the order the decode
+ * and prefill kernels' matrix-core operands want them (so one 16-byte load per lane per operand
+ * chunk reads 1 KiB contiguous per wave). Block ids, reference counts and the LRU free queue follow BlockPool
+ * (kv/src/lib.rs:36-176), so block tables and page indices match the reference bit for bit.
+ */
+#ifndef LLMARIO_HIP_H
+#define LLMARIO_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LMH_ABI_VERSION 1u
+
+/* status codes */
+#define LMH_OK 0
+#define LMH_INVALID_ARGUMENT 1
+#define LMH_KV_FULL 2
+#define LMH_UNSUPPORTED 3
+#define LMH_DEVICE_ERROR 4
+#define LMH_OUT_OF_MEMORY 5
+
+/* KvType (kv.rs:56-63) plus two declared extensions (F32, BF16) the configurations need. */
+#define LMH_KV_F16 0u
+#define LMH_KV_Q8_0 1u
+#define LMH_KV_F32 2u
+#define LMH_KV_BF16 3u
+
+typedef struct lmh_kv lmh_kv; /* opaque: the device page pool + host block bookkeeping */
+
+/* Per attention layer geometry: AttnGeom (model/src/arch.rs:73-95) restricted to what the cache
+ * and the kernels read. */
+typedef struct lmh_layer_desc {
+  uint32_t n_head;
+  uint32_t n_kv;
+  uint32_t hd;
+  uint32_t hdv;
+} lmh_layer_desc;
+
+/* KvOptions (kv.rs:328-375). */
+typedef struct lmh_kv_options {
+  uint32_t abi_version; /* LMH_ABI_VERSION */
+  uint32_t kv_type;     /* LMH_KV_* */
+  uint32_t block_tokens;
+  uint32_t n_layers;
+  const lmh_layer_desc* layers;
+  uint64_t max_ctx;
+  uint64_t n_seqs;
+  uint64_t pool_tokens; /* 0 = None: every sequence can hold max_ctx at once */
+  int32_t device;       /* HIP device ordinal */
+  uint32_t reserved0;
+} lmh_kv_options;
+
+/* KvLayout (kv.rs:377-400): sizes are the reference's for the same options. */
+typedef struct lmh_layout_info {
+  uint64_t block_bytes;
+  uint64_t blocks_per_seq;
+  uint64_t n_seqs;
+  uint64_t pool_blocks;
+  uint64_t max_ctx;
+  uint32_t block_tokens;
+  uint32_t kv_type;
+} lmh_layout_info;
+
+/* SeqTokens (forward.rs:31-35): the attention level needs the count, not the token ids. */
+typedef struct lmh_seq_tokens {
+  uint64_t seq;
+  uint64_t n_tokens;
+} lmh_seq_tokens;
+
+/* Seg (forward.rs:37-47): rows start..start+n of the stacked batch belong to `seq` and sit at
+ * positions pos0..pos0+n. */
+typedef struct lmh_seg {
+  uint64_t seq;
+  uint64_t start;
+  uint64_t n;
+  uint64_t pos0;
+} lmh_seg;
+
+/* ---- handle lifetime (KvCache::with_options, kv.rs:577-603; MetalKv::new, metal/src/kv.rs:66-100) */
+int32_t lmh_kv_create(const lmh_kv_options* opt, lmh_kv** out);
+void lmh_kv_destroy(lmh_kv* kv);
+/* Message of the last failed call on this handle ("" if none). */
+const char* lmh_kv_last_error(const lmh_kv* kv);
+/* Message of the last lmh_kv_create failure on this thread. */
+const char* lmh_create_error(void);
+int32_t lmh_kv_layout(const lmh_kv* kv, lmh_layout_info* out);
+/* Layout hash for snapshots, tagged "hip" (KvCache::fingerprint, kv.rs:983-999). */
+uint64_t lmh_kv_fingerprint(const lmh_kv* kv);
+
+/* ---- sequence bookkeeping (KvCache, kv.rs:640-827; ModelBackend, backend.rs:24-48) ---- */
+int32_t lmh_kv_seq_len(const lmh_kv* kv, uint64_t seq, uint64_t* len);
+/* Set a sequence's cached length directly (the reference tests write `seq_mut(s).len`). */
+int32_t lmh_kv_set_seq_len(lmh_kv* kv, uint64_t seq, uint64_t len);
+int32_t lmh_kv_free_blocks(const lmh_kv* kv, uint64_t* free_blocks);
+int32_t lmh_kv_resident_blocks(const lmh_kv* kv, uint64_t* n);
+int32_t lmh_kv_blocks_needed(const lmh_kv* kv, uint64_t seq, uint64_t new_len, uint64_t* needed);
+int32_t lmh_kv_reserve(lmh_kv* kv, uint64_t seq, uint64_t new_len, uint64_t* needed, uint64_t* free_blocks);
+int32_t lmh_kv_truncate(lmh_kv* kv, uint64_t seq, uint64_t n);
+int32_t lmh_kv_clear(lmh_kv* kv, uint64_t seq);
+/* The sequence's block table (BlockTable::locate, kv/src/lib.rs:243-253): writes up to `cap`
+ * ids, returns the count in *n. */
+int32_t lmh_kv_block_table(const lmh_kv* kv, uint64_t seq, uint32_t* out, uint64_t cap, uint64_t* n);
+/* Test and benchmark hook: give an empty sequence exactly these free blocks, in order (e.g. a
+ * seeded permutation of the pool), as if reserve had handed them out. */
+int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, uint64_t n);
+/* BlockPool per-block state (kv/src/lib.rs:146-167) and prefix-cache hooks (lib.rs:112-143). */
+int32_t lmh_pool_refs(const lmh_kv* kv, uint32_t block, uint32_t* refs);
+int32_t lmh_pool_set_hash(lmh_kv* kv, uint32_t block, const uint8_t hash[32]);
+int32_t lmh_pool_clear_hash(lmh_kv* kv, uint32_t block);
+int32_t lmh_pool_is_cached(const lmh_kv* kv, uint32_t block, int32_t* cached);
+
+/* ---- batch hand-off (Model::forward_batch, forward.rs:207-291) ----
+ * Validates the batch (non-empty, at most n_seqs entries, no sequence twice, no empty entry, no
+ * context overflow), reserves every entry's room all-or-nothing (LMH_KV_FULL changes nothing),
+ * and writes one lmh_seg per entry in batch order (the stacked row order the caller's q/out
+ * arrays use). `segs_out` holds n entries. Lengths do not move until lmh_batch_commit. */
+int32_t lmh_batch_prepare(lmh_kv* kv, const lmh_seq_tokens* batch, uint64_t n, lmh_seg* segs_out,
+                          uint64_t* n_rows, uint64_t* needed, uint64_t* free_blocks);
+/* run_layers' tail (forward.rs:363-366): every segment's sequence grows by its row count. */
+int32_t lmh_batch_commit(lmh_kv* kv, const lmh_seg* segs, uint64_t n_segs);
+
+/* ---- device work (all enqueued on `stream`) ---- */
+/* KvCache::store_k/store_v (kv.rs:870-889) for every row of the segments: k is
+ * [n_rows][n_kv*hd] f32, v is [n_rows][n_kv*hdv] f32 (device), encoded to the cache type
+ * (f16/bf16 round to nearest even; q8_0 as quantize_q8_0, kv.rs:156-171). */
+int32_t lmh_kv_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* k,
+                     const float* v, void* stream);
+/* The same rows given already encoded, in the reference's row format (KvType::store output:
+ * f16/bf16 bits, f32, or q8_0 34-byte blocks): k is [n_rows][k_row] bytes, v [n_rows][v_row]. */
+int32_t lmh_kv_store_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs,
+                             const void* k_rows, const void* v_rows, void* stream);
+/* Parity hooks: read rows back (LayerReader::row, kv.rs:1166-1179), decoded to f32 ... */
+int32_t lmh_kv_gather(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, float* k_out,
+                      float* v_out, void* stream);
+/* ... or in the reference's row encoding, byte for byte. */
+int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs,
+                              void* k_rows, void* v_rows, void* stream);
+
+/* attend (forward.rs:585-678) + attend_split (forward.rs:688-807) in one call: every row t of
+ * the segments (sequence segs[i].seq, position pos0+j) attends causally to positions
+ * p_lo..=pos of its own sequence (p_lo = pos+1-window when window > 0 and pos+1 > window, else 0),
+ * softmax(scale * q.K) V per query head with GQA head kvh = h / (n_head / n_kv); fp32
+ * accumulation. q is [n_rows][n_head][hd] f32, out is [n_rows][n_head][hdv] f32 (device).
+ * Decode rows, split-K over pages and prefill tiles are packed into one work list. */
+int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
+                   float* out, float scale, uint64_t window, void* stream);
+
+/* Timing hook for benchmarks: when enabled, lmh_attend brackets its main attention kernel with
+ * HIP events on `stream`; lmh_kv_kernel_time returns the accumulated milliseconds and launch
+ * count since the last reset (synchronizes on the recorded events). */
+int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
+int32_t lmh_kv_kernel_time(lmh_kv* kv, double* ms, uint64_t* launches);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LLMARIO_HIP_H */

@@ -1,0 +1,102 @@
+"""ctypes binding of ``libllmario_hip.so`` (the C ABI in ``include/llmario_hip.h``).
+
+Loading fails loudly when the library has not been built: there is no CPU fallback anywhere in
+this package.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libllmario_hip.so")
+
+OK, INVALID_ARGUMENT, KV_FULL, UNSUPPORTED, DEVICE_ERROR, OUT_OF_MEMORY = 0, 1, 2, 3, 4, 5
+STATUS_NAMES = {0: "OK", 1: "INVALID_ARGUMENT", 2: "KV_FULL", 3: "UNSUPPORTED", 4: "DEVICE_ERROR",
+                5: "OUT_OF_MEMORY"}
+KV_F16, KV_Q8_0, KV_F32, KV_BF16 = 0, 1, 2, 3
+KV_TYPES = {"f16": KV_F16, "q8_0": KV_Q8_0, "f32": KV_F32, "bf16": KV_BF16}
+ABI_VERSION = 1
+
+u32, u64, i32, P = C.c_uint32, C.c_uint64, C.c_int32, C.c_void_p
+
+
+class LayerDesc(C.Structure):
+    _fields_ = [("n_head", u32), ("n_kv", u32), ("hd", u32), ("hdv", u32)]
+
+
+class KvOptions(C.Structure):
+    _fields_ = [("abi_version", u32), ("kv_type", u32), ("block_tokens", u32), ("n_layers", u32),
+                ("layers", C.POINTER(LayerDesc)), ("max_ctx", u64), ("n_seqs", u64),
+                ("pool_tokens", u64), ("device", i32), ("reserved0", u32)]
+
+
+class LayoutInfo(C.Structure):
+    _fields_ = [("block_bytes", u64), ("blocks_per_seq", u64), ("n_seqs", u64), ("pool_blocks", u64),
+                ("max_ctx", u64), ("block_tokens", u32), ("kv_type", u32)]
+
+
+class SeqTokens(C.Structure):
+    _fields_ = [("seq", u64), ("n_tokens", u64)]
+
+
+class Seg(C.Structure):
+    _fields_ = [("seq", u64), ("start", u64), ("n", u64), ("pos0", u64)]
+
+
+# name -> (restype, argtypes); the exported C ABI, in header order.
+SIGNATURES = {
+    "lmh_kv_create": (i32, [C.POINTER(KvOptions), C.POINTER(P)]),
+    "lmh_kv_destroy": (None, [P]),
+    "lmh_kv_last_error": (C.c_char_p, [P]),
+    "lmh_create_error": (C.c_char_p, []),
+    "lmh_kv_layout": (i32, [P, C.POINTER(LayoutInfo)]),
+    "lmh_kv_fingerprint": (u64, [P]),
+    "lmh_kv_seq_len": (i32, [P, u64, C.POINTER(u64)]),
+    "lmh_kv_set_seq_len": (i32, [P, u64, u64]),
+    "lmh_kv_free_blocks": (i32, [P, C.POINTER(u64)]),
+    "lmh_kv_resident_blocks": (i32, [P, C.POINTER(u64)]),
+    "lmh_kv_blocks_needed": (i32, [P, u64, u64, C.POINTER(u64)]),
+    "lmh_kv_reserve": (i32, [P, u64, u64, C.POINTER(u64), C.POINTER(u64)]),
+    "lmh_kv_truncate": (i32, [P, u64, u64]),
+    "lmh_kv_clear": (i32, [P, u64]),
+    "lmh_kv_block_table": (i32, [P, u64, P, u64, C.POINTER(u64)]),
+    "lmh_kv_adopt_blocks": (i32, [P, u64, P, u64]),
+    "lmh_pool_refs": (i32, [P, u32, C.POINTER(u32)]),
+    "lmh_pool_set_hash": (i32, [P, u32, P]),
+    "lmh_pool_clear_hash": (i32, [P, u32]),
+    "lmh_pool_is_cached": (i32, [P, u32, C.POINTER(i32)]),
+    "lmh_batch_prepare": (i32, [P, P, u64, P, C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
+    "lmh_batch_commit": (i32, [P, P, u64]),
+    "lmh_kv_store": (i32, [P, u32, P, u64, P, P, P]),
+    "lmh_kv_store_encoded": (i32, [P, u32, P, u64, P, P, P]),
+    "lmh_kv_gather": (i32, [P, u32, P, u64, P, P, P]),
+    "lmh_kv_gather_encoded": (i32, [P, u32, P, u64, P, P, P]),
+    "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
+    "lmh_kv_set_timing": (i32, [P, i32]),
+    "lmh_kv_kernel_time": (i32, [P, C.POINTER(C.c_double), C.POINTER(u64)]),
+}
+
+_lib = None
+
+
+def lib():
+    """The loaded backend library; raises if it was not built (no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it first (python -m llmario_amd.build or "
+                "__graft_entry__.build()); the HIP backend has no CPU fallback")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols() -> list[str]:
+    return list(SIGNATURES)

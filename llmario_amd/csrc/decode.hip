@@ -1,0 +1,504 @@
+// decode.hip — paged-attention decode on gfx950 (CDNA4).
+//
+// Computes what `attend` / `attend_split` compute for decode-style rows
+// (crates/engine/model/src/forward.rs:585-807): for a row at position `pos` of sequence `seq`
+// and KV head `kvh`, every query head of the GQA group attends to keys p_lo..=pos through the
+// block table, softmax(scale * q.k) v with fp32 accumulation.
+//
+// Work decomposition (built on the host from the batch's segments): one wave64 per work item
+// (row, KV head, contiguous key range aligned to 16-token tiles). The key range of a long row is
+// cut into several items (split-K, as attend_split does for long contexts, forward.rs:688-807);
+// their partial (o, m, l) go to `part` and `merge_kernel` combines them with the exact
+// log-sum-exp merge of forward.rs:772-806.
+//
+// f16 / bf16 / q8_0 pages (matrix cores): per 16-token tile,
+//   S^T[16 keys x 16 heads] = K[16 x hd] . Q^T[hd x 16]     (v_mfma_f32_16x16x32_{f16,bf16})
+//   O^T[hdv x 16 heads]    += V^T[hdv x 16] . P^T[16 x 16]    (v_mfma_f32_16x16x16_f16)
+// The C layout of S^T (lane l: keys 4*(l/16)+r, head l%16) is exactly the B layout P^T needs,
+// and O^T's C layout keeps each head in the lanes that own its softmax state, so the online
+// softmax needs no data movement besides two cross-lane max/sum steps. The page bytes are
+// stored in operand order, so each operand is one 16-byte load per lane (1 KiB per wave).
+// Q is split into hi + lo halves of the MFMA input type, so scores keep ~22 bits of Q precision
+// (f16) or ~16 bits (bf16) against exactly represented K. P is rounded to f16 for P.V; bf16 V is
+// widened to f16 (exact for |v| in [2^-14, 65504]). q8_0: each 32-dim chunk of Q.K is one MFMA
+// whose result is scaled by that chunk's per-key scale; V scales fold into P per 32-dim block.
+//
+// f32 pages (VALU): lane per key for Q.K, lane per dim for P.V, fp32 throughout.
+#include "device.h"
+
+namespace lmh {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int WAVES = 4;  // waves (work items) per workgroup
+
+__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ inline float xmax_groups(float x) {  // max over lanes l, l^16, l^32, l^48
+  x = fmaxf(x, __shfl_xor(x, 16));
+  return fmaxf(x, __shfl_xor(x, 32));
+}
+__device__ inline float xsum_groups(float x) {
+  x += __shfl_xor(x, 16);
+  return x + __shfl_xor(x, 32);
+}
+
+__device__ inline uint16_t bf16_rne(float x) {
+  uint32_t u = __float_as_uint(x);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// int8 x4 (packed in a uint32) -> f16 x4, exact.
+__device__ inline h4 i8x4_to_h4(uint32_t w) {
+  h4 r;
+  r[0] = (_Float16)(float)(int8_t)(w & 0xff);
+  r[1] = (_Float16)(float)(int8_t)((w >> 8) & 0xff);
+  r[2] = (_Float16)(float)(int8_t)((w >> 16) & 0xff);
+  r[3] = (_Float16)(float)(int8_t)(w >> 24);
+  return r;
+}
+
+// bf16 x4 (two uint32) -> f16 x4 (exact for normal f16 range).
+__device__ inline h4 bf4_to_h4(uint32_t a, uint32_t b) {
+  h4 r;
+  r[0] = (_Float16)__uint_as_float(a << 16);
+  r[1] = (_Float16)__uint_as_float(a & 0xffff0000u);
+  r[2] = (_Float16)__uint_as_float(b << 16);
+  r[3] = (_Float16)__uint_as_float(b & 0xffff0000u);
+  return r;
+}
+
+__device__ inline float h_to_f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+
+template <int KVT, int HD, int HDV>
+struct TileRegs {
+  // f16/bf16: K one uint4 per 32 dims, V one uint4 per 32 dims.
+  // q8_0: K codes one uint4 per 64 dims, V codes one uint4 per 64 dims, plus the lane's scales.
+  static constexpr int NK = (KVT == KV_Q8) ? HD / 64 : HD / 32;
+  static constexpr int NV = (KVT == KV_Q8) ? HDV / 64 : HDV / 32;
+  static constexpr int NKS = (KVT == KV_Q8) ? (4 * (HD / 32) * 2 + 15) / 16 : 0;   // scale uint4s
+  static constexpr int NVS = (KVT == KV_Q8) ? (4 * (HDV / 32) * 2 + 15) / 16 : 0;
+  uint4 k[NK];
+  uint4 v[NV];
+  uint4 ks[NKS > 0 ? NKS : 1];
+  uint4 vs[NVS > 0 ? NVS : 1];
+};
+
+template <int KVT, int HD, int HDV>
+__device__ inline void load_tile(TileRegs<KVT, HD, HDV>& t, const uint8_t* kb, const uint8_t* vb,
+                                 const uint8_t* ksb, const uint8_t* vsb, uint32_t lane) {
+  using T = TileRegs<KVT, HD, HDV>;
+#pragma unroll
+  for (int c = 0; c < T::NK; c++) t.k[c] = *(const uint4*)(kb + c * 1024 + lane * 16);
+#pragma unroll
+  for (int c = 0; c < T::NV; c++) t.v[c] = *(const uint4*)(vb + c * 1024 + lane * 16);
+  if constexpr (KVT == KV_Q8) {
+    // scales [key m][chunk]: lane group g = lane/16 needs keys 4g..4g+3, all chunks (contiguous)
+    const uint32_t g = lane >> 4;
+#pragma unroll
+    for (int c = 0; c < T::NKS; c++) t.ks[c] = *(const uint4*)(ksb + g * (4 * (HD / 32) * 2) + c * 16);
+#pragma unroll
+    for (int c = 0; c < T::NVS; c++) t.vs[c] = *(const uint4*)(vsb + g * (4 * (HDV / 32) * 2) + c * 16);
+  }
+}
+
+// Scale (as f32) for key 4g+r, chunk c, from the lane's scale registers.
+template <int NCH>
+__device__ inline float scale_at(const uint4* s, int r, int c) {
+  const int idx = r * NCH + c;  // f16 index
+  const uint32_t w = ((const uint32_t*)s)[idx >> 1];
+  return h_to_f((uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
+}
+
+template <int KVT, int HD, int HDV>
+__global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
+                                                                 uint32_t n_items, const float* q, float* out,
+                                                                 float* part) {
+  constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
+  constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
+  using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  if (wi >= n_items) return;
+  const DecodeItem it = items[wi];
+  const int seq = r.row_seq[it.row];
+  const int32_t* tab = g.table + (size_t)seq * g.bps;
+  const uint32_t hq = lane & 15u, grp = lane >> 4;
+  const bool hv = hq < r.ng && it.h0 + hq < r.group;
+  const uint32_t head = it.kvh * r.group + it.h0 + hq;
+
+  // Q as the B operand of S^T = K Q^T: chunk c, lane (grp, hq) holds dims 32c + 8grp .. +8.
+  MT qh[NC], ql[NC];
+  {
+    const float* qp = q + ((size_t)it.row * r.n_head + (hv ? head : 0)) * HD;
+#pragma unroll
+    for (int c = 0; c < NC; c++) {
+      float4 a = hv ? *(const float4*)(qp + 32 * c + 8 * grp) : make_float4(0, 0, 0, 0);
+      float4 b = hv ? *(const float4*)(qp + 32 * c + 8 * grp + 4) : make_float4(0, 0, 0, 0);
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        if constexpr (KVT == KV_BF16) {
+          const uint16_t hb = bf16_rne(x[i]);
+          const float hf = __uint_as_float((uint32_t)hb << 16);
+          qh[c][i] = __builtin_bit_cast(__bf16, hb);
+          ql[c][i] = __builtin_bit_cast(__bf16, bf16_rne(x[i] - hf));
+        } else {
+          const _Float16 hh = (_Float16)x[i];
+          qh[c][i] = hh;
+          ql[c][i] = (_Float16)(x[i] - (float)hh);
+        }
+      }
+    }
+  }
+
+  float m = -INFINITY, lsum = 0.0f;
+  f4 O[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) O[j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t t0 = it.p0 >> 4, t1 = (it.p1 - 1) >> 4;
+  const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
+  auto ptrs = [&](uint32_t t, const uint8_t*& kb, const uint8_t*& vb, const uint8_t*& ksb, const uint8_t*& vsb) {
+    const uint32_t pos = t << 4;
+    const int blk = tab[pos >> g.bt_shift];
+    const uint32_t sub = (pos & bt_mask) >> 4;
+    const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
+    const uint8_t* kh = base + g.k_off + it.kvh * g.k_head;
+    const uint8_t* vh = base + g.v_off + it.kvh * g.v_head;
+    kb = kh + sub * g.k_tile;
+    vb = vh + sub * g.v_tile;
+    ksb = kh + g.k_scale + sub * g.k_tile_s;
+    vsb = vh + g.v_scale + sub * g.v_tile_s;
+  };
+
+  TileRegs<KVT, HD, HDV> cur, nxt;
+  {
+    const uint8_t *kb, *vb, *ksb, *vsb;
+    ptrs(t0, kb, vb, ksb, vsb);
+    load_tile(cur, kb, vb, ksb, vsb, lane);
+  }
+  for (uint32_t t = t0; t <= t1; t++) {
+    if (t < t1) {
+      const uint8_t *kb, *vb, *ksb, *vsb;
+      ptrs(t + 1, kb, vb, ksb, vsb);
+      load_tile(nxt, kb, vb, ksb, vsb, lane);
+    }
+    // ---- scores S^T for 16 keys x 16 heads
+    f4 s = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (KVT == KV_Q8) {
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const uint32_t* w = (const uint32_t*)&cur.k[c >> 1];
+        const int o = (c & 1) * 2;
+        const h4 lo4 = i8x4_to_h4(w[o]), hi4 = i8x4_to_h4(w[o + 1]);
+        const h8 kc = h8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+        f4 sc = f4{0.f, 0.f, 0.f, 0.f};
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qh[c], sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, ql[c], sc, 0, 0, 0);
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) s[rr] += sc[rr] * scale_at<NC>(cur.ks, rr, c);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        const MT kc = __builtin_bit_cast(MT, cur.k[c]);
+        if constexpr (KVT == KV_BF16) {
+          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, qh[c], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, ql[c], s, 0, 0, 0);
+        } else {
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qh[c], s, 0, 0, 0);
+          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, ql[c], s, 0, 0, 0);
+        }
+      }
+    }
+    // ---- online softmax (log2 domain), keys outside [p0, p1) masked
+    const uint32_t kbase = (t << 4) + 4u * grp;
+    float sc[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) {
+      const uint32_t key = kbase + rr;
+      sc[rr] = (key >= it.p0 && key < it.p1) ? s[rr] * r.scale_log2 : -INFINITY;
+    }
+    float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    tm = xmax_groups(tm);
+    const float mn = fmaxf(m, tm);
+    const float alpha = exp2_fast(m - mn);
+    float p[4];
+#pragma unroll
+    for (int rr = 0; rr < 4; rr++) p[rr] = exp2_fast(sc[rr] - mn);
+    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+    m = mn;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) O[j] *= alpha;
+    // ---- O^T += V^T P^T
+    if constexpr (KVT == KV_Q8) {
+#pragma unroll
+      for (int b = 0; b < HDV / 32; b++) {
+        h4 pb;
+#pragma unroll
+        for (int i = 0; i < 4; i++) pb[i] = (_Float16)(p[i] * scale_at<HDV / 32>(cur.vs, i, b));
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+          const int j = 2 * b + jj;
+          const uint32_t w = ((const uint32_t*)&cur.v[j >> 2])[j & 3];
+          O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(w), pb, O[j], 0, 0, 0);
+        }
+      }
+    } else {
+      const h4 pb = h4{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const uint32_t* w = (const uint32_t*)&cur.v[j >> 1];
+        const int o = (j & 1) * 2;
+        h4 va;
+        if constexpr (KVT == KV_BF16) {
+          va = bf4_to_h4(w[o], w[o + 1]);
+        } else {
+          va = __builtin_bit_cast(h4, make_uint2(w[o], w[o + 1]));
+        }
+        O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, O[j], 0, 0, 0);
+      }
+    }
+    cur = nxt;
+  }
+  lsum = xsum_groups(lsum);
+
+  if (!hv) return;
+  if (it.slot == NO_SLOT) {
+    const float inv = 1.0f / lsum;
+    float* op = out + ((size_t)it.row * r.n_head + head) * HDV;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const f4 o = O[j] * inv;
+      *(float4*)(op + 16 * j + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
+    }
+  } else {
+    float* pp = part + ((size_t)it.slot * r.ng + hq) * (HDV + 4);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][0], O[j][1], O[j][2], O[j][3]);
+    if (grp == 0) {
+      pp[HDV] = m;
+      pp[HDV + 1] = lsum;
+    }
+  }
+}
+
+// ---- f32 pages: VALU path ----------------------------------------------------------------------
+template <int HD, int HDV>
+__global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
+                                                                uint32_t n_items, const float* q, float* out,
+                                                                float* part) {
+  constexpr int NG = 16;
+  constexpr int ND = HDV / 64 > 0 ? HDV / 64 : 1;  // dims per lane in P.V
+  __shared__ float qs[WAVES][NG][HD];
+  __shared__ float ps[WAVES][NG][64];
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t wi = blockIdx.x * WAVES + w;
+  const bool active = wi < n_items;
+  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT};
+  const uint32_t ng = r.ng;
+  const uint32_t nh = (it.h0 + ng <= r.group) ? ng : r.group - it.h0;
+  if (active) {
+    for (uint32_t e = lane; e < nh * HD; e += 64) {
+      const uint32_t h = e / HD, d = e % HD;
+      qs[w][h][d] = q[((size_t)it.row * r.n_head + it.kvh * r.group + it.h0 + h) * HD + d];
+    }
+  }
+  __syncthreads();
+  if (!active) return;
+  const int seq = r.row_seq[it.row];
+  const int32_t* tab = g.table + (size_t)seq * g.bps;
+  const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
+  float m[NG], l[NG], o[NG][ND];
+#pragma unroll
+  for (int h = 0; h < NG; h++) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < ND; i++) o[h][i] = 0.f;
+  }
+  for (uint32_t c0 = it.p0; c0 < it.p1; c0 += 64) {
+    const uint32_t key = c0 + lane;
+    const bool valid = key < it.p1;
+    const uint32_t kk = valid ? key : it.p0;
+    const int blk = tab[kk >> g.bt_shift];
+    const uint32_t in_blk = kk & bt_mask;
+    const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
+    const float* krow = (const float*)(base + g.k_off + it.kvh * g.k_head + (in_blk >> 4) * g.k_tile) + (in_blk & 15u) * HD;
+    float s[NG];
+#pragma unroll
+    for (int h = 0; h < NG; h++) s[h] = 0.f;
+    for (int d = 0; d < HD; d += 4) {
+      const float4 kv = *(const float4*)(krow + d);
+#pragma unroll
+      for (int h = 0; h < NG; h++) {
+        if (h < (int)nh) {
+          s[h] = fmaf(qs[w][h][d], kv.x, s[h]);
+          s[h] = fmaf(qs[w][h][d + 1], kv.y, s[h]);
+          s[h] = fmaf(qs[w][h][d + 2], kv.z, s[h]);
+          s[h] = fmaf(qs[w][h][d + 3], kv.w, s[h]);
+        }
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < NG; h++) {
+      if (h < (int)nh) {
+        const float sc = valid ? s[h] * r.scale_log2 : -INFINITY;
+        float cm = sc;
+        for (int x = 32; x >= 1; x >>= 1) cm = fmaxf(cm, __shfl_xor(cm, x));
+        const float mn = fmaxf(m[h], cm);
+        const float alpha = exp2_fast(m[h] - mn);
+        const float p = exp2_fast(sc - mn);
+        float ssum = p;
+        for (int x = 32; x >= 1; x >>= 1) ssum += __shfl_xor(ssum, x);
+        l[h] = l[h] * alpha + ssum;
+        m[h] = mn;
+#pragma unroll
+        for (int i = 0; i < ND; i++) o[h][i] *= alpha;
+        ps[w][h][lane] = p;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t nk = (it.p1 - c0) < 64u ? (it.p1 - c0) : 64u;
+    for (uint32_t kq = 0; kq < nk; kq++) {
+      const uint32_t kp = c0 + kq;
+      const int b2 = tab[kp >> g.bt_shift];
+      const uint32_t ib = kp & bt_mask;
+      const float* vrow = (const float*)(g.pool + (size_t)b2 * g.block_bytes + g.v_off + it.kvh * g.v_head +
+                                         (ib >> 4) * g.v_tile) + (ib & 15u) * HDV;
+      float vv[ND];
+#pragma unroll
+      for (int i = 0; i < ND; i++) vv[i] = (lane + 64 * i < (uint32_t)HDV) ? vrow[lane + 64 * i] : 0.f;
+#pragma unroll
+      for (int h = 0; h < NG; h++) {
+        if (h < (int)nh) {
+          const float pw = ps[w][h][kq];
+#pragma unroll
+          for (int i = 0; i < ND; i++) o[h][i] = fmaf(pw, vv[i], o[h][i]);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+#pragma unroll
+  for (int h = 0; h < NG; h++) {
+    if (h < (int)nh) {
+      if (it.slot == NO_SLOT) {
+        float* op = out + ((size_t)it.row * r.n_head + it.kvh * r.group + it.h0 + h) * HDV;
+        const float inv = 1.0f / l[h];
+#pragma unroll
+        for (int i = 0; i < ND; i++)
+          if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = o[h][i] * inv;
+      } else {
+        float* pp = part + ((size_t)it.slot * r.ng + h) * (HDV + 4);
+#pragma unroll
+        for (int i = 0; i < ND; i++)
+          if (lane + 64 * i < (uint32_t)HDV) pp[lane + 64 * i] = o[h][i];
+        if (lane == 0) {
+          pp[HDV] = m[h];
+          pp[HDV + 1] = l[h];
+        }
+      }
+    }
+  }
+}
+
+// ---- split-K merge (forward.rs:772-806): m* = max m_s, out = sum e^(m_s-m*) o_s / sum e^(m_s-m*) l_s
+template <int HDV>
+__global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* items, uint32_t n_items,
+                                                    const float* part, float* out) {
+  constexpr int ND = (HDV + 63) / 64;
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wi >= n_items * r.ng) return;
+  const MergeItem mi = items[wi / r.ng];
+  const uint32_t hq = wi % r.ng;
+  if (mi.h0 + hq >= r.group) return;
+  float M = -INFINITY;
+  for (uint32_t s = 0; s < mi.n_split; s++) M = fmaxf(M, part[((size_t)(mi.slot0 + s) * r.ng + hq) * (HDV + 4) + HDV]);
+  float L = 0.f, acc[ND];
+#pragma unroll
+  for (int i = 0; i < ND; i++) acc[i] = 0.f;
+  for (uint32_t s = 0; s < mi.n_split; s++) {
+    const float* pp = part + ((size_t)(mi.slot0 + s) * r.ng + hq) * (HDV + 4);
+    const float ms = pp[HDV];
+    if (ms == -INFINITY) continue;
+    const float c = exp2_fast(ms - M);
+    L += c * pp[HDV + 1];
+#pragma unroll
+    for (int i = 0; i < ND; i++)
+      if (lane + 64 * i < (uint32_t)HDV) acc[i] += c * pp[lane + 64 * i];
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + hq) * HDV;
+#pragma unroll
+  for (int i = 0; i < ND; i++)
+    if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = acc[i] * inv;
+}
+
+template <int KVT, int HD, int HDV>
+hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
+                      const float* q, float* out, float* part, hipStream_t s) {
+  const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
+  if constexpr (KVT == KV_F32) {
+    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
+  } else {
+    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
+  }
+  return hipGetLastError();
+}
+
+template <int KVT>
+hipError_t dispatch_hd(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
+                       const float* q, float* out, float* part, hipStream_t s) {
+  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, s);
+  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, s);
+  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
+  if (hd != hdv) return false;
+  if (hd != 64 && hd != 128 && hd != 256) return false;
+  return kv_type <= KV_BF16;
+}
+
+hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
+                         const float* q, float* out, float* part, hipStream_t s) {
+  if (n_items == 0) return hipSuccess;
+  switch (g.kv_type) {
+    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, s);
+    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, s);
+    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, s);
+    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, s);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
+                        float* out, hipStream_t s) {
+  if (n_items == 0) return hipSuccess;
+  const uint32_t waves = n_items * r.ng;
+  const dim3 grid((waves + 3) / 4), block(256);
+  switch (hdv) {
+    case 64: hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 128: hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 256: hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, s, r, items, n_items, part, out); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lmh

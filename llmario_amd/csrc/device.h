@@ -1,0 +1,114 @@
+// device.h — structures shared by the host side (host.cpp) and the HIP kernels.
+//
+// Page layout (one layer's share of one block; the block holds every layer, K then V, like the
+// reference's block, crates/engine/model/src/kv.rs:286-324):
+//
+//   [K: head 0 .. n_kv-1][V: head 0 .. n_kv-1]
+//
+// Each (layer, KV head) region covers the block's `block_tokens` positions as 16-token tiles.
+// Inside a tile, elements sit in the order the matrix-core operands of the decode/prefill kernels
+// read them, so a wave's 16-byte-per-lane load covers 1 KiB of contiguous HBM:
+//
+//   f16/bf16 K (MFMA 16x16x32 A operand, lane l = 16*g + m holds key m, dims 32c+8g .. +8):
+//       byte(m, d) = (d/32)*1024 + (16*((d/8)%4) + m)*16 + (d%8)*2
+//   f16/bf16 V (MFMA 16x16x16 A operand of O^T = V^T P^T, lane l = 16*(k/4) + d%16 holds
+//       keys 4*(k/4) .. +4 of dim d):
+//       byte(k, d) = (d/32)*1024 + (16*(k/4) + d%16)*16 + ((d/16)%2)*8 + (k%4)*2
+//   q8_0 K codes: byte(m, d) = (d/64)*1024 + (16*((d/8)%4) + m)*16 + ((d/32)%2)*8 + d%8
+//   q8_0 V codes: byte(k, d) = (d/64)*1024 + (16*(k/4) + d%16)*16 + ((d/16)%4)*4 + k%4
+//   q8_0 scales (K and V alike), f16, after all code tiles of the head: [tile][key m][d/32]
+//   f32 K/V: plain row-major [key m][d] (the VALU decode path reads rows).
+//
+// The total bytes per block equal the reference's `block_bytes` for the same geometry and type
+// (q8_0: 34 bytes per 32 values; f16/bf16: 2 bytes; f32: 4 bytes per value).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace lmh {
+
+enum : uint32_t { KV_F16 = 0, KV_Q8 = 1, KV_F32 = 2, KV_BF16 = 3 };
+
+// Where one layer's pages live. Tile t (16 positions) of KV head h in block b:
+//   K values at pool + b*block_bytes + k_off + h*k_head + t*k_tile
+//   K scales at pool + b*block_bytes + k_off + h*k_head + k_scale + t*k_tile_s  (q8_0 only)
+struct PageGeom {
+  uint8_t* pool;
+  uint64_t block_bytes;
+  uint32_t k_off, v_off;
+  uint32_t k_head, v_head;
+  uint32_t k_tile, v_tile;
+  uint32_t k_scale, v_scale;
+  uint32_t k_tile_s, v_tile_s;
+  uint32_t bt_shift;  // log2(block_tokens)
+  uint32_t bps;       // blocks per sequence (table row length)
+  const int32_t* table;  // [n_seqs][bps] block ids
+  uint32_t kv_type, n_kv, hd, hdv;
+};
+
+__host__ __device__ inline uint32_t k16_off(uint32_t m, uint32_t d) {
+  return (d >> 5) * 1024u + ((((d >> 3) & 3u) << 4) + m) * 16u + (d & 7u) * 2u;
+}
+__host__ __device__ inline uint32_t v16_off(uint32_t k, uint32_t d) {
+  return (d >> 5) * 1024u + (((k >> 2) << 4) + (d & 15u)) * 16u + ((d >> 4) & 1u) * 8u + (k & 3u) * 2u;
+}
+__host__ __device__ inline uint32_t kq8_off(uint32_t m, uint32_t d) {
+  return (d >> 6) * 1024u + ((((d >> 3) & 3u) << 4) + m) * 16u + ((d >> 5) & 1u) * 8u + (d & 7u);
+}
+__host__ __device__ inline uint32_t vq8_off(uint32_t k, uint32_t d) {
+  return (d >> 6) * 1024u + (((k >> 2) << 4) + (d & 15u)) * 16u + ((d >> 4) & 3u) * 4u + (k & 3u);
+}
+
+// One decode work item: row `row` (its sequence and position come from the row arrays), KV head
+// `kvh`, query heads kvh*group + h0 .. + n_heads, keys [p0, p1). `slot` is the partial-result slot
+// (split-K) or NO_SLOT when the item covers the row's whole key range and writes the output.
+struct DecodeItem {
+  uint32_t row;
+  uint32_t kvh;
+  uint32_t h0;
+  uint32_t p0, p1;
+  uint32_t slot;
+};
+constexpr uint32_t NO_SLOT = 0xffffffffu;
+
+// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..).
+struct MergeItem {
+  uint32_t row;
+  uint32_t kvh;
+  uint32_t h0;
+  uint32_t slot0;
+  uint32_t n_split;
+  uint32_t pad;
+};
+
+struct RowGeom {
+  const int32_t* row_seq;  // [n_rows]
+  const int32_t* row_pos;  // [n_rows]
+  uint32_t n_head, group;  // group = n_head / n_kv
+  uint32_t ng;             // heads per item = min(group, 16)
+  float scale_log2;        // scale * log2(e): scores kept in the log2 domain
+  uint32_t window;         // 0 = none
+};
+
+// Launch wrappers (defined in the .hip files). Return hipSuccess or the launch error.
+hipError_t launch_store_f32(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
+                            const float* k, const float* v, hipStream_t s);
+hipError_t launch_store_encoded(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos,
+                                uint32_t n_rows, const uint8_t* k, const uint8_t* v, uint32_t k_row,
+                                uint32_t v_row, hipStream_t s);
+hipError_t launch_gather(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
+                         float* k, float* v, hipStream_t s);
+hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos,
+                                 uint32_t n_rows, uint8_t* k, uint8_t* v, uint32_t k_row, uint32_t v_row,
+                                 hipStream_t s);
+hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
+                              hipStream_t s);
+// Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.
+hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
+                         const float* q, float* out, float* part, hipStream_t s);
+hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
+                        float* out, hipStream_t s);
+bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
+
+}  // namespace lmh

@@ -1,0 +1,960 @@
+// host.cpp — the C ABI (include/llmario_hip.h): device page pool, block bookkeeping and the
+// attention hand-off for MI355X.
+//
+// Host-side semantics follow the reference engine exactly where block ids and lengths are
+// concerned (they must match bit for bit):
+//   BlockPool            crates/engine/kv/src/lib.rs:36-176   (FIFO/LRU free queue, refcounts,
+//                                                              content hashes)
+//   KvLayout sizes       crates/engine/model/src/kv.rs:402-497 (block_bytes, pool_blocks, ...)
+//   KvCache reserve/COW  kv.rs:715-827
+//   forward_batch checks crates/engine/model/src/forward.rs:207-291
+// The device side is this backend's own: one hipMalloc'd pool of pool_blocks x block_bytes,
+// an int32 block table [n_seqs][blocks_per_seq] mirrored to the device when it changes, and a
+// per-call packed work list (decode items, split-K slots, merges) uploaded from pinned memory.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <array>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <deque>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/llmario_hip.h"
+#include "device.h"
+
+using namespace lmh;
+
+namespace {
+
+thread_local std::string g_create_error;
+
+struct LayerLayout {
+  uint32_t n_head, n_kv, hd, hdv;
+  uint64_t k_row, v_row;  // the reference's row bytes (encoded I/O)
+  uint32_t k_off, v_off, k_head, v_head, k_tile, v_tile, k_scale, v_scale, k_tile_s, v_tile_s;
+};
+
+uint64_t ref_row_bytes(uint32_t t, uint64_t n) {  // kv.rs:94-99 (+ F32/BF16)
+  switch (t) {
+    case LMH_KV_F16: return 2 * n;
+    case LMH_KV_Q8_0: return (n + 31) / 32 * 34;
+    case LMH_KV_F32: return 4 * n;
+    case LMH_KV_BF16: return 2 * n;
+  }
+  return 0;
+}
+
+// Bytes of one 16-token tile of values (codes for q8_0) for `dim` dims, and of its q8_0 scales.
+uint32_t tile_bytes(uint32_t t, uint32_t dim) {
+  switch (t) {
+    case LMH_KV_F16:
+    case LMH_KV_BF16: return 16 * dim * 2;
+    case LMH_KV_Q8_0: return 16 * dim;
+    default: return 16 * dim * 4;
+  }
+}
+uint32_t tile_scale_bytes(uint32_t t, uint32_t dim) { return t == LMH_KV_Q8_0 ? 16 * (dim / 32) * 2 : 0; }
+
+struct Uploader {  // pinned staging ring -> device, stream ordered
+  static constexpr int N = 4;
+  uint8_t* host[N] = {};
+  size_t cap[N] = {};
+  hipEvent_t ev[N] = {};
+  bool used[N] = {};
+  int next = 0;
+  ~Uploader() {
+    for (int i = 0; i < N; i++) {
+      if (ev[i]) {
+        if (used[i]) (void)hipEventSynchronize(ev[i]);
+        (void)hipEventDestroy(ev[i]);
+      }
+      if (host[i]) (void)hipHostFree(host[i]);
+    }
+  }
+  // A host buffer of at least `bytes` whose previous copy has finished.
+  hipError_t acquire(size_t bytes, int& idx, uint8_t*& ptr) {
+    idx = next;
+    next = (next + 1) % N;
+    hipError_t e;
+    if (!ev[idx]) {
+      if ((e = hipEventCreateWithFlags(&ev[idx], hipEventDisableTiming)) != hipSuccess) return e;
+    }
+    if (used[idx]) {
+      if ((e = hipEventSynchronize(ev[idx])) != hipSuccess) return e;
+      used[idx] = false;
+    }
+    if (cap[idx] < bytes) {
+      if (host[idx]) (void)hipHostFree(host[idx]);
+      host[idx] = nullptr;
+      size_t c = std::max<size_t>(bytes, 1 << 16);
+      if ((e = hipHostMalloc((void**)&host[idx], c, hipHostMallocDefault)) != hipSuccess) {
+        cap[idx] = 0;
+        return e;
+      }
+      cap[idx] = c;
+    }
+    ptr = host[idx];
+    return hipSuccess;
+  }
+  hipError_t send(int idx, void* dst, size_t bytes, hipStream_t s) {
+    hipError_t e = hipMemcpyAsync(dst, host[idx], bytes, hipMemcpyHostToDevice, s);
+    if (e != hipSuccess) return e;
+    e = hipEventRecord(ev[idx], s);
+    used[idx] = e == hipSuccess;
+    return e;
+  }
+};
+
+struct DevBuf {  // grow-only device scratch
+  void* p = nullptr;
+  size_t cap = 0;
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  hipError_t ensure(size_t bytes) {
+    if (cap >= bytes) return hipSuccess;
+    if (p) {
+      (void)hipDeviceSynchronize();  // in-flight work of earlier calls may still read it
+      (void)hipFree(p);
+      p = nullptr;
+      cap = 0;
+    }
+    size_t c = std::max<size_t>(bytes + bytes / 4, 1 << 16);
+    hipError_t e = hipMalloc(&p, c);
+    if (e == hipSuccess) cap = c;
+    return e;
+  }
+};
+
+using Hash = std::array<uint8_t, 32>;
+
+struct BlockMeta {
+  uint32_t refs = 0;
+  bool has_hash = false;
+  Hash hash{};
+};
+
+struct Seq {
+  std::vector<uint32_t> blocks;
+  uint64_t len = 0;
+};
+
+// Pending device-side page operations queued by host bookkeeping (reserve), run in order at the
+// start of the next device call, on that call's stream: zero a freshly backed block (src < 0)
+// or copy a shared block for copy-on-write.
+struct PageOp {
+  int32_t src, dst;
+};
+
+}  // namespace
+
+struct lmh_kv {
+  // ---- layout
+  uint32_t kv_type = 0, bt = 16, bt_shift = 4;
+  uint64_t max_ctx = 0, n_seqs = 0, bps = 0, pool_blocks = 0, block_bytes = 0;
+  std::vector<LayerLayout> layers;
+  // ---- BlockPool (kv/src/lib.rs:36-176)
+  std::vector<BlockMeta> meta;
+  std::deque<uint32_t> free_q;
+  std::map<Hash, uint32_t> by_hash;
+  uint64_t hits = 0, misses = 0, evictions = 0;
+  std::vector<uint8_t> backed;
+  // ---- sequences
+  std::vector<Seq> seqs;
+  // ---- device
+  int device = 0;
+  uint8_t* d_pool = nullptr;
+  int32_t* d_table = nullptr;
+  std::vector<int32_t> h_table;
+  bool table_dirty = true;
+  std::vector<PageOp> pending;
+  Uploader up;
+  DevBuf meta_buf, part_buf, ops_buf;
+  // ---- per-call host scratch
+  std::vector<int32_t> row_seq, row_pos;
+  std::vector<DecodeItem> items;
+  std::vector<MergeItem> merges;
+  // ---- timing
+  bool timing = false;
+  std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
+  size_t ev_used = 0;
+  double acc_ms = 0;
+  uint64_t launches = 0;
+  std::string err;
+
+  ~lmh_kv() {
+    if (d_pool || d_table) (void)hipDeviceSynchronize();
+    if (d_pool) (void)hipFree(d_pool);
+    if (d_table) (void)hipFree(d_table);
+    for (auto& p : evs) {
+      (void)hipEventDestroy(p.first);
+      (void)hipEventDestroy(p.second);
+    }
+  }
+
+  int32_t fail(int32_t code, const std::string& m) {
+    err = m;
+    return code;
+  }
+  int32_t hip_fail(hipError_t e, const char* what) {
+    err = std::string(what) + ": " + hipGetErrorString(e);
+    return e == hipErrorOutOfMemory ? LMH_OUT_OF_MEMORY : LMH_DEVICE_ERROR;
+  }
+
+  // ---- BlockPool operations --------------------------------------------------------------
+  bool pool_alloc(uint64_t n, std::vector<uint32_t>& out) {  // lib.rs:93-109
+    if (free_q.size() < n) return false;
+    for (uint64_t i = 0; i < n; i++) {
+      const uint32_t b = free_q.front();
+      free_q.pop_front();
+      BlockMeta& m = meta[b];
+      if (m.has_hash) {
+        by_hash.erase(m.hash);
+        m.has_hash = false;
+        evictions++;
+      }
+      m.refs = 1;
+      out.push_back(b);
+    }
+    return true;
+  }
+  void pool_release(uint32_t b) {  // lib.rs:121-128
+    BlockMeta& m = meta[b];
+    if (m.refs == 0) return;
+    if (--m.refs == 0) free_q.push_back(b);
+  }
+  void pool_clear_hash(uint32_t b) {  // lib.rs:161-167
+    BlockMeta& m = meta[b];
+    if (!m.has_hash) return;
+    auto it = by_hash.find(m.hash);
+    if (it != by_hash.end() && it->second == b) by_hash.erase(it);
+    m.has_hash = false;
+  }
+  // ---- backing (kv.rs:690-712): a block is resident while referenced or cached
+  void back(uint32_t b, bool zero) {
+    if (!backed[b]) {
+      backed[b] = 1;
+      if (zero) pending.push_back({-1, (int32_t)b});
+    }
+  }
+  void maybe_unback(uint32_t b) {
+    if (meta[b].refs == 0 && !meta[b].has_hash) backed[b] = 0;
+  }
+  void release_block(uint32_t b) {
+    pool_release(b);
+    maybe_unback(b);
+  }
+  void set_table(uint64_t s) {
+    int32_t* row = h_table.data() + s * bps;
+    const auto& bl = seqs[s].blocks;
+    for (uint64_t i = 0; i < bps; i++) row[i] = i < bl.size() ? (int32_t)bl[i] : -1;
+    table_dirty = true;
+  }
+
+  // kv.rs:715-725
+  uint64_t blocks_needed(uint64_t s, uint64_t new_len) const {
+    const Seq& q = seqs[s];
+    const uint64_t want = (new_len + bt - 1) / bt;
+    const uint64_t missing = want > q.blocks.size() ? want - q.blocks.size() : 0;
+    const bool cow = q.len % bt != 0 && q.len < new_len && meta[q.blocks[q.len / bt]].refs > 1;
+    return missing + (cow ? 1 : 0);
+  }
+
+  // kv.rs:730-785
+  int32_t reserve(uint64_t s, uint64_t new_len, uint64_t* needed, uint64_t* free_blocks) {
+    if (new_len > max_ctx) return fail(LMH_INVALID_ARGUMENT, "context overflow");
+    const uint64_t len = seqs[s].len;
+    const uint64_t want = (new_len + bt - 1) / bt;
+    const uint64_t missing = want > seqs[s].blocks.size() ? want - seqs[s].blocks.size() : 0;
+    const uint64_t wanted = blocks_needed(s, new_len);
+    const bool cow = wanted > missing;
+    if (free_q.size() < wanted) {
+      if (needed) *needed = wanted;
+      if (free_blocks) *free_blocks = free_q.size();
+      return fail(LMH_KV_FULL, "KV cache full: " + std::to_string(wanted) + " more blocks needed, " +
+                                   std::to_string(free_q.size()) + " free");
+    }
+    if (len % bt != 0 && len < new_len) {
+      const uint64_t bi = len / bt;
+      const uint32_t old = seqs[s].blocks[bi];
+      if (cow) {
+        std::vector<uint32_t> nb;
+        pool_alloc(1, nb);
+        back(nb[0], false);  // fully overwritten by the copy below
+        pending.push_back({(int32_t)old, (int32_t)nb[0]});
+        seqs[s].blocks[bi] = nb[0];
+        release_block(old);
+      } else {
+        pool_clear_hash(old);
+      }
+    }
+    if (missing > 0) {
+      std::vector<uint32_t> fresh;
+      pool_alloc(missing, fresh);
+      for (uint32_t b : fresh) {
+        back(b, true);
+        seqs[s].blocks.push_back(b);
+      }
+    }
+    set_table(s);
+    return LMH_OK;
+  }
+
+  // kv.rs:792-816 (paged layers: no rings, no recurrent state)
+  void truncate(uint64_t s, uint64_t n) {
+    n = std::min(n, seqs[s].len);
+    seqs[s].len = n;
+    const uint64_t keep = (n + bt - 1) / bt;
+    while (seqs[s].blocks.size() > keep) {
+      const uint32_t b = seqs[s].blocks.back();
+      seqs[s].blocks.pop_back();
+      release_block(b);
+    }
+    set_table(s);
+  }
+  void clear(uint64_t s) {  // kv.rs:820-827
+    seqs[s].len = 0;
+    while (!seqs[s].blocks.empty()) {
+      const uint32_t b = seqs[s].blocks.back();
+      seqs[s].blocks.pop_back();
+      release_block(b);
+    }
+    set_table(s);
+  }
+
+  // ---- device helpers --------------------------------------------------------------------
+  int32_t flush(hipStream_t st) {
+    hipError_t e;
+    if (hipSetDevice(device) != hipSuccess) return fail(LMH_DEVICE_ERROR, "hipSetDevice failed");
+    size_t i = 0;
+    while (i < pending.size()) {
+      if (pending[i].src < 0) {
+        size_t j = i;
+        std::vector<int32_t> zb;
+        while (j < pending.size() && pending[j].src < 0) zb.push_back(pending[j++].dst);
+        int idx;
+        uint8_t* h;
+        if ((e = up.acquire(zb.size() * 4, idx, h)) != hipSuccess) return hip_fail(e, "staging");
+        std::memcpy(h, zb.data(), zb.size() * 4);
+        if ((e = ops_buf.ensure(zb.size() * 4)) != hipSuccess) return hip_fail(e, "hipMalloc");
+        if ((e = up.send(idx, ops_buf.p, zb.size() * 4, st)) != hipSuccess) return hip_fail(e, "upload");
+        if ((e = launch_zero_blocks(d_pool, block_bytes, (const int32_t*)ops_buf.p, (uint32_t)zb.size(), st)) !=
+            hipSuccess)
+          return hip_fail(e, "zero kernel");
+        i = j;
+      } else {
+        e = hipMemcpyAsync(d_pool + (size_t)pending[i].dst * block_bytes,
+                           d_pool + (size_t)pending[i].src * block_bytes, block_bytes, hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return hip_fail(e, "copy-on-write");
+        i++;
+      }
+    }
+    pending.clear();
+    if (table_dirty) {
+      int idx;
+      uint8_t* h;
+      const size_t bytes = h_table.size() * 4;
+      if ((e = up.acquire(bytes, idx, h)) != hipSuccess) return hip_fail(e, "staging");
+      std::memcpy(h, h_table.data(), bytes);
+      if ((e = up.send(idx, d_table, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
+      table_dirty = false;
+    }
+    return LMH_OK;
+  }
+
+  PageGeom geom(uint32_t l) const {
+    const LayerLayout& y = layers[l];
+    PageGeom g{};
+    g.pool = d_pool;
+    g.block_bytes = block_bytes;
+    g.k_off = y.k_off;
+    g.v_off = y.v_off;
+    g.k_head = y.k_head;
+    g.v_head = y.v_head;
+    g.k_tile = y.k_tile;
+    g.v_tile = y.v_tile;
+    g.k_scale = y.k_scale;
+    g.v_scale = y.v_scale;
+    g.k_tile_s = y.k_tile_s;
+    g.v_tile_s = y.v_tile_s;
+    g.bt_shift = bt_shift;
+    g.bps = (uint32_t)bps;
+    g.table = d_table;
+    g.kv_type = kv_type;
+    g.n_kv = y.n_kv;
+    g.hd = y.hd;
+    g.hdv = y.hdv;
+    return g;
+  }
+
+  // Validate segments against the tables; fill row_seq/row_pos. Rows must be stacked in segment
+  // order (start = running row count), as Rows::push builds them (forward.rs:63-77).
+  int32_t rows_from(const lmh_seg* segs, uint64_t n_segs, uint64_t& n_rows) {
+    row_seq.clear();
+    row_pos.clear();
+    n_rows = 0;
+    if (n_segs > 0 && !segs) return fail(LMH_INVALID_ARGUMENT, "null segments");
+    for (uint64_t i = 0; i < n_segs; i++) {
+      const lmh_seg& sg = segs[i];
+      if (sg.seq >= n_seqs) return fail(LMH_INVALID_ARGUMENT, "segment sequence out of range");
+      if (sg.start != n_rows) return fail(LMH_INVALID_ARGUMENT, "segments must stack rows in order");
+      if (sg.pos0 + sg.n > seqs[sg.seq].blocks.size() * bt)
+        return fail(LMH_INVALID_ARGUMENT, "segment positions beyond the sequence's reserved blocks");
+      if (sg.pos0 + sg.n > 0x7fffffffull) return fail(LMH_INVALID_ARGUMENT, "position too large");
+      for (uint64_t j = 0; j < sg.n; j++) {
+        row_seq.push_back((int32_t)sg.seq);
+        row_pos.push_back((int32_t)(sg.pos0 + j));
+      }
+      n_rows += sg.n;
+    }
+    if (n_rows > 0x7fffffffull) return fail(LMH_INVALID_ARGUMENT, "too many rows");
+    return LMH_OK;
+  }
+
+  // Upload row arrays (+ optional extra payload) in one copy; returns device pointers.
+  int32_t upload_rows(hipStream_t st, const void* extra, size_t extra_bytes, const int32_t*& d_rs,
+                      const int32_t*& d_rp, const uint8_t*& d_extra) {
+    const size_t nr = row_seq.size();
+    const size_t rows_bytes = (nr * 8 + 255) / 256 * 256;
+    const size_t total = rows_bytes + extra_bytes;
+    hipError_t e;
+    if ((e = meta_buf.ensure(total)) != hipSuccess) return hip_fail(e, "hipMalloc");
+    int idx;
+    uint8_t* h;
+    if ((e = up.acquire(total, idx, h)) != hipSuccess) return hip_fail(e, "staging");
+    std::memcpy(h, row_seq.data(), nr * 4);
+    std::memcpy(h + nr * 4, row_pos.data(), nr * 4);
+    if (extra_bytes) std::memcpy(h + rows_bytes, extra, extra_bytes);
+    if ((e = up.send(idx, meta_buf.p, total, st)) != hipSuccess) return hip_fail(e, "upload");
+    d_rs = (const int32_t*)meta_buf.p;
+    d_rp = d_rs + nr;
+    d_extra = (const uint8_t*)meta_buf.p + rows_bytes;
+    return LMH_OK;
+  }
+
+  hipError_t time_begin(hipStream_t st) {
+    if (!timing) return hipSuccess;
+    if (ev_used == evs.size()) {
+      hipEvent_t a, b;
+      (void)hipEventCreate(&a);
+      (void)hipEventCreate(&b);
+      evs.push_back({a, b});
+    }
+    return hipEventRecord(evs[ev_used].first, st);
+  }
+  hipError_t time_end(hipStream_t st) {
+    if (!timing) return hipSuccess;
+    hipError_t e = hipEventRecord(evs[ev_used].second, st);
+    ev_used++;
+    return e;
+  }
+};
+
+namespace {
+
+uint64_t env_u64(const char* name, uint64_t dflt) {
+  const char* v = std::getenv(name);
+  if (!v || !*v) return dflt;
+  return std::strtoull(v, nullptr, 10);
+}
+
+// FNV-1a (kv.rs:944-960 StableHasher)
+struct Fnv {
+  uint64_t h = 0xcbf29ce484222325ull;
+  void bytes(const void* p, size_t n) {
+    const uint8_t* b = (const uint8_t*)p;
+    for (size_t i = 0; i < n; i++) h = (h ^ b[i]) * 0x00000100000001b3ull;
+  }
+  void u64(uint64_t v) { bytes(&v, 8); }
+};
+
+}  // namespace
+
+// =============================================================================================
+// C ABI
+// =============================================================================================
+
+extern "C" {
+
+const char* lmh_create_error(void) { return g_create_error.c_str(); }
+
+int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
+  g_create_error.clear();
+  if (!o || !out) {
+    g_create_error = "null argument";
+    return LMH_INVALID_ARGUMENT;
+  }
+  *out = nullptr;
+  if (o->abi_version != LMH_ABI_VERSION) {
+    g_create_error = "ABI version mismatch";
+    return LMH_INVALID_ARGUMENT;
+  }
+  if (o->kv_type > LMH_KV_BF16) {
+    g_create_error = "unknown KV type";
+    return LMH_INVALID_ARGUMENT;
+  }
+  const uint32_t bt = o->block_tokens;
+  if (bt == 0 || (bt & (bt - 1)) != 0) {  // kv.rs:403-406
+    g_create_error = "block size must be a power of two";
+    return LMH_INVALID_ARGUMENT;
+  }
+  if (bt < 16) {
+    g_create_error = "the HIP page layout needs blocks of at least 16 positions";
+    return LMH_UNSUPPORTED;
+  }
+  if (o->n_layers == 0 || !o->layers) {
+    g_create_error = "no attention layers";
+    return LMH_INVALID_ARGUMENT;
+  }
+  lmh_kv* kv = new (std::nothrow) lmh_kv();
+  if (!kv) return LMH_OUT_OF_MEMORY;
+  kv->kv_type = o->kv_type;
+  kv->bt = bt;
+  kv->bt_shift = 0;
+  while ((1u << kv->bt_shift) < bt) kv->bt_shift++;
+  kv->max_ctx = std::max<uint64_t>(o->max_ctx, 1);
+  kv->n_seqs = std::max<uint64_t>(o->n_seqs, 1);
+  // KvLayout::new (kv.rs:402-497): per layer K rows then V rows of bt positions; same byte totals.
+  uint64_t off = 0;
+  for (uint32_t l = 0; l < o->n_layers; l++) {
+    const lmh_layer_desc& d = o->layers[l];
+    if (d.n_kv == 0 || d.n_head == 0 || d.n_head % d.n_kv != 0 || d.hd == 0 || d.hdv == 0) {
+      delete kv;
+      g_create_error = "bad layer geometry";
+      return LMH_INVALID_ARGUMENT;
+    }
+    if (o->kv_type == LMH_KV_Q8_0 && (d.hd % 32 != 0 || d.hdv % 32 != 0)) {  // kv.rs:103-109
+      delete kv;
+      g_create_error = "q8_0 cannot hold heads that are not a multiple of 32 wide";
+      return LMH_INVALID_ARGUMENT;
+    }
+    if (!decode_supported(o->kv_type, d.hd, d.hdv) || (o->kv_type == LMH_KV_Q8_0 && d.hd % 64 != 0)) {
+      delete kv;
+      g_create_error = "unsupported head geometry for the HIP kernels (hd = hdv in {64, 128, 256})";
+      return LMH_UNSUPPORTED;
+    }
+    LayerLayout y{};
+    y.n_head = d.n_head;
+    y.n_kv = d.n_kv;
+    y.hd = d.hd;
+    y.hdv = d.hdv;
+    y.k_row = ref_row_bytes(o->kv_type, (uint64_t)d.n_kv * d.hd);
+    y.v_row = ref_row_bytes(o->kv_type, (uint64_t)d.n_kv * d.hdv);
+    const uint32_t tiles = bt / 16;
+    y.k_tile = tile_bytes(o->kv_type, d.hd);
+    y.v_tile = tile_bytes(o->kv_type, d.hdv);
+    y.k_tile_s = tile_scale_bytes(o->kv_type, d.hd);
+    y.v_tile_s = tile_scale_bytes(o->kv_type, d.hdv);
+    y.k_scale = tiles * y.k_tile;
+    y.v_scale = tiles * y.v_tile;
+    y.k_head = tiles * (y.k_tile + y.k_tile_s);
+    y.v_head = tiles * (y.v_tile + y.v_tile_s);
+    y.k_off = (uint32_t)off;
+    off += (uint64_t)d.n_kv * y.k_head;
+    y.v_off = (uint32_t)off;
+    off += (uint64_t)d.n_kv * y.v_head;
+    kv->layers.push_back(y);
+  }
+  kv->block_bytes = off;
+  kv->bps = (kv->max_ctx + bt - 1) / bt;
+  if (o->pool_tokens > 0) {
+    const uint64_t t = o->pool_tokens;
+    kv->pool_blocks = std::min((t + bt - 1) / bt, kv->n_seqs * kv->bps) + kv->n_seqs;
+  } else {
+    kv->pool_blocks = kv->n_seqs * (kv->bps + 1);
+  }
+  if (kv->pool_blocks > 0x7fffffffull) {
+    delete kv;
+    g_create_error = "pool too large";
+    return LMH_INVALID_ARGUMENT;
+  }
+  kv->meta.assign(kv->pool_blocks, BlockMeta{});
+  for (uint64_t i = 0; i < kv->pool_blocks; i++) kv->free_q.push_back((uint32_t)i);
+  kv->backed.assign(kv->pool_blocks, 0);
+  kv->seqs.assign(kv->n_seqs, Seq{});
+  kv->h_table.assign(kv->n_seqs * kv->bps, -1);
+  kv->device = o->device;
+  hipError_t e = hipSetDevice(o->device);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_pool, kv->pool_blocks * kv->block_bytes);
+  if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
+  if (e != hipSuccess) {
+    g_create_error = std::string("device allocation failed: ") + hipGetErrorString(e);
+    delete kv;
+    return e == hipErrorOutOfMemory ? LMH_OUT_OF_MEMORY : LMH_DEVICE_ERROR;
+  }
+  *out = kv;
+  return LMH_OK;
+}
+
+void lmh_kv_destroy(lmh_kv* kv) { delete kv; }
+
+const char* lmh_kv_last_error(const lmh_kv* kv) { return kv ? kv->err.c_str() : "null handle"; }
+
+int32_t lmh_kv_layout(const lmh_kv* kv, lmh_layout_info* out) {
+  if (!kv || !out) return LMH_INVALID_ARGUMENT;
+  out->block_bytes = kv->block_bytes;
+  out->blocks_per_seq = kv->bps;
+  out->n_seqs = kv->n_seqs;
+  out->pool_blocks = kv->pool_blocks;
+  out->max_ctx = kv->max_ctx;
+  out->block_tokens = kv->bt;
+  out->kv_type = kv->kv_type;
+  return LMH_OK;
+}
+
+uint64_t lmh_kv_fingerprint(const lmh_kv* kv) {
+  if (!kv) return 0;
+  Fnv h;
+  h.bytes("hip", 3);
+  const uint32_t one = 1;
+  h.bytes(&one, 1);  // little-endian tag
+  h.u64(kv->kv_type);
+  h.u64(kv->bt);
+  h.u64(kv->block_bytes);
+  h.u64(kv->max_ctx);
+  for (const auto& y : kv->layers) {
+    h.u64(y.n_kv);
+    h.u64(y.hd);
+    h.u64(y.hdv);
+    h.u64(y.k_off);
+    h.u64(y.v_off);
+    h.u64(y.k_head);
+    h.u64(y.v_head);
+  }
+  return h.h;
+}
+
+int32_t lmh_kv_seq_len(const lmh_kv* kv, uint64_t seq, uint64_t* len) {
+  if (!kv || !len || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  *len = kv->seqs[seq].len;
+  return LMH_OK;
+}
+
+int32_t lmh_kv_set_seq_len(lmh_kv* kv, uint64_t seq, uint64_t len) {
+  if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  if (len > kv->seqs[seq].blocks.size() * kv->bt) return kv->fail(LMH_INVALID_ARGUMENT, "length beyond reserved blocks");
+  kv->seqs[seq].len = len;
+  return LMH_OK;
+}
+
+int32_t lmh_kv_free_blocks(const lmh_kv* kv, uint64_t* n) {
+  if (!kv || !n) return LMH_INVALID_ARGUMENT;
+  *n = kv->free_q.size();
+  return LMH_OK;
+}
+
+int32_t lmh_kv_resident_blocks(const lmh_kv* kv, uint64_t* n) {
+  if (!kv || !n) return LMH_INVALID_ARGUMENT;
+  uint64_t c = 0;
+  for (uint8_t b : kv->backed) c += b;
+  *n = c;
+  return LMH_OK;
+}
+
+int32_t lmh_kv_blocks_needed(const lmh_kv* kv, uint64_t seq, uint64_t new_len, uint64_t* needed) {
+  if (!kv || !needed || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  *needed = kv->blocks_needed(seq, new_len);
+  return LMH_OK;
+}
+
+int32_t lmh_kv_reserve(lmh_kv* kv, uint64_t seq, uint64_t new_len, uint64_t* needed, uint64_t* free_blocks) {
+  if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  return kv->reserve(seq, new_len, needed, free_blocks);
+}
+
+int32_t lmh_kv_truncate(lmh_kv* kv, uint64_t seq, uint64_t n) {
+  if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  kv->truncate(seq, n);
+  return LMH_OK;
+}
+
+int32_t lmh_kv_clear(lmh_kv* kv, uint64_t seq) {
+  if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  kv->clear(seq);
+  return LMH_OK;
+}
+
+int32_t lmh_kv_block_table(const lmh_kv* kv, uint64_t seq, uint32_t* out, uint64_t cap, uint64_t* n) {
+  if (!kv || !n || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  const auto& b = kv->seqs[seq].blocks;
+  for (uint64_t i = 0; i < b.size() && i < cap && out; i++) out[i] = b[i];
+  *n = b.size();
+  return LMH_OK;
+}
+
+int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, uint64_t n) {
+  if (!kv || seq >= kv->n_seqs || (n > 0 && !blocks)) return LMH_INVALID_ARGUMENT;
+  if (!kv->seqs[seq].blocks.empty()) return kv->fail(LMH_INVALID_ARGUMENT, "sequence already holds blocks");
+  if (n > kv->bps) return kv->fail(LMH_INVALID_ARGUMENT, "more blocks than one sequence can hold");
+  std::vector<uint8_t> want(kv->pool_blocks, 0);
+  for (uint64_t i = 0; i < n; i++) {
+    if (blocks[i] >= kv->pool_blocks || want[blocks[i]])
+      return kv->fail(LMH_INVALID_ARGUMENT, "block id out of range or repeated");
+    want[blocks[i]] = 1;
+  }
+  uint64_t found = 0;
+  for (uint32_t b : kv->free_q) found += want[b];
+  if (found != n) return kv->fail(LMH_INVALID_ARGUMENT, "a requested block is not free");
+  std::deque<uint32_t> rest;
+  for (uint32_t b : kv->free_q)
+    if (!want[b]) rest.push_back(b);
+  kv->free_q.swap(rest);
+  for (uint64_t i = 0; i < n; i++) {
+    BlockMeta& m = kv->meta[blocks[i]];
+    if (m.has_hash) {
+      kv->by_hash.erase(m.hash);
+      m.has_hash = false;
+      kv->evictions++;
+    }
+    m.refs = 1;
+    kv->back(blocks[i], true);
+    kv->seqs[seq].blocks.push_back(blocks[i]);
+  }
+  kv->set_table(seq);
+  return LMH_OK;
+}
+
+int32_t lmh_pool_refs(const lmh_kv* kv, uint32_t block, uint32_t* refs) {
+  if (!kv || !refs || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
+  *refs = kv->meta[block].refs;
+  return LMH_OK;
+}
+
+int32_t lmh_pool_set_hash(lmh_kv* kv, uint32_t block, const uint8_t hash[32]) {  // lib.rs:113-118
+  if (!kv || !hash || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
+  Hash h;
+  std::memcpy(h.data(), hash, 32);
+  BlockMeta& m = kv->meta[block];
+  if (m.has_hash) kv->by_hash.erase(m.hash);
+  m.hash = h;
+  m.has_hash = true;
+  kv->by_hash[h] = block;
+  return LMH_OK;
+}
+
+int32_t lmh_pool_clear_hash(lmh_kv* kv, uint32_t block) {
+  if (!kv || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
+  kv->pool_clear_hash(block);
+  kv->maybe_unback(block);
+  return LMH_OK;
+}
+
+int32_t lmh_pool_is_cached(const lmh_kv* kv, uint32_t block, int32_t* cached) {
+  if (!kv || !cached || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
+  *cached = kv->meta[block].has_hash ? 1 : 0;
+  return LMH_OK;
+}
+
+// forward.rs:207-262: checks, then all-or-nothing reservation, then Rows::push in batch order
+// (one pass: paged layers never bound the per-call append, kv.rs:522-531).
+int32_t lmh_batch_prepare(lmh_kv* kv, const lmh_seq_tokens* batch, uint64_t n, lmh_seg* segs_out, uint64_t* n_rows,
+                          uint64_t* needed, uint64_t* free_blocks) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  if (n == 0 || !batch || !segs_out) return kv->fail(LMH_INVALID_ARGUMENT, "empty batch");
+  if (n > kv->n_seqs) return kv->fail(LMH_INVALID_ARGUMENT, "more sequences than slots in one call");
+  for (uint64_t i = 0; i < n; i++) {
+    if (batch[i].seq >= kv->n_seqs) return kv->fail(LMH_INVALID_ARGUMENT, "sequence out of range");
+    if (batch[i].n_tokens == 0) return kv->fail(LMH_INVALID_ARGUMENT, "empty token list");
+    for (uint64_t j = 0; j < i; j++)
+      if (batch[j].seq == batch[i].seq) return kv->fail(LMH_INVALID_ARGUMENT, "sequence appears twice in one batch");
+    if (kv->seqs[batch[i].seq].len + batch[i].n_tokens > kv->max_ctx)
+      return kv->fail(LMH_INVALID_ARGUMENT, "context overflow");
+  }
+  uint64_t need = 0;
+  for (uint64_t i = 0; i < n; i++) need += kv->blocks_needed(batch[i].seq, kv->seqs[batch[i].seq].len + batch[i].n_tokens);
+  if (need > kv->free_q.size()) {
+    if (needed) *needed = need;
+    if (free_blocks) *free_blocks = kv->free_q.size();
+    return kv->fail(LMH_KV_FULL, "KV cache full: " + std::to_string(need) + " more blocks needed, " +
+                                     std::to_string(kv->free_q.size()) + " free");
+  }
+  for (uint64_t i = 0; i < n; i++) kv->reserve(batch[i].seq, kv->seqs[batch[i].seq].len + batch[i].n_tokens, nullptr, nullptr);
+  uint64_t start = 0;
+  for (uint64_t i = 0; i < n; i++) {
+    segs_out[i].seq = batch[i].seq;
+    segs_out[i].start = start;
+    segs_out[i].n = batch[i].n_tokens;
+    segs_out[i].pos0 = kv->seqs[batch[i].seq].len;
+    start += batch[i].n_tokens;
+  }
+  if (n_rows) *n_rows = start;
+  return LMH_OK;
+}
+
+int32_t lmh_batch_commit(lmh_kv* kv, const lmh_seg* segs, uint64_t n_segs) {
+  if (!kv || (n_segs > 0 && !segs)) return LMH_INVALID_ARGUMENT;
+  for (uint64_t i = 0; i < n_segs; i++) {
+    if (segs[i].seq >= kv->n_seqs) return kv->fail(LMH_INVALID_ARGUMENT, "sequence out of range");
+    const uint64_t nl = kv->seqs[segs[i].seq].len + segs[i].n;
+    if (nl > kv->seqs[segs[i].seq].blocks.size() * kv->bt) return kv->fail(LMH_INVALID_ARGUMENT, "commit beyond reserved blocks");
+  }
+  for (uint64_t i = 0; i < n_segs; i++) kv->seqs[segs[i].seq].len += segs[i].n;
+  return LMH_OK;
+}
+
+static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const void* a, const void* b,
+                     void* stream, int mode) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  if (layer >= kv->layers.size()) return kv->fail(LMH_INVALID_ARGUMENT, "layer out of range");
+  uint64_t n_rows;
+  int32_t rc = kv->rows_from(segs, n_segs, n_rows);
+  if (rc != LMH_OK) return rc;
+  if (n_rows == 0) return LMH_OK;
+  if (!a || !b) return kv->fail(LMH_INVALID_ARGUMENT, "null data pointer");
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = kv->flush(st)) != LMH_OK) return rc;
+  const int32_t *rs, *rp;
+  const uint8_t* ex;
+  if ((rc = kv->upload_rows(st, nullptr, 0, rs, rp, ex)) != LMH_OK) return rc;
+  const PageGeom g = kv->geom(layer);
+  const LayerLayout& y = kv->layers[layer];
+  hipError_t e = hipSuccess;
+  switch (mode) {
+    case 0: e = launch_store_f32(g, rs, rp, (uint32_t)n_rows, (const float*)a, (const float*)b, st); break;
+    case 1:
+      e = launch_store_encoded(g, rs, rp, (uint32_t)n_rows, (const uint8_t*)a, (const uint8_t*)b, (uint32_t)y.k_row,
+                               (uint32_t)y.v_row, st);
+      break;
+    case 2: e = launch_gather(g, rs, rp, (uint32_t)n_rows, (float*)a, (float*)b, st); break;
+    case 3:
+      e = launch_gather_encoded(g, rs, rp, (uint32_t)n_rows, (uint8_t*)a, (uint8_t*)b, (uint32_t)y.k_row,
+                                (uint32_t)y.v_row, st);
+      break;
+  }
+  if (e != hipSuccess) return kv->hip_fail(e, "kernel launch");
+  return LMH_OK;
+}
+
+int32_t lmh_kv_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* k, const float* v,
+                     void* stream) {
+  return kv_io(kv, layer, segs, n_segs, k, v, stream, 0);
+}
+int32_t lmh_kv_store_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const void* k,
+                             const void* v, void* stream) {
+  return kv_io(kv, layer, segs, n_segs, k, v, stream, 1);
+}
+int32_t lmh_kv_gather(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, float* k, float* v,
+                      void* stream) {
+  return kv_io(kv, layer, segs, n_segs, k, v, stream, 2);
+}
+int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, void* k, void* v,
+                              void* stream) {
+  return kv_io(kv, layer, segs, n_segs, k, v, stream, 3);
+}
+
+int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q, float* out,
+                   float scale, uint64_t window, void* stream) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  if (layer >= kv->layers.size()) return kv->fail(LMH_INVALID_ARGUMENT, "layer out of range");
+  if (!std::isfinite(scale)) return kv->fail(LMH_INVALID_ARGUMENT, "scale must be finite");
+  uint64_t n_rows;
+  int32_t rc = kv->rows_from(segs, n_segs, n_rows);
+  if (rc != LMH_OK) return rc;
+  if (n_rows == 0) return LMH_OK;
+  if (!q || !out) return kv->fail(LMH_INVALID_ARGUMENT, "null q/out");
+  const LayerLayout& y = kv->layers[layer];
+  const uint32_t group = y.n_head / y.n_kv;
+  const uint32_t ng = std::min<uint32_t>(group, 16);
+  const uint32_t head_blocks = (group + ng - 1) / ng;
+  hipStream_t st = (hipStream_t)stream;
+
+  // ---- work list: per (row, KV head, head block), the key range [lo, pos] cut into chunks of
+  // whole 16-token tiles, spread evenly; rows whose range fits one chunk write the output.
+  uint64_t total_tiles = 0;
+  for (uint64_t t = 0; t < n_rows; t++) {
+    const uint64_t pos = (uint64_t)kv->row_pos[t];
+    const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+    total_tiles += pos / 16 - lo / 16 + 1;
+  }
+  total_tiles *= (uint64_t)y.n_kv * head_blocks;
+  const uint64_t target = env_u64("LMH_DECODE_TARGET_ITEMS", 2048);
+  const uint64_t min_chunk = std::max<uint64_t>(env_u64("LMH_DECODE_MIN_TILES", 8), 1);
+  const uint64_t chunk = std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / std::max<uint64_t>(target, 1));
+  kv->items.clear();
+  kv->merges.clear();
+  uint32_t slots = 0;
+  for (uint64_t t = 0; t < n_rows; t++) {
+    const uint64_t pos = (uint64_t)kv->row_pos[t];
+    const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+    const uint64_t hi = pos + 1;
+    const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
+    const uint64_t n_split = (n_t + chunk - 1) / chunk;
+    for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
+      for (uint32_t hb = 0; hb < head_blocks; hb++) {
+        if (n_split == 1) {
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT});
+          continue;
+        }
+        kv->merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, slots, (uint32_t)n_split, 0});
+        for (uint64_t s = 0; s < n_split; s++) {
+          const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
+          const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++});
+        }
+      }
+    }
+  }
+  if ((rc = kv->flush(st)) != LMH_OK) return rc;
+  const size_t items_bytes = kv->items.size() * sizeof(DecodeItem);
+  const size_t items_pad = (items_bytes + 255) / 256 * 256;
+  std::vector<uint8_t> extra(items_pad + kv->merges.size() * sizeof(MergeItem));
+  std::memcpy(extra.data(), kv->items.data(), items_bytes);
+  if (!kv->merges.empty()) std::memcpy(extra.data() + items_pad, kv->merges.data(), kv->merges.size() * sizeof(MergeItem));
+  const int32_t *rs, *rp;
+  const uint8_t* ex;
+  if ((rc = kv->upload_rows(st, extra.data(), extra.size(), rs, rp, ex)) != LMH_OK) return rc;
+  hipError_t e;
+  if (slots > 0) {
+    if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+  }
+  const PageGeom g = kv->geom(layer);
+  RowGeom r{};
+  r.row_seq = rs;
+  r.row_pos = rp;
+  r.n_head = y.n_head;
+  r.group = group;
+  r.ng = ng;
+  r.scale_log2 = scale * 1.4426950408889634f;
+  r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
+  if ((e = kv->time_begin(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, st);
+  if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
+  if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  if (!kv->merges.empty()) {
+    e = launch_merge(r, y.hdv, (const MergeItem*)(ex + items_pad), (uint32_t)kv->merges.size(),
+                     (const float*)kv->part_buf.p, out, st);
+    if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
+  }
+  return LMH_OK;
+}
+
+int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  kv->timing = enable != 0;
+  return LMH_OK;
+}
+
+int32_t lmh_kv_kernel_time(lmh_kv* kv, double* ms, uint64_t* launches) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  for (size_t i = 0; i < kv->ev_used; i++) {
+    float t = 0;
+    hipError_t e = hipEventSynchronize(kv->evs[i].second);
+    if (e == hipSuccess) e = hipEventElapsedTime(&t, kv->evs[i].first, kv->evs[i].second);
+    if (e != hipSuccess) return kv->hip_fail(e, "event timing");
+    kv->acc_ms += t;
+    kv->launches++;
+  }
+  kv->ev_used = 0;
+  if (ms) *ms = kv->acc_ms;
+  if (launches) *launches = kv->launches;
+  kv->acc_ms = 0;
+  kv->launches = 0;
+  return LMH_OK;
+}
+
+}  // extern "C"

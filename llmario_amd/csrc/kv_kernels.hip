@@ -1,0 +1,273 @@
+// kv_kernels.hip — paged KV writes, reads and block zeroing on gfx950.
+//
+// store:   KvCache::store_k / store_v (crates/engine/model/src/kv.rs:870-889) for a batch of
+//          rows: f32 in, encoded as the cache type (KvType::store, kv.rs:112-126), scattered to
+//          the row's (block, tile, slot) through the block table (BlockTable::locate,
+//          kv/src/lib.rs:243-253).
+// encoded: the same rows given in the reference's row encoding (f16/bf16 bits, f32, q8_0
+//          34-byte blocks), transcoded into the page layout; the inverse read gives the bytes back.
+// gather:  LayerReader::row + KvType::load (kv.rs:1166-1179, 131-151) decoded to f32.
+//
+// One workgroup per row; these kernels move ~n_kv*(hd+hdv) values per row and are HBM-bound.
+#include "device.h"
+
+namespace lmh {
+namespace {
+
+struct Slot {
+  uint8_t* base;  // block base + layer offset handled by callers
+  uint32_t tile, m;
+};
+
+__device__ inline Slot locate(const PageGeom& g, int seq, uint32_t pos) {
+  const int blk = g.table[(size_t)seq * g.bps + (pos >> g.bt_shift)];
+  const uint32_t in_blk = pos & ((1u << g.bt_shift) - 1u);
+  Slot s;
+  s.base = g.pool + (size_t)blk * g.block_bytes;
+  s.tile = in_blk >> 4;
+  s.m = in_blk & 15u;
+  return s;
+}
+
+// f32 -> f16, round to nearest even (v_cvt_f16_f32 under the default rounding mode).
+__device__ inline uint16_t f16_bits(float x) {
+  _Float16 h = (_Float16)x;
+  return __builtin_bit_cast(uint16_t, h);
+}
+__device__ inline float f16_val(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+// f32 -> bf16, round to nearest even on the dropped 16 bits (NaN kept quiet).
+__device__ inline uint16_t bf16_bits(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ inline float bf16_val(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
+
+// Byte offset of element (m, d) of a 16-token tile, and of its q8_0 scale, for one side (K or V).
+__device__ inline uint32_t elem_off(uint32_t type, bool is_v, uint32_t m, uint32_t d, uint32_t dim) {
+  switch (type) {
+    case KV_F16:
+    case KV_BF16: return is_v ? v16_off(m, d) : k16_off(m, d);
+    case KV_Q8: return is_v ? vq8_off(m, d) : kq8_off(m, d);
+    default: return (m * dim + d) * 4u;
+  }
+}
+
+struct Side {
+  uint32_t off, head, tile, scale, tile_s, dim;
+};
+__device__ inline Side side(const PageGeom& g, bool is_v) {
+  Side s;
+  s.off = is_v ? g.v_off : g.k_off;
+  s.head = is_v ? g.v_head : g.k_head;
+  s.tile = is_v ? g.v_tile : g.k_tile;
+  s.scale = is_v ? g.v_scale : g.k_scale;
+  s.tile_s = is_v ? g.v_tile_s : g.k_tile_s;
+  s.dim = is_v ? g.hdv : g.hd;
+  return s;
+}
+
+// Encode one row side (n_kv*dim values starting at src) into its pages. Threads stride over the
+// elements in steps of blockDim.x (a multiple of 32), so a q8_0 block of 32 values is one half
+// wave and its amax is a 32-lane reduction.
+__device__ void store_side(const PageGeom& g, const Slot& sl, bool is_v, const float* src) {
+  const Side sd = side(g, is_v);
+  const uint32_t n = g.n_kv * sd.dim;
+  for (uint32_t e = threadIdx.x; e < n; e += blockDim.x) {
+    const uint32_t h = e / sd.dim, d = e % sd.dim;
+    uint8_t* head = sl.base + sd.off + h * sd.head;
+    const float x = src[e];
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    switch (g.kv_type) {
+      case KV_F16: *(uint16_t*)(head + o) = f16_bits(x); break;
+      case KV_BF16: *(uint16_t*)(head + o) = bf16_bits(x); break;
+      case KV_F32: *(float*)(head + o) = x; break;
+      case KV_Q8: {
+        // quantize_q8_0 (kv.rs:156-171): d = amax/127, id = d ? 1/d : 0, q = round_ties_even(x*id)
+        float amax = fabsf(x);
+        for (int w = 16; w >= 1; w >>= 1) amax = fmaxf(amax, __shfl_xor(amax, w, 32));
+        const float dsc = amax / 127.0f;
+        const float id = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+        const float r = rintf(x * id);
+        head[o] = (uint8_t)(int8_t)(int32_t)r;
+        if ((d & 31u) == 0) {
+          uint8_t* sp = head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d >> 5)) * 2u;
+          *(uint16_t*)sp = f16_bits(dsc);
+        }
+        break;
+      }
+    }
+  }
+}
+
+__global__ void store_f32_kernel(PageGeom g, const int32_t* row_seq, const int32_t* row_pos, const float* k,
+                                 const float* v) {
+  const uint32_t row = blockIdx.x;
+  const Slot sl = locate(g, row_seq[row], (uint32_t)row_pos[row]);
+  store_side(g, sl, false, k + (size_t)row * g.n_kv * g.hd);
+  store_side(g, sl, true, v + (size_t)row * g.n_kv * g.hdv);
+}
+
+// Reference row encoding -> page layout (bit copy, no re-rounding).
+__device__ void store_enc_side(const PageGeom& g, const Slot& sl, bool is_v, const uint8_t* src) {
+  const Side sd = side(g, is_v);
+  const uint32_t n = g.n_kv * sd.dim;
+  for (uint32_t e = threadIdx.x; e < n; e += blockDim.x) {
+    const uint32_t h = e / sd.dim, d = e % sd.dim;
+    uint8_t* head = sl.base + sd.off + h * sd.head;
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    switch (g.kv_type) {
+      case KV_F16:
+      case KV_BF16: *(uint16_t*)(head + o) = (uint16_t)(src[2 * e] | (src[2 * e + 1] << 8)); break;
+      case KV_F32: {
+        uint32_t u = src[4 * e] | (src[4 * e + 1] << 8) | (src[4 * e + 2] << 16) | ((uint32_t)src[4 * e + 3] << 24);
+        *(uint32_t*)(head + o) = u;
+        break;
+      }
+      case KV_Q8: {
+        const uint8_t* blk = src + (e >> 5) * 34u;
+        head[o] = blk[2 + (e & 31u)];
+        if ((d & 31u) == 0) {
+          uint8_t* sp = head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d >> 5)) * 2u;
+          *(uint16_t*)sp = (uint16_t)(blk[0] | (blk[1] << 8));
+        }
+        break;
+      }
+    }
+  }
+}
+
+__global__ void store_encoded_kernel(PageGeom g, const int32_t* row_seq, const int32_t* row_pos, const uint8_t* k,
+                                     const uint8_t* v, uint32_t k_row, uint32_t v_row) {
+  const uint32_t row = blockIdx.x;
+  const Slot sl = locate(g, row_seq[row], (uint32_t)row_pos[row]);
+  store_enc_side(g, sl, false, k + (size_t)row * k_row);
+  store_enc_side(g, sl, true, v + (size_t)row * v_row);
+}
+
+__device__ float load_elem(const PageGeom& g, const Slot& sl, bool is_v, uint32_t e) {
+  const Side sd = side(g, is_v);
+  const uint32_t h = e / sd.dim, d = e % sd.dim;
+  const uint8_t* head = sl.base + sd.off + h * sd.head;
+  const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+  switch (g.kv_type) {
+    case KV_F16: return f16_val(*(const uint16_t*)(head + o));
+    case KV_BF16: return bf16_val(*(const uint16_t*)(head + o));
+    case KV_F32: return *(const float*)(head + o);
+    default: {
+      // dequantize_q8_0 (kv.rs:174-184): (q as i8) as f32 * d, exact in f32
+      const uint8_t* sp = head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d >> 5)) * 2u;
+      return (float)(int8_t)head[o] * f16_val(*(const uint16_t*)sp);
+    }
+  }
+}
+
+__global__ void gather_kernel(PageGeom g, const int32_t* row_seq, const int32_t* row_pos, float* k, float* v) {
+  const uint32_t row = blockIdx.x;
+  const Slot sl = locate(g, row_seq[row], (uint32_t)row_pos[row]);
+  const uint32_t nk = g.n_kv * g.hd, nv = g.n_kv * g.hdv;
+  for (uint32_t e = threadIdx.x; e < nk; e += blockDim.x) k[(size_t)row * nk + e] = load_elem(g, sl, false, e);
+  for (uint32_t e = threadIdx.x; e < nv; e += blockDim.x) v[(size_t)row * nv + e] = load_elem(g, sl, true, e);
+}
+
+__device__ void gather_enc_side(const PageGeom& g, const Slot& sl, bool is_v, uint8_t* dst) {
+  const Side sd = side(g, is_v);
+  const uint32_t n = g.n_kv * sd.dim;
+  for (uint32_t e = threadIdx.x; e < n; e += blockDim.x) {
+    const uint32_t h = e / sd.dim, d = e % sd.dim;
+    const uint8_t* head = sl.base + sd.off + h * sd.head;
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    switch (g.kv_type) {
+      case KV_F16:
+      case KV_BF16: {
+        const uint16_t b = *(const uint16_t*)(head + o);
+        dst[2 * e] = (uint8_t)b;
+        dst[2 * e + 1] = (uint8_t)(b >> 8);
+        break;
+      }
+      case KV_F32: {
+        const uint32_t u = *(const uint32_t*)(head + o);
+        for (int i = 0; i < 4; i++) dst[4 * e + i] = (uint8_t)(u >> (8 * i));
+        break;
+      }
+      case KV_Q8: {
+        uint8_t* blk = dst + (e >> 5) * 34u;
+        blk[2 + (e & 31u)] = head[o];
+        if ((d & 31u) == 0) {
+          const uint8_t* sp = head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d >> 5)) * 2u;
+          blk[0] = sp[0];
+          blk[1] = sp[1];
+        }
+        break;
+      }
+    }
+  }
+}
+
+__global__ void gather_encoded_kernel(PageGeom g, const int32_t* row_seq, const int32_t* row_pos, uint8_t* k,
+                                      uint8_t* v, uint32_t k_row, uint32_t v_row) {
+  const uint32_t row = blockIdx.x;
+  const Slot sl = locate(g, row_seq[row], (uint32_t)row_pos[row]);
+  gather_enc_side(g, sl, false, k + (size_t)row * k_row);
+  gather_enc_side(g, sl, true, v + (size_t)row * v_row);
+}
+
+// Zero whole blocks (a newly backed block reads as zeros, like the reference's anonymous
+// mappings, kv.rs:29-37). block_bytes is a multiple of 16.
+__global__ void zero_blocks_kernel(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n) {
+  const uint64_t per = block_bytes / 16u;
+  const uint32_t b = blockIdx.y;
+  if (b >= n) return;
+  uint4* base = (uint4*)(pool + (size_t)blocks[b] * block_bytes);
+  for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < per; i += (uint64_t)gridDim.x * blockDim.x)
+    base[i] = make_uint4(0, 0, 0, 0);
+}
+
+}  // namespace
+
+hipError_t launch_store_f32(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
+                            const float* k, const float* v, hipStream_t s) {
+  if (n_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(store_f32_kernel, dim3(n_rows), dim3(256), 0, s, g, row_seq, row_pos, k, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_store_encoded(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos,
+                                uint32_t n_rows, const uint8_t* k, const uint8_t* v, uint32_t k_row,
+                                uint32_t v_row, hipStream_t s) {
+  if (n_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(store_encoded_kernel, dim3(n_rows), dim3(256), 0, s, g, row_seq, row_pos, k, v, k_row, v_row);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
+                         float* k, float* v, hipStream_t s) {
+  if (n_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_kernel, dim3(n_rows), dim3(256), 0, s, g, row_seq, row_pos, k, v);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos,
+                                 uint32_t n_rows, uint8_t* k, uint8_t* v, uint32_t k_row, uint32_t v_row,
+                                 hipStream_t s) {
+  if (n_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(gather_encoded_kernel, dim3(n_rows), dim3(256), 0, s, g, row_seq, row_pos, k, v, k_row,
+                     v_row);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
+                              hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const uint64_t per = block_bytes / 16u;
+  uint32_t gx = (uint32_t)((per + 255) / 256);
+  if (gx > 64) gx = 64;
+  for (uint32_t b0 = 0; b0 < n; b0 += 65535u) {
+    const uint32_t nb = (n - b0) < 65535u ? (n - b0) : 65535u;
+    hipLaunchKernelGGL(zero_blocks_kernel, dim3(gx, nb), dim3(256), 0, s, pool, block_bytes, blocks + b0, nb);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace lmh

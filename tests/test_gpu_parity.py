@@ -1,0 +1,201 @@
+"""GPU parity: the HIP path against the CPU oracle on identical seeded inputs, through the C ABI.
+
+Block tables, free counts and KvFull outcomes must be identical; gathered rows byte-identical in
+the reference's row encoding; attention outputs within the per-row relative tolerance
+(1e-5 f32, 2e-3 f16/bf16/q8_0), max over rows and heads of ||got - ref||_inf / ||ref||_inf.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from conftest import TOL, row_rel_err
+from llmario_amd import harness
+from llmario_amd.kv import HipKvCache, KvFull, Layer
+from llmario_amd.workloads import Generator, config, small
+
+pytestmark = pytest.mark.gpu
+
+THREADS = min(os.cpu_count() or 1, 16)
+
+
+def pair(w):
+    import torch
+    gen = Generator(w)
+    oc = O.empty_cache_for(w)
+    hc = harness.load(w, gen, on_rows=lambda s, t, k, v: O.fill(oc, t, s, k, v, w.prior[s]))
+    q = gen.q()
+    return hc, oc, q
+
+
+def run_gpu(hc, w, q, segs=None):
+    import torch
+    segs = segs or w.segments()
+    L = w.layer
+    qd = torch.from_numpy(np.ascontiguousarray(q)).cuda()
+    out = torch.full((q.shape[0], L.n_head, L.hdv), float("nan"), device="cuda")
+    hc.attend(0, segs, qd, out, w.scale, w.window)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def oracle_rows(oc, w, q, rows):
+    """Oracle output for selected stacked rows (each attends to its own causal prefix)."""
+    pos_of, seq_of = [], []
+    for (s, start, n, pos0) in w.segments():
+        for i in range(n):
+            seq_of.append(s)
+            pos_of.append(pos0 + i)
+    segs = [(seq_of[r], i, 1, pos_of[r]) for i, r in enumerate(rows)]
+    return oc.attend(0, segs, q[rows], w.scale, w.window, THREADS)
+
+
+# ---- block bookkeeping ---------------------------------------------------------------------
+
+def test_block_tables_free_counts_and_kv_full_match(cuda):
+    layers = [(8, 2, 64, 64)]
+    hc = HipKvCache([Layer(*layers[0])], max_ctx=128, n_seqs=3, kv_type="f16", block_tokens=16, pool_tokens=160)
+    oc = O.Cache(layers, max_ctx=128, n_seqs=3, kv_type="f16", block_tokens=16, pool_tokens=160)
+    assert hc.layout()["pool_blocks"] == oc.layout()["pool_blocks"] == 13
+    assert hc.layout()["block_bytes"] == oc.layout()["block_bytes"]
+    script = [("b", [(0, 20), (1, 5)]), ("b", [(0, 1), (1, 40), (2, 16)]), ("t", 1, 7), ("b", [(2, 70)]),
+              ("c", 0), ("b", [(1, 50), (0, 33)]), ("b", [(2, 42)]), ("b", [(0, 128)]), ("t", 2, 0),
+              ("b", [(2, 60)])]
+    for step in script:
+        if step[0] == "b":
+            try:
+                segs_o, n_o = oc.prepare_batch(step[1])
+                oc.commit_batch(segs_o)
+                res_o = ("ok", segs_o, n_o)
+            except O.KvFullError as e:
+                res_o = ("full", e.needed, e.free)
+            except ValueError:
+                res_o = ("invalid",)
+            try:
+                segs_h, n_h = hc.prepare_batch(step[1])
+                hc.commit_batch(segs_h)
+                res_h = ("ok", segs_h, n_h)
+            except KvFull as e:
+                res_h = ("full", e.needed, e.free)
+            except Exception:
+                res_h = ("invalid",)
+            assert res_o == res_h, step
+        elif step[0] == "t":
+            oc.truncate(step[1], step[2])
+            hc.truncate(step[1], step[2])
+        else:
+            oc.clear(step[1])
+            hc.clear(step[1])
+        for s in range(3):
+            assert hc.blocks(s) == oc.blocks(s), (step, s)
+            assert hc.len(s) == oc.len(s)
+        assert hc.free_blocks() == oc.pool.free_blocks()
+        assert hc.resident_blocks() == oc.resident_blocks()
+
+
+# ---- stores and gathers --------------------------------------------------------------------
+
+@pytest.mark.parametrize("kv", ["f32", "f16", "bf16", "q8_0"])
+@pytest.mark.parametrize("bt", [16, 32])
+def test_store_then_gather_is_byte_exact(cuda, kv, bt):
+    import torch
+    L = Layer(8, 4, 128, 128)
+    rng = np.random.default_rng(21)
+    hc = HipKvCache([L, Layer(4, 2, 64, 64)], max_ctx=300, n_seqs=2, kv_type=kv, block_tokens=bt)
+    oc = O.Cache([(8, 4, 128, 128), (4, 2, 64, 64)], max_ctx=300, n_seqs=2, kv_type=kv, block_tokens=bt)
+    for c in (hc, oc):
+        segs, n = c.prepare_batch([(0, 37), (1, 250)])
+    assert hc.blocks(0) == oc.blocks(0) and hc.blocks(1) == oc.blocks(1)
+    for layer, (nkv, hd) in enumerate([(4, 128), (2, 64)]):
+        k = (rng.standard_normal((n, nkv * hd)) * 3).astype(np.float32)
+        v = (rng.standard_normal((n, nkv * hd)) * 3).astype(np.float32)
+        k[5, :32] = 0.0  # an all-zero q8_0 block
+        hc.store(layer, segs, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+        for (s, start, cnt, pos0) in segs:
+            oc.store_rows(s, layer, pos0, k[start:start + cnt], v[start:start + cnt])
+        li = oc.layer(layer)
+        kb = torch.zeros((n, li["k_row"]), dtype=torch.uint8, device="cuda")
+        vb = torch.zeros((n, li["v_row"]), dtype=torch.uint8, device="cuda")
+        hc.gather_encoded(layer, segs, kb, vb)
+        kf = torch.zeros((n, nkv * hd), device="cuda")
+        vf = torch.zeros((n, nkv * hd), device="cuda")
+        hc.gather(layer, segs, kf, vf)
+        torch.cuda.synchronize()
+        kb, vb, kf, vf = kb.cpu().numpy(), vb.cpu().numpy(), kf.cpu().numpy(), vf.cpu().numpy()
+        for (s, start, cnt, pos0) in segs:
+            rk, rv = oc.load_rows_raw(s, layer, pos0, cnt)
+            assert np.array_equal(kb[start:start + cnt], rk), (layer, s)
+            assert np.array_equal(vb[start:start + cnt], rv), (layer, s)
+            for i in (0, cnt // 2, cnt - 1):
+                ek, ev = oc.load(s, layer, pos0 + i)
+                assert np.array_equal(kf[start + i], ek) and np.array_equal(vf[start + i], ev)
+        # encoded rows back in: identical bytes
+        hc.store_encoded(layer, segs, torch.from_numpy(kb).cuda(), torch.from_numpy(vb).cuda())
+        kb2 = torch.zeros_like(torch.from_numpy(kb)).cuda()
+        vb2 = torch.zeros_like(torch.from_numpy(vb)).cuda()
+        hc.gather_encoded(layer, segs, kb2, vb2)
+        torch.cuda.synchronize()
+        assert np.array_equal(kb2.cpu().numpy(), kb) and np.array_equal(vb2.cpu().numpy(), vb)
+
+
+# ---- attention -----------------------------------------------------------------------------
+
+SMALL = [
+    ("f32", Layer(8, 8, 64, 64), [255], [1], 0, 16),
+    ("f32", Layer(16, 4, 128, 128), [100, 900], [1, 1], 0, 16),
+    ("f16", Layer(32, 8, 128, 128), [700, 33, 1500, 0], [1, 1, 1, 1], 0, 16),
+    ("f16", Layer(16, 1, 128, 128), [5000], [1], 0, 32),
+    ("f16", Layer(40, 8, 128, 128), [100, 333], [1, 17], 0, 16),
+    ("f16", Layer(40, 8, 128, 128), [4096, 200], [1, 64], 1000, 16),
+    ("bf16", Layer(8, 2, 64, 64), [0, 40], [48, 9], 0, 16),
+    ("bf16", Layer(32, 8, 128, 128), [2000], [3], 0, 16),
+    ("q8_0", Layer(64, 8, 128, 128), [3000, 17], [1, 1], 0, 16),
+    ("q8_0", Layer(16, 2, 64, 64), [300, 5], [1, 3], 0, 64),
+    ("f16", Layer(32, 32, 64, 64), [250, 1], [1, 1], 0, 16),
+    ("f16", Layer(64, 2, 256, 256), [700], [2], 0, 16),
+]
+
+
+@pytest.mark.parametrize("kv,layer,prior,new,window,bt", SMALL)
+@pytest.mark.parametrize("split", ["auto", "forced"])
+def test_attend_small(cuda, monkeypatch, kv, layer, prior, new, window, bt, split):
+    if split == "forced":
+        monkeypatch.setenv("LMH_DECODE_MIN_TILES", "1")
+        monkeypatch.setenv("LMH_DECODE_TARGET_ITEMS", "100000")
+    w = small("t", kv, layer, prior, new, window=window, seed=31, block_tokens=bt)
+    hc, oc, q = pair(w)
+    got = run_gpu(hc, w, q)
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    assert np.isfinite(got).all()
+    err = row_rel_err(got, ref)
+    print(f"{kv} {layer} prior={prior} new={new} window={window} bt={bt} split={split}: {err:.3e}")
+    assert err <= TOL[kv], err
+
+
+@pytest.mark.parametrize("name", ["c1", "c2", "c4"])
+def test_attend_config_all_rows(cuda, name):
+    w = config(name)
+    hc, oc, q = pair(w)
+    got = run_gpu(hc, w, q)
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    err = row_rel_err(got, ref)
+    print(f"{name}: rows={w.n_rows} max row rel err {err:.3e} (tol {TOL[w.kv_type]})")
+    assert err <= TOL[w.kv_type], err
+
+
+@pytest.mark.parametrize("name", ["c3", "c5", "c5w"])
+def test_attend_config_sampled_rows(cuda, name):
+    w = config(name)
+    hc, oc, q = pair(w)
+    got = run_gpu(hc, w, q)
+    assert np.isfinite(got).all()
+    rng = np.random.default_rng(0)
+    n = w.n_rows
+    decode_rows = [r for r in range(n) if r < 16] if name.startswith("c5") else []
+    rows = sorted(set(decode_rows) | set(rng.choice(n, size=min(n, 96), replace=False).tolist()) | {n - 1})
+    ref = oracle_rows(oc, w, q, rows)
+    err = row_rel_err(got[rows], ref)
+    print(f"{name}: {len(rows)} sampled rows, max row rel err {err:.3e} (tol {TOL[w.kv_type]})")
+    assert err <= TOL[w.kv_type], err
