@@ -14,6 +14,7 @@ CPU baseline (the C++ restatement of the reference's CPU attention, oracle/, on 
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -38,6 +39,7 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
     import torch
 
     from llmario_amd import harness
+    from llmario_amd.kv import Segments
     from llmario_amd.workloads import Generator, config
 
     w = config(name)
@@ -47,11 +49,12 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
     L = w.layer
     q = torch.from_numpy(gen.q()).cuda()
     out = torch.empty((w.n_rows, L.n_head, L.hdv), device="cuda")
-    segs = w.segments()
+    segs = Segments(w.segments())
     stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
     log(f"[bench] {name}: loaded in {time.perf_counter() - t_load:.1f}s; warmup {warmup}")
     for _ in range(warmup):
-        hc.attend(0, segs, q, out, w.scale, w.window, stream)
+        hc.attend(0, segs, q, out, w.scale, w.window, sp)
     torch.cuda.synchronize()
     hc.kernel_time()  # reset
     hc.set_timing(timing_kernel)
@@ -60,7 +63,7 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
     t0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(steps):
-        hc.attend(0, segs, q, out, w.scale, w.window, stream)
+        hc.attend(0, segs, q, out, w.scale, w.window, sp)
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -143,7 +146,20 @@ def main():
     ap.add_argument("--extra", default="c1,c3,c4,c5,c5w", help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only run a plain device copy of this many MiB (20 launches): the known-size "
+                         "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
     args = ap.parse_args()
+    if args.copy_calibration_mb:
+        import torch
+        n = args.copy_calibration_mb * (1 << 20) // 4
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copied {args.copy_calibration_mb} MiB x 20")
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the paged-attention path is single-device here (no "
               "collectives, no sharding); run with --gpus 1", file=sys.stderr)

@@ -8,8 +8,9 @@
 // Work decomposition (built on the host from the batch's segments): one wave64 per work item
 // (row, KV head, contiguous key range aligned to 16-token tiles). The key range of a long row is
 // cut into several items (split-K, as attend_split does for long contexts, forward.rs:688-807);
-// their partial (o, m, l) go to `part` and `merge_kernel` combines them with the exact
-// log-sum-exp merge of forward.rs:772-806.
+// their partial (o, m, l) go to `part`, and the last item of a row to finish (an atomic count per
+// row and KV head) combines them with the exact log-sum-exp merge of forward.rs:772-806, in the
+// same launch.
 //
 // f16 / bf16 / q8_0 pages (matrix cores): per 16-token tile,
 //   S^T[16 keys x 16 heads] = K[16 x hd] . Q^T[hd x 16]     (v_mfma_f32_16x16x32_{f16,bf16})
@@ -35,6 +36,13 @@ typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int WAVES = 4;  // waves (work items) per workgroup
+
+// Waves per SIMD the register allocator must allow: two tile buffers in flight per wave fit in
+// 256 VGPRs up to hd 128 (2 waves/SIMD); hd 256 needs the whole file (1 wave/SIMD).
+template <int HD>
+constexpr int waves_per_eu() {
+  return HD >= 256 ? 1 : 2;
+}
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -115,10 +123,58 @@ __device__ inline float scale_at(const uint4* s, int r, int c) {
   return h_to_f((uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
 }
 
+// Last-arriver merge of a split-K task (forward.rs:772-806): m* = max m_s,
+// out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m kept in the log2 domain. One wave;
+// lanes over the head's dims.
+template <int HDV>
+__device__ void merge_task(const RowGeom& r, const MergeItem& mi, uint32_t nh, const float* part, float* out,
+                           uint32_t lane) {
+  constexpr int ND = (HDV + 63) / 64;
+  for (uint32_t h = 0; h < nh; h++) {
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < mi.n_split; s++)
+      M = fmaxf(M, part[((size_t)(mi.slot0 + s) * r.ng + h) * (HDV + 4) + HDV]);
+    float L = 0.f, acc[ND];
+#pragma unroll
+    for (int i = 0; i < ND; i++) acc[i] = 0.f;
+    for (uint32_t s = 0; s < mi.n_split; s++) {
+      const float* pp = part + ((size_t)(mi.slot0 + s) * r.ng + h) * (HDV + 4);
+      const float ms = pp[HDV];
+      if (ms == -INFINITY) continue;
+      const float c = exp2_fast(ms - M);
+      L += c * pp[HDV + 1];
+#pragma unroll
+      for (int i = 0; i < ND; i++)
+        if (lane + 64 * i < (uint32_t)HDV) acc[i] += c * pp[lane + 64 * i];
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h) * HDV;
+#pragma unroll
+    for (int i = 0; i < ND; i++)
+      if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = acc[i] * inv;
+  }
+}
+
+// A split item has written its partials: count it off on its task's counter (release), and if it
+// is the last of the task, acquire everyone's partials, reset the counter and merge.
+template <int HDV>
+__device__ void finish_split(const RowGeom& r, const DecodeItem& it, const MergeItem* merges, uint32_t* counters,
+                             uint32_t nh, const float* part, float* out, uint32_t lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  uint32_t prev = 0;
+  if (lane == 0) prev = __hip_atomic_fetch_add(counters + it.merge, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  prev = __shfl(prev, 0);
+  const MergeItem mi = merges[it.merge];
+  if (prev + 1 != mi.n_split) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (lane == 0) __hip_atomic_store(counters + it.merge, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  merge_task<HDV>(r, mi, nh, part, out, lane);
+}
+
 template <int KVT, int HD, int HDV>
-__global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
-                                                                 uint32_t n_items, const float* q, float* out,
-                                                                 float* part) {
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD>(), waves_per_eu<HD>())))
+void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const MergeItem* merges,
+                        uint32_t* counters, const float* q, float* out, float* part) {
   constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
   constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
   using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
@@ -162,11 +218,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, Row
 #pragma unroll
   for (int j = 0; j < NJ; j++) O[j] = f4{0.f, 0.f, 0.f, 0.f};
 
+  // The item's tiles t0..t1 (at most 64, the host caps chunks): lane i holds the block id of
+  // tile t0 + i, so the loop reads ids with readlane instead of a dependent memory load.
   const uint32_t t0 = it.p0 >> 4, t1 = (it.p1 - 1) >> 4;
   const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
+  int my_blk = 0;
+  if (t0 + lane <= t1) my_blk = tab[((t0 + lane) << 4) >> g.bt_shift];
   auto ptrs = [&](uint32_t t, const uint8_t*& kb, const uint8_t*& vb, const uint8_t*& ksb, const uint8_t*& vsb) {
     const uint32_t pos = t << 4;
-    const int blk = tab[pos >> g.bt_shift];
+    const int blk = __builtin_amdgcn_readlane(my_blk, (int)(t - t0));
     const uint32_t sub = (pos & bt_mask) >> 4;
     const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
     const uint8_t* kh = base + g.k_off + it.kvh * g.k_head;
@@ -176,19 +236,13 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, Row
     ksb = kh + g.k_scale + sub * g.k_tile_s;
     vsb = vh + g.v_scale + sub * g.v_tile_s;
   };
-
-  TileRegs<KVT, HD, HDV> cur, nxt;
-  {
+  auto fetch = [&](TileRegs<KVT, HD, HDV>& buf, uint32_t t) {
     const uint8_t *kb, *vb, *ksb, *vsb;
-    ptrs(t0, kb, vb, ksb, vsb);
-    load_tile(cur, kb, vb, ksb, vsb, lane);
-  }
-  for (uint32_t t = t0; t <= t1; t++) {
-    if (t < t1) {
-      const uint8_t *kb, *vb, *ksb, *vsb;
-      ptrs(t + 1, kb, vb, ksb, vsb);
-      load_tile(nxt, kb, vb, ksb, vsb, lane);
-    }
+    ptrs(t, kb, vb, ksb, vsb);
+    load_tile(buf, kb, vb, ksb, vsb, lane);
+  };
+
+  auto step = [&](const TileRegs<KVT, HD, HDV>& cur, uint32_t t) {
     // ---- scores S^T for 16 keys x 16 heads
     f4 s = f4{0.f, 0.f, 0.f, 0.f};
     if constexpr (KVT == KV_Q8) {
@@ -265,12 +319,22 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, Row
         O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, O[j], 0, 0, 0);
       }
     }
-    cur = nxt;
+  };
+
+  // Two-deep ping-pong: tile t+1 is in flight while tile t is computed.
+  TileRegs<KVT, HD, HDV> b0, b1;
+  fetch(b0, t0);
+  for (uint32_t t = t0; t <= t1; t += 2) {
+    if (t + 1 <= t1) fetch(b1, t + 1);
+    step(b0, t);
+    if (t + 1 > t1) break;
+    if (t + 2 <= t1) fetch(b0, t + 2);
+    step(b1, t + 1);
   }
   lsum = xsum_groups(lsum);
 
-  if (!hv) return;
   if (it.slot == NO_SLOT) {
+    if (!hv) return;
     const float inv = 1.0f / lsum;
     float* op = out + ((size_t)it.row * r.n_head + head) * HDV;
 #pragma unroll
@@ -278,7 +342,9 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, Row
       const f4 o = O[j] * inv;
       *(float4*)(op + 16 * j + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
     }
-  } else {
+    return;
+  }
+  if (hv) {
     float* pp = part + ((size_t)it.slot * r.ng + hq) * (HDV + 4);
 #pragma unroll
     for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][0], O[j][1], O[j][2], O[j][3]);
@@ -287,12 +353,15 @@ __global__ __launch_bounds__(64 * WAVES) void decode_mfma_kernel(PageGeom g, Row
       pp[HDV + 1] = lsum;
     }
   }
+  const uint32_t nh = (it.h0 + r.ng <= r.group) ? r.ng : r.group - it.h0;
+  finish_split<HDV>(r, it, merges, counters, nh, part, out, lane);
 }
 
 // ---- f32 pages: VALU path ----------------------------------------------------------------------
 template <int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
-                                                                uint32_t n_items, const float* q, float* out,
+                                                                uint32_t n_items, const MergeItem* merges,
+                                                                uint32_t* counters, const float* q, float* out,
                                                                 float* part) {
   constexpr int NG = 16;
   constexpr int ND = HDV / 64 > 0 ? HDV / 64 : 1;  // dims per lane in P.V
@@ -301,7 +370,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t wi = blockIdx.x * WAVES + w;
   const bool active = wi < n_items;
-  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT};
+  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, NO_SLOT, 0};
   const uint32_t ng = r.ng;
   const uint32_t nh = (it.h0 + ng <= r.group) ? ng : r.group - it.h0;
   if (active) {
@@ -370,7 +439,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     const uint32_t nk = (it.p1 - c0) < 64u ? (it.p1 - c0) : 64u;
     for (uint32_t kq = 0; kq < nk; kq++) {
       const uint32_t kp = c0 + kq;
-      const int b2 = tab[kp >> g.bt_shift];
+      const int b2 = __builtin_amdgcn_readlane(blk, (int)kq);  // lane kq resolved key c0 + kq's block
       const uint32_t ib = kp & bt_mask;
       const float* vrow = (const float*)(g.pool + (size_t)b2 * g.block_bytes + g.v_off + it.kvh * g.v_head +
                                          (ib >> 4) * g.v_tile) + (ib & 15u) * HDV;
@@ -390,80 +459,59 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   }
+  if (it.slot == NO_SLOT) {
 #pragma unroll
-  for (int h = 0; h < NG; h++) {
-    if (h < (int)nh) {
-      if (it.slot == NO_SLOT) {
+    for (int h = 0; h < NG; h++) {
+      if (h < (int)nh) {
         float* op = out + ((size_t)it.row * r.n_head + it.kvh * r.group + it.h0 + h) * HDV;
         const float inv = 1.0f / l[h];
 #pragma unroll
         for (int i = 0; i < ND; i++)
           if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = o[h][i] * inv;
-      } else {
-        float* pp = part + ((size_t)it.slot * r.ng + h) * (HDV + 4);
+      }
+    }
+    return;
+  }
 #pragma unroll
-        for (int i = 0; i < ND; i++)
-          if (lane + 64 * i < (uint32_t)HDV) pp[lane + 64 * i] = o[h][i];
-        if (lane == 0) {
-          pp[HDV] = m[h];
-          pp[HDV + 1] = l[h];
-        }
+  for (int h = 0; h < NG; h++) {
+    if (h < (int)nh) {
+      float* pp = part + ((size_t)it.slot * r.ng + h) * (HDV + 4);
+#pragma unroll
+      for (int i = 0; i < ND; i++)
+        if (lane + 64 * i < (uint32_t)HDV) pp[lane + 64 * i] = o[h][i];
+      if (lane == 0) {
+        pp[HDV] = m[h];
+        pp[HDV + 1] = l[h];
       }
     }
   }
-}
-
-// ---- split-K merge (forward.rs:772-806): m* = max m_s, out = sum e^(m_s-m*) o_s / sum e^(m_s-m*) l_s
-template <int HDV>
-__global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* items, uint32_t n_items,
-                                                    const float* part, float* out) {
-  constexpr int ND = (HDV + 63) / 64;
-  const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wi >= n_items * r.ng) return;
-  const MergeItem mi = items[wi / r.ng];
-  const uint32_t hq = wi % r.ng;
-  if (mi.h0 + hq >= r.group) return;
-  float M = -INFINITY;
-  for (uint32_t s = 0; s < mi.n_split; s++) M = fmaxf(M, part[((size_t)(mi.slot0 + s) * r.ng + hq) * (HDV + 4) + HDV]);
-  float L = 0.f, acc[ND];
-#pragma unroll
-  for (int i = 0; i < ND; i++) acc[i] = 0.f;
-  for (uint32_t s = 0; s < mi.n_split; s++) {
-    const float* pp = part + ((size_t)(mi.slot0 + s) * r.ng + hq) * (HDV + 4);
-    const float ms = pp[HDV];
-    if (ms == -INFINITY) continue;
-    const float c = exp2_fast(ms - M);
-    L += c * pp[HDV + 1];
-#pragma unroll
-    for (int i = 0; i < ND; i++)
-      if (lane + 64 * i < (uint32_t)HDV) acc[i] += c * pp[lane + 64 * i];
-  }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
-  float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + hq) * HDV;
-#pragma unroll
-  for (int i = 0; i < ND; i++)
-    if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = acc[i] * inv;
+  finish_split<HDV>(r, it, merges, counters, nh, part, out, lane);
 }
 
 template <int KVT, int HD, int HDV>
 hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                      const float* q, float* out, float* part, hipStream_t s) {
+                      const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
+                      hipStream_t s) {
   const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
   if constexpr (KVT == KV_F32) {
-    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
+    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, merges, counters, q,
+                       out, part);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
+    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, merges,
+                       counters, q, out, part);
   }
   return hipGetLastError();
 }
 
 template <int KVT>
 hipError_t dispatch_hd(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                       const float* q, float* out, float* part, hipStream_t s) {
-  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, s);
-  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, s);
-  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, s);
+                       const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
+                       hipStream_t s) {
+  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, merges, counters, q, out, part, s);
+  if (g.hd == 128 && g.hdv == 128)
+    return launch_one<KVT, 128, 128>(g, r, items, n_items, merges, counters, q, out, part, s);
+  if (g.hd == 256 && g.hdv == 256)
+    return launch_one<KVT, 256, 256>(g, r, items, n_items, merges, counters, q, out, part, s);
   return hipErrorInvalidValue;
 }
 
@@ -476,29 +524,16 @@ bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
 }
 
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const float* q, float* out, float* part, hipStream_t s) {
+                         const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
+                         hipStream_t s) {
   if (n_items == 0) return hipSuccess;
   switch (g.kv_type) {
-    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, s);
-    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, s);
-    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, s);
-    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, s);
+    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, merges, counters, q, out, part, s);
+    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, merges, counters, q, out, part, s);
+    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, merges, counters, q, out, part, s);
+    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, merges, counters, q, out, part, s);
   }
   return hipErrorInvalidValue;
-}
-
-hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, hipStream_t s) {
-  if (n_items == 0) return hipSuccess;
-  const uint32_t waves = n_items * r.ng;
-  const dim3 grid((waves + 3) / 4), block(256);
-  switch (hdv) {
-    case 64: hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, s, r, items, n_items, part, out); break;
-    case 128: hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, s, r, items, n_items, part, out); break;
-    case 256: hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, s, r, items, n_items, part, out); break;
-    default: return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
 }
 
 }  // namespace lmh

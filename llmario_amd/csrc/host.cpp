@@ -174,7 +174,8 @@ struct lmh_kv {
   bool table_dirty = true;
   std::vector<PageOp> pending;
   Uploader up;
-  DevBuf meta_buf, part_buf, ops_buf;
+  DevBuf meta_buf, part_buf, ops_buf, counter_buf;
+  size_t counters_zeroed = 0;  // bytes of counter_buf known to hold zeros
   // ---- per-call host scratch
   std::vector<int32_t> row_seq, row_pos;
   std::vector<DecodeItem> items;
@@ -416,12 +417,14 @@ struct lmh_kv {
     return LMH_OK;
   }
 
-  // Upload row arrays (+ optional extra payload) in one copy; returns device pointers.
-  int32_t upload_rows(hipStream_t st, const void* extra, size_t extra_bytes, const int32_t*& d_rs,
-                      const int32_t*& d_rp, const uint8_t*& d_extra) {
+  // Upload row arrays plus up to two payloads (each 256-byte aligned, back to back) in one copy;
+  // returns the device addresses of the row arrays and of the first payload.
+  int32_t upload_rows(hipStream_t st, const void* extra, size_t extra_bytes, const void* extra2, size_t extra2_bytes,
+                      const int32_t*& d_rs, const int32_t*& d_rp, const uint8_t*& d_extra) {
     const size_t nr = row_seq.size();
     const size_t rows_bytes = (nr * 8 + 255) / 256 * 256;
-    const size_t total = rows_bytes + extra_bytes;
+    const size_t extra_pad = (extra_bytes + 255) / 256 * 256;
+    const size_t total = rows_bytes + extra_pad + extra2_bytes;
     hipError_t e;
     if ((e = meta_buf.ensure(total)) != hipSuccess) return hip_fail(e, "hipMalloc");
     int idx;
@@ -430,10 +433,22 @@ struct lmh_kv {
     std::memcpy(h, row_seq.data(), nr * 4);
     std::memcpy(h + nr * 4, row_pos.data(), nr * 4);
     if (extra_bytes) std::memcpy(h + rows_bytes, extra, extra_bytes);
+    if (extra2_bytes) std::memcpy(h + rows_bytes + extra_pad, extra2, extra2_bytes);
     if ((e = up.send(idx, meta_buf.p, total, st)) != hipSuccess) return hip_fail(e, "upload");
     d_rs = (const int32_t*)meta_buf.p;
     d_rp = d_rs + nr;
     d_extra = (const uint8_t*)meta_buf.p + rows_bytes;
+    return LMH_OK;
+  }
+
+  // Split-K counters start at zero; the kernel's last arriver resets each one it used.
+  int32_t ensure_counters(size_t n, hipStream_t st) {
+    const size_t bytes = std::max<size_t>(n, 1) * 4;
+    if (counters_zeroed >= bytes) return LMH_OK;
+    hipError_t e = counter_buf.ensure(bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    if ((e = hipMemsetAsync(counter_buf.p, 0, counter_buf.cap, st)) != hipSuccess) return hip_fail(e, "counter reset");
+    counters_zeroed = counter_buf.cap;
     return LMH_OK;
   }
 
@@ -810,7 +825,7 @@ static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
   const int32_t *rs, *rp;
   const uint8_t* ex;
-  if ((rc = kv->upload_rows(st, nullptr, 0, rs, rp, ex)) != LMH_OK) return rc;
+  if ((rc = kv->upload_rows(st, nullptr, 0, nullptr, 0, rs, rp, ex)) != LMH_OK) return rc;
   const PageGeom g = kv->geom(layer);
   const LayerLayout& y = kv->layers[layer];
   hipError_t e = hipSuccess;
@@ -874,7 +889,9 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   total_tiles *= (uint64_t)y.n_kv * head_blocks;
   const uint64_t target = env_u64("LMH_DECODE_TARGET_ITEMS", 2048);
   const uint64_t min_chunk = std::max<uint64_t>(env_u64("LMH_DECODE_MIN_TILES", 8), 1);
-  const uint64_t chunk = std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / std::max<uint64_t>(target, 1));
+  // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane)
+  const uint64_t chunk = std::min<uint64_t>(
+      64, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / std::max<uint64_t>(target, 1)));
   kv->items.clear();
   kv->merges.clear();
   uint32_t slots = 0;
@@ -887,14 +904,15 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
       for (uint32_t hb = 0; hb < head_blocks; hb++) {
         if (n_split == 1) {
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT});
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, NO_SLOT, 0});
           continue;
         }
+        const uint32_t mi = (uint32_t)kv->merges.size();
         kv->merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, slots, (uint32_t)n_split, 0});
         for (uint64_t s = 0; s < n_split; s++) {
           const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
           const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++});
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++, mi, 0});
         }
       }
     }
@@ -902,15 +920,15 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
   const size_t items_bytes = kv->items.size() * sizeof(DecodeItem);
   const size_t items_pad = (items_bytes + 255) / 256 * 256;
-  std::vector<uint8_t> extra(items_pad + kv->merges.size() * sizeof(MergeItem));
-  std::memcpy(extra.data(), kv->items.data(), items_bytes);
-  if (!kv->merges.empty()) std::memcpy(extra.data() + items_pad, kv->merges.data(), kv->merges.size() * sizeof(MergeItem));
   const int32_t *rs, *rp;
   const uint8_t* ex;
-  if ((rc = kv->upload_rows(st, extra.data(), extra.size(), rs, rp, ex)) != LMH_OK) return rc;
+  if ((rc = kv->upload_rows(st, kv->items.data(), items_bytes, kv->merges.data(),
+                            kv->merges.size() * sizeof(MergeItem), rs, rp, ex)) != LMH_OK)
+    return rc;
   hipError_t e;
   if (slots > 0) {
     if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+    if ((rc = kv->ensure_counters(kv->merges.size(), st)) != LMH_OK) return rc;
   }
   const PageGeom g = kv->geom(layer);
   RowGeom r{};
@@ -922,14 +940,10 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
   if ((e = kv->time_begin(st)) != hipSuccess) return kv->hip_fail(e, "event");
-  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, st);
+  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), (const MergeItem*)(ex + items_pad),
+                    (uint32_t*)kv->counter_buf.p, q, out, (float*)kv->part_buf.p, st);
   if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
   if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
-  if (!kv->merges.empty()) {
-    e = launch_merge(r, y.hdv, (const MergeItem*)(ex + items_pad), (uint32_t)kv->merges.size(),
-                     (const float*)kv->part_buf.p, out, st);
-    if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
-  }
   return LMH_OK;
 }
 

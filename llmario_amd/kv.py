@@ -39,6 +39,8 @@ class Layer:
 
 
 def _stream_ptr(stream):
+    if isinstance(stream, C.c_void_p):
+        return stream
     if stream is None:
         import torch
         return C.c_void_p(torch.cuda.current_stream().cuda_stream)
@@ -47,7 +49,18 @@ def _stream_ptr(stream):
     return C.c_void_p(stream.cuda_stream)
 
 
+class Segments:
+    """A batch's segments packed once for the C ABI (reuse it across calls on the same batch)."""
+
+    def __init__(self, segs):
+        self.segs = [tuple(int(x) for x in s) for s in segs]
+        self.arr = (N.Seg * max(len(self.segs), 1))(*[N.Seg(*s) for s in self.segs])
+        self.n = len(self.segs)
+
+
 def _segs(segs):
+    if isinstance(segs, Segments):
+        return segs.arr, segs.n
     arr = (N.Seg * max(len(segs), 1))(*[N.Seg(*map(int, s)) for s in segs])
     return arr, len(segs)
 
