@@ -8,9 +8,8 @@
 // Work decomposition (built on the host from the batch's segments): one wave64 per work item
 // (row, KV head, contiguous key range aligned to 16-token tiles). The key range of a long row is
 // cut into several items (split-K, as attend_split does for long contexts, forward.rs:688-807);
-// their partial (o, m, l) go to `part`, and the last item of a row to finish (an atomic count per
-// row and KV head) combines them with the exact log-sum-exp merge of forward.rs:772-806, in the
-// same launch.
+// their partial (o, m, l) go to `part`, and `merge_kernel` combines them with the exact
+// log-sum-exp merge of forward.rs:772-806.
 //
 // f16 / bf16 / q8_0 pages (matrix cores): per 16-token tile,
 //   S^T[16 keys x 16 heads] = K[16 x hd] . Q^T[hd x 16]     (v_mfma_f32_16x16x32_{f16,bf16})
@@ -39,9 +38,12 @@ constexpr int WAVES = 4;  // waves (work items) per workgroup
 
 // Waves per SIMD the register allocator must allow: two tile buffers in flight per wave fit in
 // 256 VGPRs up to hd 128 (2 waves/SIMD); hd 256 needs the whole file (1 wave/SIMD).
+#ifndef LMH_DECODE_WPE
+#define LMH_DECODE_WPE 2
+#endif
 template <int HD>
 constexpr int waves_per_eu() {
-  return HD >= 256 ? 1 : 2;
+  return HD >= 256 ? 1 : LMH_DECODE_WPE;
 }
 
 __device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -123,58 +125,81 @@ __device__ inline float scale_at(const uint4* s, int r, int c) {
   return h_to_f((uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
 }
 
-// Last-arriver merge of a split-K task (forward.rs:772-806): m* = max m_s,
-// out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m kept in the log2 domain. One wave;
-// lanes over the head's dims.
+// Split-K merge (forward.rs:772-806), one wave per (task, query head), lanes over dims:
+// m* = max m_s, out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m in the log2 domain.
+// A separate launch: the kernel boundary makes every split's partials visible across XCDs.
 template <int HDV>
-__device__ void merge_task(const RowGeom& r, const MergeItem& mi, uint32_t nh, const float* part, float* out,
-                           uint32_t lane) {
+__global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* items, uint32_t n_items,
+                                                    const float* part, float* out) {
   constexpr int ND = (HDV + 63) / 64;
-  for (uint32_t h = 0; h < nh; h++) {
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < mi.n_split; s++)
-      M = fmaxf(M, part[((size_t)(mi.slot0 + s) * r.ng + h) * (HDV + 4) + HDV]);
-    float L = 0.f, acc[ND];
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wi >= n_items * r.ng) return;
+  const MergeItem mi = items[wi / r.ng];
+  const uint32_t h = wi % r.ng;
+  if (mi.h0 + h >= r.group) return;
+  static_assert(HDV % 64 == 0, "two or more dims per lane");
+  constexpr int NP = HDV / 64;  // dims per lane, loaded as one NP-wide vector
+  const size_t stride = (size_t)r.ng * (HDV + 4);
+  const float* base = part + (size_t)mi.slot0 * stride + (size_t)h * (HDV + 4);
+  float acc[NP];
 #pragma unroll
-    for (int i = 0; i < ND; i++) acc[i] = 0.f;
-    for (uint32_t s = 0; s < mi.n_split; s++) {
-      const float* pp = part + ((size_t)(mi.slot0 + s) * r.ng + h) * (HDV + 4);
-      const float ms = pp[HDV];
-      if (ms == -INFINITY) continue;
-      const float c = exp2_fast(ms - M);
-      L += c * pp[HDV + 1];
-#pragma unroll
-      for (int i = 0; i < ND; i++)
-        if (lane + 64 * i < (uint32_t)HDV) acc[i] += c * pp[lane + 64 * i];
+  for (int i = 0; i < NP; i++) acc[i] = 0.f;
+  float M = -INFINITY, L = 0.f;
+  // Up to 64 splits per round: lane s holds split s's (m, l); every lane then folds all of the
+  // round's partial rows into its NP dims (independent loads, issued together).
+  for (uint32_t s0 = 0; s0 < mi.n_split; s0 += 64) {
+    const uint32_t s = s0 + lane;
+    float ms = -INFINITY, ls = 0.f;
+    if (s < mi.n_split) {
+      const float2 ml = *(const float2*)(base + s * stride + HDV);
+      ms = ml.x;
+      ls = ml.y;
     }
-    const float inv = L > 0.f ? 1.0f / L : 0.f;
-    float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h) * HDV;
+    float Mr = ms;
+    for (int x = 32; x >= 1; x >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, x));
+    const float Mn = fmaxf(M, Mr);
+    const float rescale = M == -INFINITY ? 0.f : exp2_fast(M - Mn);
+    const float c = ms == -INFINITY ? 0.f : exp2_fast(ms - Mn);
+    float Ls = c * ls;
+    for (int x = 32; x >= 1; x >>= 1) Ls += __shfl_xor(Ls, x);
+    L = L * rescale + Ls;
 #pragma unroll
-    for (int i = 0; i < ND; i++)
-      if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = acc[i] * inv;
+    for (int i = 0; i < NP; i++) acc[i] *= rescale;
+    M = Mn;
+    const uint32_t n = (mi.n_split - s0) < 64u ? (mi.n_split - s0) : 64u;
+#pragma unroll 16
+    for (uint32_t k = 0; k < n; k++) {
+      const float ck = __shfl(c, (int)k);
+      const float* pp = base + (s0 + k) * stride + lane * NP;
+      if constexpr (NP == 1) {
+        acc[0] += ck * pp[0];
+      } else if constexpr (NP == 2) {
+        const float2 v = *(const float2*)pp;
+        acc[0] += ck * v.x;
+        acc[1] += ck * v.y;
+      } else {
+#pragma unroll
+        for (int i = 0; i < NP; i += 4) {
+          const float4 v = *(const float4*)(pp + i);
+          acc[i] += ck * v.x;
+          acc[i + 1] += ck * v.y;
+          acc[i + 2] += ck * v.z;
+          acc[i + 3] += ck * v.w;
+        }
+      }
+    }
   }
-}
-
-// A split item has written its partials: count it off on its task's counter (release), and if it
-// is the last of the task, acquire everyone's partials, reset the counter and merge.
-template <int HDV>
-__device__ void finish_split(const RowGeom& r, const DecodeItem& it, const MergeItem* merges, uint32_t* counters,
-                             uint32_t nh, const float* part, float* out, uint32_t lane) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  uint32_t prev = 0;
-  if (lane == 0) prev = __hip_atomic_fetch_add(counters + it.merge, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  prev = __shfl(prev, 0);
-  const MergeItem mi = merges[it.merge];
-  if (prev + 1 != mi.n_split) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  if (lane == 0) __hip_atomic_store(counters + it.merge, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  merge_task<HDV>(r, mi, nh, part, out, lane);
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h) * HDV + lane * NP;
+#pragma unroll
+  for (int i = 0; i < NP; i++) op[i] = acc[i] * inv;
 }
 
 template <int KVT, int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD>(), waves_per_eu<HD>())))
-void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const MergeItem* merges,
-                        uint32_t* counters, const float* q, float* out, float* part) {
+void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q, float* out,
+                        float* part) {
   constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
   constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
   using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
@@ -182,7 +207,7 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
   const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
   if (wi >= n_items) return;
   const DecodeItem it = items[wi];
-  const int seq = r.row_seq[it.row];
+  const int seq = (int)it.seq;
   const int32_t* tab = g.table + (size_t)seq * g.bps;
   const uint32_t hq = lane & 15u, grp = lane >> 4;
   const bool hv = hq < r.ng && it.h0 + hq < r.group;
@@ -353,15 +378,12 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
       pp[HDV + 1] = lsum;
     }
   }
-  const uint32_t nh = (it.h0 + r.ng <= r.group) ? r.ng : r.group - it.h0;
-  finish_split<HDV>(r, it, merges, counters, nh, part, out, lane);
 }
 
 // ---- f32 pages: VALU path ----------------------------------------------------------------------
 template <int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
-                                                                uint32_t n_items, const MergeItem* merges,
-                                                                uint32_t* counters, const float* q, float* out,
+                                                                uint32_t n_items, const float* q, float* out,
                                                                 float* part) {
   constexpr int NG = 16;
   constexpr int ND = HDV / 64 > 0 ? HDV / 64 : 1;  // dims per lane in P.V
@@ -370,7 +392,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t wi = blockIdx.x * WAVES + w;
   const bool active = wi < n_items;
-  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, NO_SLOT, 0};
+  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, 0, 0};
   const uint32_t ng = r.ng;
   const uint32_t nh = (it.h0 + ng <= r.group) ? ng : r.group - it.h0;
   if (active) {
@@ -381,7 +403,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
   }
   __syncthreads();
   if (!active) return;
-  const int seq = r.row_seq[it.row];
+  const int seq = (int)it.seq;
   const int32_t* tab = g.table + (size_t)seq * g.bps;
   const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
   float m[NG], l[NG], o[NG][ND];
@@ -485,33 +507,26 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
       }
     }
   }
-  finish_split<HDV>(r, it, merges, counters, nh, part, out, lane);
 }
 
 template <int KVT, int HD, int HDV>
 hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                      const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
-                      hipStream_t s) {
+                      const float* q, float* out, float* part, hipStream_t s) {
   const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
   if constexpr (KVT == KV_F32) {
-    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, merges, counters, q,
-                       out, part);
+    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, merges,
-                       counters, q, out, part);
+    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
   }
   return hipGetLastError();
 }
 
 template <int KVT>
 hipError_t dispatch_hd(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                       const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
-                       hipStream_t s) {
-  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, merges, counters, q, out, part, s);
-  if (g.hd == 128 && g.hdv == 128)
-    return launch_one<KVT, 128, 128>(g, r, items, n_items, merges, counters, q, out, part, s);
-  if (g.hd == 256 && g.hdv == 256)
-    return launch_one<KVT, 256, 256>(g, r, items, n_items, merges, counters, q, out, part, s);
+                       const float* q, float* out, float* part, hipStream_t s) {
+  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, s);
+  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, s);
+  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, s);
   return hipErrorInvalidValue;
 }
 
@@ -524,16 +539,29 @@ bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
 }
 
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
-                         hipStream_t s) {
+                         const float* q, float* out, float* part, hipStream_t s) {
   if (n_items == 0) return hipSuccess;
   switch (g.kv_type) {
-    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, merges, counters, q, out, part, s);
-    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, merges, counters, q, out, part, s);
-    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, merges, counters, q, out, part, s);
-    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, merges, counters, q, out, part, s);
+    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, s);
+    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, s);
+    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, s);
+    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, s);
   }
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
+                        float* out, hipStream_t s) {
+  if (n_items == 0) return hipSuccess;
+  const uint32_t waves = n_items * r.ng;
+  const dim3 grid((waves + 3) / 4), block(256);
+  switch (hdv) {
+    case 64: hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 128: hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 256: hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, s, r, items, n_items, part, out); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace lmh

@@ -69,14 +69,12 @@ struct DecodeItem {
   uint32_t h0;
   uint32_t p0, p1;
   uint32_t slot;
-  uint32_t merge;  // index of this item's MergeItem (split-K) or NO_SLOT
-  uint32_t pad;
+  uint32_t seq;  // the row's sequence (saves a dependent read of the row arrays)
+  uint32_t pad;  // 32-byte items
 };
 constexpr uint32_t NO_SLOT = 0xffffffffu;
 
-// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..). The
-// split items of one merge count themselves off on counters[merge]; the last one to finish merges
-// (and resets the counter to zero for the next call).
+// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..).
 struct MergeItem {
   uint32_t row;
   uint32_t kvh;
@@ -110,8 +108,9 @@ hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t
                               hipStream_t s);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const MergeItem* merges, uint32_t* counters, const float* q, float* out, float* part,
-                         hipStream_t s);
+                         const float* q, float* out, float* part, hipStream_t s);
+hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
+                        float* out, hipStream_t s);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 
 }  // namespace lmh

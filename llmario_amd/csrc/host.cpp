@@ -10,7 +10,8 @@
 //   forward_batch checks crates/engine/model/src/forward.rs:207-291
 // The device side is this backend's own: one hipMalloc'd pool of pool_blocks x block_bytes,
 // an int32 block table [n_seqs][blocks_per_seq] mirrored to the device when it changes, and a
-// per-call packed work list (decode items, split-K slots, merges) uploaded from pinned memory.
+// per-call packed work list (decode items, split-K slots, merges) that the kernels read straight
+// from pinned, device-mapped host memory (no copy on the stream ahead of them).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -60,9 +61,10 @@ uint32_t tile_bytes(uint32_t t, uint32_t dim) {
 }
 uint32_t tile_scale_bytes(uint32_t t, uint32_t dim) { return t == LMH_KV_Q8_0 ? 16 * (dim / 32) * 2 : 0; }
 
-struct Uploader {  // pinned staging ring -> device, stream ordered
+struct Uploader {  // ring of pinned, device-mapped staging slots, reused once their event has passed
   static constexpr int N = 4;
   uint8_t* host[N] = {};
+  uint8_t* dev[N] = {};  // the device address of host[i]
   size_t cap[N] = {};
   hipEvent_t ev[N] = {};
   bool used[N] = {};
@@ -92,21 +94,26 @@ struct Uploader {  // pinned staging ring -> device, stream ordered
       if (host[idx]) (void)hipHostFree(host[idx]);
       host[idx] = nullptr;
       size_t c = std::max<size_t>(bytes, 1 << 16);
-      if ((e = hipHostMalloc((void**)&host[idx], c, hipHostMallocDefault)) != hipSuccess) {
+      if ((e = hipHostMalloc((void**)&host[idx], c, hipHostMallocMapped | hipHostMallocCoherent)) != hipSuccess) {
         cap[idx] = 0;
         return e;
       }
+      if ((e = hipHostGetDevicePointer((void**)&dev[idx], host[idx], 0)) != hipSuccess) return e;
       cap[idx] = c;
     }
     ptr = host[idx];
     return hipSuccess;
   }
+  // The slot's contents are in use by work enqueued on `s` so far.
+  hipError_t mark(int idx, hipStream_t s) {
+    hipError_t e = hipEventRecord(ev[idx], s);
+    used[idx] = e == hipSuccess;
+    return e;
+  }
   hipError_t send(int idx, void* dst, size_t bytes, hipStream_t s) {
     hipError_t e = hipMemcpyAsync(dst, host[idx], bytes, hipMemcpyHostToDevice, s);
     if (e != hipSuccess) return e;
-    e = hipEventRecord(ev[idx], s);
-    used[idx] = e == hipSuccess;
-    return e;
+    return mark(idx, s);
   }
 };
 
@@ -174,8 +181,7 @@ struct lmh_kv {
   bool table_dirty = true;
   std::vector<PageOp> pending;
   Uploader up;
-  DevBuf meta_buf, part_buf, ops_buf, counter_buf;
-  size_t counters_zeroed = 0;  // bytes of counter_buf known to hold zeros
+  DevBuf part_buf, ops_buf;
   // ---- per-call host scratch
   std::vector<int32_t> row_seq, row_pos;
   std::vector<DecodeItem> items;
@@ -417,39 +423,32 @@ struct lmh_kv {
     return LMH_OK;
   }
 
-  // Upload row arrays plus up to two payloads (each 256-byte aligned, back to back) in one copy;
-  // returns the device addresses of the row arrays and of the first payload.
-  int32_t upload_rows(hipStream_t st, const void* extra, size_t extra_bytes, const void* extra2, size_t extra2_bytes,
-                      const int32_t*& d_rs, const int32_t*& d_rp, const uint8_t*& d_extra) {
+  // Stage row arrays plus up to two payloads (each 256-byte aligned, back to back) in a pinned,
+  // device-mapped staging slot: the kernels read this per-call metadata straight from host memory
+  // (a few dozen bytes per wave), so no copy has to run on the stream before them. The caller
+  // enqueues every kernel that reads the slot, then calls release_rows(slot, stream).
+  int32_t stage_rows(const void* extra, size_t extra_bytes, const void* extra2, size_t extra2_bytes,
+                     const int32_t*& d_rs, const int32_t*& d_rp, const uint8_t*& d_extra, int& slot) {
     const size_t nr = row_seq.size();
     const size_t rows_bytes = (nr * 8 + 255) / 256 * 256;
     const size_t extra_pad = (extra_bytes + 255) / 256 * 256;
     const size_t total = rows_bytes + extra_pad + extra2_bytes;
     hipError_t e;
-    if ((e = meta_buf.ensure(total)) != hipSuccess) return hip_fail(e, "hipMalloc");
-    int idx;
     uint8_t* h;
-    if ((e = up.acquire(total, idx, h)) != hipSuccess) return hip_fail(e, "staging");
+    if ((e = up.acquire(total, slot, h)) != hipSuccess) return hip_fail(e, "staging");
     std::memcpy(h, row_seq.data(), nr * 4);
     std::memcpy(h + nr * 4, row_pos.data(), nr * 4);
     if (extra_bytes) std::memcpy(h + rows_bytes, extra, extra_bytes);
     if (extra2_bytes) std::memcpy(h + rows_bytes + extra_pad, extra2, extra2_bytes);
-    if ((e = up.send(idx, meta_buf.p, total, st)) != hipSuccess) return hip_fail(e, "upload");
-    d_rs = (const int32_t*)meta_buf.p;
+    uint8_t* d = up.dev[slot];
+    d_rs = (const int32_t*)d;
     d_rp = d_rs + nr;
-    d_extra = (const uint8_t*)meta_buf.p + rows_bytes;
+    d_extra = d + rows_bytes;
     return LMH_OK;
   }
-
-  // Split-K counters start at zero; the kernel's last arriver resets each one it used.
-  int32_t ensure_counters(size_t n, hipStream_t st) {
-    const size_t bytes = std::max<size_t>(n, 1) * 4;
-    if (counters_zeroed >= bytes) return LMH_OK;
-    hipError_t e = counter_buf.ensure(bytes);
-    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
-    if ((e = hipMemsetAsync(counter_buf.p, 0, counter_buf.cap, st)) != hipSuccess) return hip_fail(e, "counter reset");
-    counters_zeroed = counter_buf.cap;
-    return LMH_OK;
+  int32_t release_rows(int slot, hipStream_t st) {
+    hipError_t e = up.mark(slot, st);
+    return e == hipSuccess ? LMH_OK : hip_fail(e, "event");
   }
 
   hipError_t time_begin(hipStream_t st) {
@@ -825,7 +824,8 @@ static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
   const int32_t *rs, *rp;
   const uint8_t* ex;
-  if ((rc = kv->upload_rows(st, nullptr, 0, nullptr, 0, rs, rp, ex)) != LMH_OK) return rc;
+  int slot;
+  if ((rc = kv->stage_rows(nullptr, 0, nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
   const PageGeom g = kv->geom(layer);
   const LayerLayout& y = kv->layers[layer];
   hipError_t e = hipSuccess;
@@ -842,7 +842,7 @@ static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n
       break;
   }
   if (e != hipSuccess) return kv->hip_fail(e, "kernel launch");
-  return LMH_OK;
+  return kv->release_rows(slot, st);
 }
 
 int32_t lmh_kv_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* k, const float* v,
@@ -904,15 +904,14 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
       for (uint32_t hb = 0; hb < head_blocks; hb++) {
         if (n_split == 1) {
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, NO_SLOT, 0});
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, (uint32_t)kv->row_seq[t], 0});
           continue;
         }
-        const uint32_t mi = (uint32_t)kv->merges.size();
         kv->merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, slots, (uint32_t)n_split, 0});
         for (uint64_t s = 0; s < n_split; s++) {
           const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
           const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++, mi, 0});
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++, (uint32_t)kv->row_seq[t], 0});
         }
       }
     }
@@ -922,13 +921,13 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   const size_t items_pad = (items_bytes + 255) / 256 * 256;
   const int32_t *rs, *rp;
   const uint8_t* ex;
-  if ((rc = kv->upload_rows(st, kv->items.data(), items_bytes, kv->merges.data(),
-                            kv->merges.size() * sizeof(MergeItem), rs, rp, ex)) != LMH_OK)
+  int slot;
+  if ((rc = kv->stage_rows(kv->items.data(), items_bytes, kv->merges.data(), kv->merges.size() * sizeof(MergeItem),
+                           rs, rp, ex, slot)) != LMH_OK)
     return rc;
   hipError_t e;
   if (slots > 0) {
     if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
-    if ((rc = kv->ensure_counters(kv->merges.size(), st)) != LMH_OK) return rc;
   }
   const PageGeom g = kv->geom(layer);
   RowGeom r{};
@@ -940,11 +939,15 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
   if ((e = kv->time_begin(st)) != hipSuccess) return kv->hip_fail(e, "event");
-  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), (const MergeItem*)(ex + items_pad),
-                    (uint32_t*)kv->counter_buf.p, q, out, (float*)kv->part_buf.p, st);
+  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, st);
   if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
   if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
-  return LMH_OK;
+  if (!kv->merges.empty()) {
+    e = launch_merge(r, y.hdv, (const MergeItem*)(ex + items_pad), (uint32_t)kv->merges.size(),
+                     (const float*)kv->part_buf.p, out, st);
+    if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
+  }
+  return kv->release_rows(slot, st);
 }
 
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
