@@ -56,7 +56,7 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
     for _ in range(warmup):
         hc.attend(0, segs, q, out, w.scale, w.window, sp)
     torch.cuda.synchronize()
-    hc.kernel_time()  # reset
+    hc.kernel_times()  # reset
     hc.set_timing(timing_kernel)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
@@ -68,12 +68,16 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     hc.set_timing(False)
-    k_ms, launches = hc.kernel_time()
+    kt = hc.kernel_times()
     ms_step = max(wall * 1e3 / steps, ev0.elapsed_time(ev1) / steps)
-    k_avg = k_ms / max(launches, 1)
+    per_kind = {k: (ms / n if n else 0.0) for k, (ms, n) in kt.items()}
+    # the dominant kernel: prefill when the step has multi-token segments, else decode
+    main = "prefill" if per_kind["prefill"] > 0 else "decode"
+    k_avg = per_kind[main]
     res = {
         "config": name, "kv_type": w.kv_type, "rows": w.n_rows, "ms_per_step": ms_step,
-        "kernel_ms": k_avg, "bytes": w.algorithmic_bytes(), "flops": w.flops(),
+        "kernel": main, "kernel_ms": k_avg, "decode_ms": per_kind["decode"], "prefill_ms": per_kind["prefill"],
+        "merge_ms": per_kind["merge"], "bytes": w.algorithmic_bytes(), "flops": w.flops(),
     }
     res["GBps"] = res["bytes"] / (ms_step * 1e-3) / 1e9
     res["TFLOPs"] = res["flops"] / (ms_step * 1e-3) / 1e12

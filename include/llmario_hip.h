@@ -166,11 +166,14 @@ int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, u
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
-/* Timing hook for benchmarks: when enabled, lmh_attend brackets its main attention kernel with
- * HIP events on `stream`; lmh_kv_kernel_time returns the accumulated milliseconds and launch
- * count since the last reset (synchronizes on the recorded events). */
+/* Timing hook for benchmarks: when enabled, lmh_attend brackets each kernel it launches with HIP
+ * events on `stream`; lmh_kv_kernel_time returns the accumulated milliseconds and launch count of
+ * one kernel kind since its last read, and resets them (it waits for the recorded events). */
+#define LMH_KERNEL_DECODE 0u
+#define LMH_KERNEL_PREFILL 1u
+#define LMH_KERNEL_MERGE 2u
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
-int32_t lmh_kv_kernel_time(lmh_kv* kv, double* ms, uint64_t* launches);
+int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches);
 
 #ifdef __cplusplus
 }

@@ -75,8 +75,10 @@ SIGNATURES = {
     "lmh_kv_gather_encoded": (i32, [P, u32, P, u64, P, P, P]),
     "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
     "lmh_kv_set_timing": (i32, [P, i32]),
-    "lmh_kv_kernel_time": (i32, [P, C.POINTER(C.c_double), C.POINTER(u64)]),
+    "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
 }
+
+KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE = 0, 1, 2
 
 _lib = None
 

@@ -93,6 +93,23 @@ struct RowGeom {
   uint32_t window;         // 0 = none
 };
 
+// One prefill work unit: KV head `kvh` of sequence `seq`, tokens at positions pos0 .. pos0+n_tok-1
+// which are stacked rows row0 .. row0+n_tok-1 (n_tok * group <= prefill_cols_per_unit()).
+struct PrefillItem {
+  uint32_t seq;
+  uint32_t kvh;
+  uint32_t row0;
+  uint32_t pos0;
+  uint32_t n_tok;
+  uint32_t pad0, pad1, pad2;
+};
+
+struct PrefillGeom {
+  uint32_t n_head, group;
+  float scale_log2;  // scale * log2(e)
+  uint32_t window;   // 0 = none
+};
+
 // Launch wrappers (defined in the .hip files). Return hipSuccess or the launch error.
 hipError_t launch_store_f32(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
                             const float* k, const float* v, hipStream_t s);
@@ -112,5 +129,12 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
                         float* out, hipStream_t s);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
+
+// Prefill (multi-token segments on matrix cores). `max_pages` bounds the key pages of any item.
+hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_items,
+                          uint32_t max_pages, const float* q, float* out, hipStream_t s);
+bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group);
+uint32_t prefill_cols_per_unit();
+size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages);
 
 }  // namespace lmh

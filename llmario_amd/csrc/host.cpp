@@ -189,9 +189,12 @@ struct lmh_kv {
   // ---- timing
   bool timing = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
+  std::vector<uint32_t> ev_kind;
   size_t ev_used = 0;
-  double acc_ms = 0;
-  uint64_t launches = 0;
+  double acc_ms[3] = {0, 0, 0};
+  uint64_t launches[3] = {0, 0, 0};
+  std::vector<PrefillItem> pitems;
+  std::vector<uint8_t> payload;
   std::string err;
 
   ~lmh_kv() {
@@ -451,14 +454,18 @@ struct lmh_kv {
     return e == hipSuccess ? LMH_OK : hip_fail(e, "event");
   }
 
-  hipError_t time_begin(hipStream_t st) {
+  // Event pairs around one kernel launch of kind LMH_KERNEL_* (timing hook for benchmarks).
+  hipError_t time_begin(hipStream_t st, uint32_t kind) {
     if (!timing) return hipSuccess;
     if (ev_used == evs.size()) {
       hipEvent_t a, b;
-      (void)hipEventCreate(&a);
-      (void)hipEventCreate(&b);
+      hipError_t e = hipEventCreate(&a);
+      if (e == hipSuccess) e = hipEventCreate(&b);
+      if (e != hipSuccess) return e;
       evs.push_back({a, b});
+      ev_kind.push_back(0);
     }
+    ev_kind[ev_used] = kind;
     return hipEventRecord(evs[ev_used].first, st);
   }
   hipError_t time_end(hipStream_t st) {
@@ -466,6 +473,19 @@ struct lmh_kv {
     hipError_t e = hipEventRecord(evs[ev_used].second, st);
     ev_used++;
     return e;
+  }
+  // Fold recorded pairs into the per-kind totals.
+  hipError_t collect_times() {
+    for (size_t i = 0; i < ev_used; i++) {
+      float t = 0;
+      hipError_t e = hipEventSynchronize(evs[i].second);
+      if (e == hipSuccess) e = hipEventElapsedTime(&t, evs[i].first, evs[i].second);
+      if (e != hipSuccess) return e;
+      acc_ms[ev_kind[i]] += t;
+      launches[ev_kind[i]]++;
+    }
+    ev_used = 0;
+    return hipSuccess;
   }
 };
 
@@ -878,10 +898,46 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   const uint32_t head_blocks = (group + ng - 1) / ng;
   hipStream_t st = (hipStream_t)stream;
 
-  // ---- work list: per (row, KV head, head block), the key range [lo, pos] cut into chunks of
-  // whole 16-token tiles, spread evenly; rows whose range fits one chunk write the output.
+  // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
+  // in units of up to prefill_cols_per_unit()/group tokens per KV head, heaviest first.
+  const uint64_t pf_min = env_u64("LMH_PREFILL_MIN_ROWS", 16);
+  const bool pf_ok = prefill_supported(kv->kv_type, y.hd, y.hdv, group);
+  std::vector<uint8_t> decode_row(n_rows, 1);
+  kv->pitems.clear();
+  uint32_t max_pages = 0;
+  if (pf_ok) {
+    const uint32_t unit_tok = prefill_cols_per_unit() / group;
+    for (uint64_t i = 0; i < n_segs; i++) {
+      const lmh_seg& sg = segs[i];
+      if (sg.n < pf_min) continue;
+      for (uint64_t u = 0; u < sg.n; u += unit_tok) {
+        const uint32_t n_tok = (uint32_t)std::min<uint64_t>(unit_tok, sg.n - u);
+        const uint64_t pos0 = sg.pos0 + u, last = pos0 + n_tok - 1;
+        const uint64_t lo = (window > 0 && pos0 + 1 > window) ? pos0 + 1 - window : 0;
+        max_pages = std::max<uint32_t>(max_pages, (uint32_t)(last / 16 - lo / 16 + 1));
+        for (uint32_t kvh = 0; kvh < y.n_kv; kvh++)
+          kv->pitems.push_back(PrefillItem{(uint32_t)sg.seq, kvh, (uint32_t)(sg.start + u), (uint32_t)pos0, n_tok, 0, 0, 0});
+      }
+      for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
+    }
+    // longest key ranges first, so the short causal units fill in behind them
+    std::stable_sort(kv->pitems.begin(), kv->pitems.end(), [&](const PrefillItem& a, const PrefillItem& b) {
+      const uint64_t la = a.pos0 + a.n_tok, lb = b.pos0 + b.n_tok;
+      return la > lb;
+    });
+    if (prefill_lds_bytes(y.hd, max_pages) > 160 * 1024) {
+      // key ranges too long to list in LDS: those segments go through the decode kernel
+      kv->pitems.clear();
+      std::fill(decode_row.begin(), decode_row.end(), 1);
+      max_pages = 0;
+    }
+  }
+
+  // ---- decode work list: per (row, KV head, head block), the key range [lo, pos] cut into
+  // chunks of whole 16-token tiles, spread evenly; rows whose range fits one chunk write the output.
   uint64_t total_tiles = 0;
   for (uint64_t t = 0; t < n_rows; t++) {
+    if (!decode_row[t]) continue;
     const uint64_t pos = (uint64_t)kv->row_pos[t];
     const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
     total_tiles += pos / 16 - lo / 16 + 1;
@@ -896,6 +952,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   kv->merges.clear();
   uint32_t slots = 0;
   for (uint64_t t = 0; t < n_rows; t++) {
+    if (!decode_row[t]) continue;
     const uint64_t pos = (uint64_t)kv->row_pos[t];
     const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
     const uint64_t hi = pos + 1;
@@ -919,13 +976,32 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
   const size_t items_bytes = kv->items.size() * sizeof(DecodeItem);
   const size_t items_pad = (items_bytes + 255) / 256 * 256;
+  const size_t merges_bytes = kv->merges.size() * sizeof(MergeItem);
+  const size_t merges_pad = (merges_bytes + 255) / 256 * 256;
+  // one staged payload: [decode items | merges | prefill items]
+  kv->payload.resize(items_pad + merges_pad + kv->pitems.size() * sizeof(PrefillItem));
+  if (items_bytes) std::memcpy(kv->payload.data(), kv->items.data(), items_bytes);
+  if (merges_bytes) std::memcpy(kv->payload.data() + items_pad, kv->merges.data(), merges_bytes);
+  if (!kv->pitems.empty())
+    std::memcpy(kv->payload.data() + items_pad + merges_pad, kv->pitems.data(), kv->pitems.size() * sizeof(PrefillItem));
   const int32_t *rs, *rp;
   const uint8_t* ex;
   int slot;
-  if ((rc = kv->stage_rows(kv->items.data(), items_bytes, kv->merges.data(), kv->merges.size() * sizeof(MergeItem),
-                           rs, rp, ex, slot)) != LMH_OK)
-    return rc;
+  if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
   hipError_t e;
+  if (!kv->pitems.empty()) {
+    PrefillGeom pg{};
+    pg.n_head = y.n_head;
+    pg.group = group;
+    pg.scale_log2 = scale * 1.4426950408889634f;
+    pg.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
+    if ((e = kv->time_begin(st, LMH_KERNEL_PREFILL)) != hipSuccess) return kv->hip_fail(e, "event");
+    e = launch_prefill(kv->geom(layer), pg, (const PrefillItem*)(ex + items_pad + merges_pad),
+                       (uint32_t)kv->pitems.size(), max_pages, q, out, st);
+    if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
+    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  }
+  if (kv->items.empty()) return kv->release_rows(slot, st);
   if (slots > 0) {
     if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
   }
@@ -938,14 +1014,16 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   r.ng = ng;
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
-  if ((e = kv->time_begin(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  if ((e = kv->time_begin(st, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
   e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, st);
   if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
   if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   if (!kv->merges.empty()) {
+    if ((e = kv->time_begin(st, LMH_KERNEL_MERGE)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_merge(r, y.hdv, (const MergeItem*)(ex + items_pad), (uint32_t)kv->merges.size(),
                      (const float*)kv->part_buf.p, out, st);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
+    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   return kv->release_rows(slot, st);
 }
@@ -956,21 +1034,14 @@ int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
   return LMH_OK;
 }
 
-int32_t lmh_kv_kernel_time(lmh_kv* kv, double* ms, uint64_t* launches) {
-  if (!kv) return LMH_INVALID_ARGUMENT;
-  for (size_t i = 0; i < kv->ev_used; i++) {
-    float t = 0;
-    hipError_t e = hipEventSynchronize(kv->evs[i].second);
-    if (e == hipSuccess) e = hipEventElapsedTime(&t, kv->evs[i].first, kv->evs[i].second);
-    if (e != hipSuccess) return kv->hip_fail(e, "event timing");
-    kv->acc_ms += t;
-    kv->launches++;
-  }
-  kv->ev_used = 0;
-  if (ms) *ms = kv->acc_ms;
-  if (launches) *launches = kv->launches;
-  kv->acc_ms = 0;
-  kv->launches = 0;
+int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches) {
+  if (!kv || kernel > LMH_KERNEL_MERGE) return LMH_INVALID_ARGUMENT;
+  hipError_t e = kv->collect_times();
+  if (e != hipSuccess) return kv->hip_fail(e, "event timing");
+  if (ms) *ms = kv->acc_ms[kernel];
+  if (launches) *launches = kv->launches[kernel];
+  kv->acc_ms[kernel] = 0;
+  kv->launches[kernel] = 0;
   return LMH_OK;
 }
 

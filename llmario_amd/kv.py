@@ -217,8 +217,13 @@ class HipKvCache:
     def set_timing(self, on: bool):
         self._check(N.lib().lmh_kv_set_timing(self.h, 1 if on else 0))
 
-    def kernel_time(self):
-        """(milliseconds, launches) of the attention kernel since the last call."""
+    def kernel_time(self, kernel: str = "decode"):
+        """(milliseconds, launches) of one kernel kind ("decode" | "prefill" | "merge") since its
+        last read (needs set_timing(True) while the calls ran)."""
+        kind = {"decode": N.KERNEL_DECODE, "prefill": N.KERNEL_PREFILL, "merge": N.KERNEL_MERGE}[kernel]
         ms, n = C.c_double(), N.u64()
-        self._check(N.lib().lmh_kv_kernel_time(self.h, C.byref(ms), C.byref(n)))
+        self._check(N.lib().lmh_kv_kernel_time(self.h, kind, C.byref(ms), C.byref(n)))
         return ms.value, n.value
+
+    def kernel_times(self) -> dict:
+        return {k: self.kernel_time(k) for k in ("decode", "prefill", "merge")}

@@ -155,6 +155,13 @@ SMALL = [
     ("q8_0", Layer(16, 2, 64, 64), [300, 5], [1, 3], 0, 64),
     ("f16", Layer(32, 32, 64, 64), [250, 1], [1, 1], 0, 16),
     ("f16", Layer(64, 2, 256, 256), [700], [2], 0, 16),
+    # multi-token segments: the matrix-core prefill path (16+ rows)
+    ("bf16", Layer(32, 8, 128, 128), [0, 7, 300], [300, 70, 16], 0, 16),
+    ("f16", Layer(8, 8, 128, 128), [3], [200], 0, 32),
+    ("f16", Layer(64, 8, 128, 128), [40, 0], [90, 33], 0, 16),
+    ("bf16", Layer(16, 1, 64, 64), [500], [45], 0, 64),
+    ("f16", Layer(40, 8, 128, 128), [600, 20], [130, 1], 37, 16),
+    ("bf16", Layer(32, 8, 128, 128), [1000], [260], 300, 16),
 ]
 
 
