@@ -831,6 +831,14 @@ int32_t lmh_batch_commit(lmh_kv* kv, const lmh_seg* segs, uint64_t n_segs) {
   return LMH_OK;
 }
 
+// Launch order of the prefill units: longest key ranges first, so the short causal units fill in
+// behind them.
+static void order_prefill_units(std::vector<PrefillItem>& items) {
+  std::stable_sort(items.begin(), items.end(), [](const PrefillItem& a, const PrefillItem& b) {
+    return a.pos0 + a.n_tok > b.pos0 + b.n_tok;
+  });
+}
+
 static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const void* a, const void* b,
                      void* stream, int mode) {
   if (!kv) return LMH_INVALID_ARGUMENT;
@@ -901,7 +909,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
   // in units of up to prefill_cols_per_unit()/group tokens per KV head, heaviest first.
   const uint64_t pf_min = env_u64("LMH_PREFILL_MIN_ROWS", 16);
-  const bool pf_ok = prefill_supported(kv->kv_type, y.hd, y.hdv, group);
+  const bool pf_ok = scale > 0.f && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
   std::vector<uint8_t> decode_row(n_rows, 1);
   kv->pitems.clear();
   uint32_t max_pages = 0;
@@ -920,11 +928,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
       }
       for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
     }
-    // longest key ranges first, so the short causal units fill in behind them
-    std::stable_sort(kv->pitems.begin(), kv->pitems.end(), [&](const PrefillItem& a, const PrefillItem& b) {
-      const uint64_t la = a.pos0 + a.n_tok, lb = b.pos0 + b.n_tok;
-      return la > lb;
-    });
+    order_prefill_units(kv->pitems);
     if (prefill_lds_bytes(y.hd, max_pages) > 160 * 1024) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
       kv->pitems.clear();
