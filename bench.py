@@ -150,6 +150,9 @@ def main():
     ap.add_argument("--extra", default="c1,c3,c4,c5,c5w", help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-config", default="",
+                    help="only time this one config (c1..c5, c5w) and print its result dict: the "
+                         "command the rocprofv3 summaries under profiles/ were taken with")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (20 launches): the known-size "
                          "kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE readings")
@@ -173,6 +176,10 @@ def main():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.profile_config:
+        res = time_config(args.profile_config, args.steps, args.warmup)
+        print(json.dumps(res), flush=True)
+        return
 
     head = time_config("c2", args.steps, args.warmup)
     extra = {}

@@ -15,6 +15,7 @@ from conftest import TOL, row_rel_err
 from llmario_amd import harness
 from llmario_amd.kv import HipKvCache, KvFull, Layer
 from llmario_amd.workloads import Generator, config, small
+from golden_io import load as load_golden, names as golden_names
 
 pytestmark = pytest.mark.gpu
 
@@ -206,3 +207,40 @@ def test_attend_config_sampled_rows(cuda, name):
     err = row_rel_err(got[rows], ref)
     print(f"{name}: {len(rows)} sampled rows, max row rel err {err:.3e} (tol {TOL[w.kv_type]})")
     assert err <= TOL[w.kv_type], err
+
+
+# ---- committed golden fixtures ----------------------------------------------------------------
+
+@pytest.mark.parametrize("name", golden_names())
+@pytest.mark.parametrize("split", ["auto", "forced"])
+def test_golden_fixture(cuda, monkeypatch, name, split):
+    """The fixture's encoded rows stored through the C ABI come back byte for byte, and attention
+    over them matches the fixture's expected outputs (oracle and float64) within tolerance."""
+    import torch
+    if split == "forced":
+        monkeypatch.setenv("LMH_DECODE_MIN_TILES", "1")
+        monkeypatch.setenv("LMH_DECODE_TARGET_ITEMS", "100000")
+    f = load_golden(name)
+    L = Layer(*f.layer)
+    hc = HipKvCache([L], max_ctx=f.max_ctx, n_seqs=len(f.prior), kv_type=f.kv_type,
+                    block_tokens=f.block_tokens, pool_tokens=f.pool_tokens)
+    for s in range(len(f.prior)):
+        hc.adopt_blocks(s, f.tables[s])
+        n = f.k_rows[s].shape[0]
+        seg = [(s, 0, n, 0)]
+        kr = torch.from_numpy(np.ascontiguousarray(f.k_rows[s])).cuda()
+        vr = torch.from_numpy(np.ascontiguousarray(f.v_rows[s])).cuda()
+        hc.store_encoded(0, seg, kr, vr)
+        kb, vb = torch.zeros_like(kr), torch.zeros_like(vr)
+        hc.gather_encoded(0, seg, kb, vb)
+        torch.cuda.synchronize()
+        assert np.array_equal(kb.cpu().numpy(), f.k_rows[s]) and np.array_equal(vb.cpu().numpy(), f.v_rows[s])
+        hc.set_len(s, f.prior[s])
+    n_rows = sum(sg[2] for sg in f.segs)
+    out = torch.full((n_rows, L.n_head, L.hdv), float("nan"), device="cuda")
+    hc.attend(0, f.segs, torch.from_numpy(f.q).cuda(), out, f.scale, f.window)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    e1, e2 = row_rel_err(got, f.out), row_rel_err(got, f.out_f64)
+    print(f"{name} split={split}: vs oracle {e1:.3e}, vs f64 {e2:.3e}")
+    assert e1 <= TOL[f.kv_type] and e2 <= TOL[f.kv_type], (e1, e2)
