@@ -128,6 +128,8 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
                          const float* q, float* out, float* part, hipStream_t s);
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
                         float* out, hipStream_t s);
+// Decode work items (waves) one CU holds at once for a layer's decode kernel (occupancy query).
+uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 
 // Prefill (multi-token segments on matrix cores). `max_pages` bounds the key pages of any item.

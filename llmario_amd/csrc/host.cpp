@@ -175,6 +175,8 @@ struct lmh_kv {
   std::vector<Seq> seqs;
   // ---- device
   int device = 0;
+  uint32_t n_cu = 0;                        // compute units of the device
+  std::vector<uint32_t> decode_capacity;    // per layer: decode items resident at once (0 = not yet asked)
   uint8_t* d_pool = nullptr;
   int32_t* d_table = nullptr;
   std::vector<int32_t> h_table;
@@ -614,6 +616,10 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   kv->h_table.assign(kv->n_seqs * kv->bps, -1);
   kv->device = o->device;
   hipError_t e = hipSetDevice(o->device);
+  int n_cu = 0;
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, o->device);
+  kv->n_cu = (uint32_t)std::max(n_cu, 1);
+  kv->decode_capacity.assign(kv->layers.size(), 0);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_pool, kv->pool_blocks * kv->block_bytes);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
   if (e != hipSuccess) {
@@ -947,11 +953,26 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     total_tiles += pos / 16 - lo / 16 + 1;
   }
   total_tiles *= (uint64_t)y.n_kv * head_blocks;
-  const uint64_t target = env_u64("LMH_DECODE_TARGET_ITEMS", 2048);
+  // Items the GPU holds at once: with at most that many, every item starts in the first round and
+  // none waits for a slot to free up (a second, mostly empty round would double the kernel time).
+  if (kv->decode_capacity[layer] == 0)
+    kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd) * kv->n_cu;
+  const uint64_t target = std::max<uint64_t>(env_u64("LMH_DECODE_TARGET_ITEMS", kv->decode_capacity[layer]), 1);
   const uint64_t min_chunk = std::max<uint64_t>(env_u64("LMH_DECODE_MIN_TILES", 8), 1);
-  // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane)
-  const uint64_t chunk = std::min<uint64_t>(
-      64, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / std::max<uint64_t>(target, 1)));
+  // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane);
+  // grown until the rows' rounded-up split counts fit the target
+  auto n_items_for = [&](uint64_t c) {
+    uint64_t n = 0;
+    for (uint64_t t = 0; t < n_rows; t++) {
+      if (!decode_row[t]) continue;
+      const uint64_t pos = (uint64_t)kv->row_pos[t];
+      const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+      n += (pos / 16 - lo / 16 + 1 + c - 1) / c;
+    }
+    return n * y.n_kv * head_blocks;
+  };
+  uint64_t chunk = std::min<uint64_t>(64, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / target));
+  while (chunk < 64 && n_items_for(chunk) > target) chunk++;
   kv->items.clear();
   kv->merges.clear();
   uint32_t slots = 0;

@@ -85,7 +85,10 @@ class HipKvCache:
 
     def close(self):
         if getattr(self, "h", None):
-            N.lib().lmh_kv_destroy(self.h)
+            lib = getattr(N, "lib", None)
+            if lib is None:  # interpreter shutdown: the module is already torn down
+                return
+            lib().lmh_kv_destroy(self.h)
             self.h = None
 
     def __del__(self):
