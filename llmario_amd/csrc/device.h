@@ -132,11 +132,12 @@ hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, 
 uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 
-// Prefill (multi-token segments on matrix cores). `max_pages` bounds the key pages of any item.
-hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_items,
-                          uint32_t max_pages, const float* q, float* out, hipStream_t s);
+// Prefill (multi-token segments on matrix cores): n_wg workgroups, workgroup b runs the units
+// items[b * per_wg ..] up to the first with n_tok == 0. `max_pages` bounds the key pages of any unit.
+hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
+                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s);
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group);
 uint32_t prefill_cols_per_unit();
-size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages);
+size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg);
 
 }  // namespace lmh

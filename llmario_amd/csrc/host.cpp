@@ -22,6 +22,7 @@
 #include <cstring>
 #include <deque>
 #include <map>
+#include <queue>
 #include <string>
 #include <vector>
 
@@ -837,12 +838,37 @@ int32_t lmh_batch_commit(lmh_kv* kv, const lmh_seg* segs, uint64_t n_segs) {
   return LMH_OK;
 }
 
-// Launch order of the prefill units: longest key ranges first, so the short causal units fill in
-// behind them.
-static void order_prefill_units(std::vector<PrefillItem>& items) {
-  std::stable_sort(items.begin(), items.end(), [](const PrefillItem& a, const PrefillItem& b) {
-    return a.pos0 + a.n_tok > b.pos0 + b.n_tok;
-  });
+// Prefill units grouped per workgroup: one workgroup per CU (the kernel's LDS admits one), each
+// running a list of units. Longest-processing-time-first: units by decreasing key pages (plus a
+// fixed cost for the unit's Q load and output), each to the currently least loaded workgroup.
+// Lists are padded to the longest with empty units (n_tok = 0) at a fixed stride.
+static void assign_prefill_units(std::vector<PrefillItem>& items, uint64_t window, uint32_t n_cu, uint32_t& n_wg,
+                                 uint32_t& per_wg) {
+  n_wg = (uint32_t)std::min<uint64_t>(items.size(), std::max<uint32_t>(n_cu, 1));
+  per_wg = 0;
+  if (n_wg == 0) return;
+  auto work = [&](const PrefillItem& it) -> uint64_t {
+    const uint64_t last = (uint64_t)it.pos0 + it.n_tok - 1;
+    const uint64_t lo = (window > 0 && it.pos0 + 1 > window) ? it.pos0 + 1 - window : 0;
+    return last / 16 - lo / 16 + 1 + 8;
+  };
+  std::stable_sort(items.begin(), items.end(),
+                   [&](const PrefillItem& a, const PrefillItem& b) { return work(a) > work(b); });
+  std::vector<std::vector<uint32_t>> lists(n_wg);
+  std::priority_queue<std::pair<uint64_t, uint32_t>, std::vector<std::pair<uint64_t, uint32_t>>,
+                      std::greater<std::pair<uint64_t, uint32_t>>> load;
+  for (uint32_t b = 0; b < n_wg; b++) load.push({0, b});
+  for (uint32_t i = 0; i < items.size(); i++) {
+    auto [l, b] = load.top();
+    load.pop();
+    lists[b].push_back(i);
+    load.push({l + work(items[i]), b});
+  }
+  for (const auto& li : lists) per_wg = std::max<uint32_t>(per_wg, (uint32_t)li.size());
+  std::vector<PrefillItem> out((size_t)n_wg * per_wg, PrefillItem{0, 0, 0, 0, 0, 0, 0, 0});
+  for (uint32_t b = 0; b < n_wg; b++)
+    for (size_t j = 0; j < lists[b].size(); j++) out[(size_t)b * per_wg + j] = items[lists[b][j]];
+  items.swap(out);
 }
 
 static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const void* a, const void* b,
@@ -913,12 +939,13 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   hipStream_t st = (hipStream_t)stream;
 
   // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
-  // in units of up to prefill_cols_per_unit()/group tokens per KV head, heaviest first.
+  // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over one
+  // workgroup per CU.
   const uint64_t pf_min = env_u64("LMH_PREFILL_MIN_ROWS", 16);
   const bool pf_ok = scale > 0.f && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
   std::vector<uint8_t> decode_row(n_rows, 1);
   kv->pitems.clear();
-  uint32_t max_pages = 0;
+  uint32_t max_pages = 0, pf_wg = 0, pf_per_wg = 0;
   if (pf_ok) {
     const uint32_t unit_tok = prefill_cols_per_unit() / group;
     for (uint64_t i = 0; i < n_segs; i++) {
@@ -934,12 +961,13 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
       }
       for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
     }
-    order_prefill_units(kv->pitems);
-    if (prefill_lds_bytes(y.hd, max_pages) > 160 * 1024) {
+    assign_prefill_units(kv->pitems, window, kv->n_cu, pf_wg, pf_per_wg);
+    if (prefill_lds_bytes(y.hd, max_pages, pf_per_wg) > 160 * 1024) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
       kv->pitems.clear();
       std::fill(decode_row.begin(), decode_row.end(), 1);
       max_pages = 0;
+      pf_wg = pf_per_wg = 0;
     }
   }
 
@@ -1021,8 +1049,8 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     pg.scale_log2 = scale * 1.4426950408889634f;
     pg.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
     if ((e = kv->time_begin(st, LMH_KERNEL_PREFILL)) != hipSuccess) return kv->hip_fail(e, "event");
-    e = launch_prefill(kv->geom(layer), pg, (const PrefillItem*)(ex + items_pad + merges_pad),
-                       (uint32_t)kv->pitems.size(), max_pages, q, out, st);
+    e = launch_prefill(kv->geom(layer), pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg,
+                       max_pages, q, out, st);
     if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
     if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }

@@ -6,26 +6,27 @@
 // per query head, fp32 accumulation. The Metal sibling is attn_prefill_t
 // (crates/engine/metal/src/shaders/attn_prefill.metal:17-195); this kernel is designed for CDNA4.
 //
-// Work unit (one workgroup of 8 waves, two per SIMD): one sequence, one KV head, a run of up to
-// 256/G tokens. Its "columns" are the (token, query-head) pairs of the run flattened token-major
-// (c = token*G + head), so all G query heads of the KV group share every K/V tile; wave w owns
+// Work unit: one sequence, one KV head, a run of up to 256/G tokens. Its "columns" are the
+// (token, query-head) pairs of the run flattened token-major (c = token*G + head), so all G query
+// heads of the KV group share every K/V tile. One workgroup of 8 waves (two per SIMD, one
+// workgroup per CU) runs a list of units the host balanced across the workgroups; wave w owns
 // columns 32w .. 32w+31 as two 16-column MFMA blocks. Per 64-key tile, in two 32-key halves:
-//   S^T[32 keys x 32 cols] = K . Q^T     v_mfma_f32_16x16x32_{bf16,f16}, Q resident in VGPRs
+//   S^T[32 keys x 32 cols] = K . Q^T     v_mfma_f32_16x16x32_f16, Q resident in VGPRs
 //   online softmax per column in the S^T layout (keys along the 4 lane groups and 4 registers)
 //   O^T[hd x 32 cols]     += V^T . P^T  v_mfma_f32_16x16x32_f16, P rounded to f16
-// K/V tiles go from HBM straight into LDS (global_load_lds, three stages, two tiles in flight)
-// in the page layout, which already holds each 16-token tile in MFMA operand order; bf16 V is
-// widened to f16 in LDS once per tile by the thread that loaded it (exact for |v| in
-// [2^-14, 65504]). Scores are scaled in fp32 (log2 domain) rather than pre-scaling Q in the
-// 16-bit type. The reference max of a column moves lazily (only when a block's max exceeds it
-// by more than 2^8), so the O accumulators are almost never rescaled.
+// K/V tiles go from HBM straight into LDS (global_load_lds, four stages, two tiles in flight)
+// in the page layout, which already holds each 16-token tile in MFMA operand order; bf16 K and V
+// are widened to f16 in LDS once per tile by the thread that loaded them (exact for |x| in
+// [2^-14, 65504]), so Q keeps 11 bits. Q carries the softmax scale (log2 domain) and each
+// column's reference max enters as the initial accumulator of Q.K, so the products are the
+// exponent arguments directly. The reference max moves lazily (only when a score exceeds it by
+// more than 8 in the log2 domain), so the O accumulators are almost never rescaled.
 #include "device.h"
 
 namespace lmh {
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef __bf16 b8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int PW = 8;          // waves per workgroup
@@ -54,11 +55,6 @@ __device__ inline float sum_over_groups(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
-__device__ inline uint16_t bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane L reads
 // sbase + voff(L) and writes lds_dst + 16*L, where sbase and lds_dst are wave-uniform (an SGPR pair
@@ -81,16 +77,26 @@ __device__ inline uint32_t bf2_to_h2(uint32_t w) {
 
 template <int KVT, int HD>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const float* q, float* out) {
+void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32_t per_wg, const float* q,
+                    float* out) {
   constexpr int NC = HD / 32;                 // Q.K chunks of 32 dims
   constexpr int NJ = HD / 16;                 // O^T blocks of 16 dims
   constexpr int TILE = 16 * HD * 2;           // bytes of one 16-token page tile (K or V)
-  using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* kv_lds = smem;                                 // [NSTAGE][K 4 tiles | V 4 tiles]
-  int* blk_lds = (int*)(smem + NSTAGE * 8 * TILE);        // block id of each key page in range
+  uint8_t* kv_lds = smem;                                          // [NSTAGE][K 4 tiles | V 4 tiles]
+  PrefillItem* units = (PrefillItem*)(smem + NSTAGE * 8 * TILE);   // this workgroup's unit list
+  int* blk_lds = (int*)(units + per_wg);                           // block id of each key page in range
 
-  const PrefillItem it = items[blockIdx.x];
+  // The workgroup's units (the host's balanced assignment, per_wg slots, an empty unit ends the
+  // list): fetched once, so each unit starts without a memory round trip for its descriptor.
+  {
+    const uint32_t* src = (const uint32_t*)(items + (size_t)blockIdx.x * per_wg);
+    for (uint32_t i = threadIdx.x; i < per_wg * (sizeof(PrefillItem) / 4); i += NT) ((uint32_t*)units)[i] = src[i];
+  }
+  __syncthreads();
+  for (uint32_t unit = 0; unit < per_wg; unit++) {
+  const PrefillItem it = units[unit];
+  if (it.n_tok == 0) break;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
   const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, kept in a scalar register
   const uint32_t hq = lane & 15u, grp = lane >> 4;
@@ -109,7 +115,7 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
   // ---- this lane's columns (one per 16-column block) and their Q fragments
   uint32_t cpos[NCB], clo[NCB];
   bool cval[NCB];
-  MT qf[NCB][NC];
+  h8 qf[NCB][NC];
 #pragma unroll
   for (int cb = 0; cb < NCB; cb++) {
     const uint32_t c = w * COLS + cb * 16 + hq;
@@ -124,68 +130,118 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
       float4 b = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp + 4) : make_float4(0, 0, 0, 0);
       const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        if constexpr (KVT == KV_BF16) {
-          qf[cb][ch][i] = __builtin_bit_cast(__bf16, bf16_rne(x[i]));
-        } else {
-          qf[cb][ch][i] = (_Float16)x[i];
-        }
-      }
+      for (int i = 0; i < 8; i++) qf[cb][ch][i] = (_Float16)(x[i] * pg.scale_log2);
     }
   }
   __syncthreads();
 
-  // ---- K/V staging. Tile i covers keys (page0 + 4i)*16 .. +64: 4 K and 4 V page tiles. Wave w
-  // copies half (w & 1) of page tile (w >> 1) on each side, CPT rows of 1024 bytes, so its page
-  // (and the block id behind it) is wave-uniform and the addresses are scalar. Pages past the
-  // range re-read the last page (finite values whose keys are masked), so stale LDS never meets a
-  // zero weight.
-  constexpr int CPT = TILE / 2 / 1024;        // DMA rows per wave per side per tile
-  static_assert(CPT >= 1 && 8 * CPT * 1024 == 4 * TILE, "8 waves cover the 4 page tiles of a side");
+  // ---- K/V staging. Tile i covers keys (page0 + 4i)*16 .. +64: 4 K and 4 V page tiles, each
+  // R rows of 1 KiB (one wave-wide DMA per row). Every wave issues 2*CPT DMAs per tile, so its
+  // block ids are wave-uniform and the addresses scalar.
+  //   f16: wave w copies half (w & 1) of page tile (w >> 1) on both sides (one page).
+  //   bf16: K as two consecutive rows of one page tile; V as the same row of page tiles 2h and
+  //      2h+1 (the two tiles of half h), so the thread that loaded them can interleave them for
+  //      the P.V products (settle, below). hd 128 (R = 4): every wave does two K rows and one V
+  //      row pair; hd 64 (R = 2): waves 0-3 a V row pair each, waves 4-7 two K rows each.
+  // Pages past the range re-read the last page (finite values whose keys are masked), so stale
+  // LDS never meets a zero weight.
+  constexpr bool PAIR_V = KVT == KV_BF16;
+  constexpr int R = TILE / 1024;
+  constexpr int CPT = TILE / 2 / 1024;        // DMAs per wave per side per tile (on average)
+  static_assert((R == 4 || R == 2) && CPT * 2048 == TILE, "page tiles of 2 or 4 KiB");
   const uint32_t n_tiles = (n_pages + 3) / 4;
-  const uint32_t my_tile = w >> 1, my_off = my_tile * TILE + (w & 1) * (TILE / 2);
-  const uint32_t voff = (w & 1) * (TILE / 2) + lane * 16;
+  const bool do_k = R == 4 || w >= 4, do_v = R == 4 || w < 4;
+  const uint32_t kw = R == 4 ? w : w - 4;
+  const uint32_t k_tile = 2 * kw / R, k_row = (2 * kw) % R * 1024;   // K rows k_row, k_row + 1 KiB
+  const uint32_t v_half = w / R, v_row = w % R * 1024;               // V row of tiles 2h, 2h+1
+  const uint32_t my_tile = w >> 1, my_row = (w & 1) * (TILE / 2);   // f16: both sides
   const uint64_t k_head = g.k_off + (uint64_t)it.kvh * g.k_head;
   const uint64_t v_head = g.v_off + (uint64_t)it.kvh * g.v_head;
+  // block base and 16-token sub-tile index of page tile `tile` of tile ti
+  auto page = [&](uint32_t ti, uint32_t tile, const uint8_t*& base, uint32_t& sub) {
+    const uint32_t p = min(ti * 4 + tile, n_pages - 1);
+    const uint64_t blk = (uint32_t)__builtin_amdgcn_readfirstlane(blk_lds[p]);
+    sub = (((page0 + p) << 4) & ((1u << g.bt_shift) - 1u)) >> 4;
+    base = g.pool + blk * g.block_bytes;
+  };
   auto issue = [&](uint32_t ti) {
     uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
-    const uint32_t p = min(ti * 4 + my_tile, n_pages - 1);
-    const uint64_t blk = (uint32_t)__builtin_amdgcn_readfirstlane(blk_lds[p]);
-    const uint32_t sub = (((page0 + p) << 4) & ((1u << g.bt_shift) - 1u)) >> 4;
-    const uint8_t* pb = g.pool + blk * g.block_bytes;
-    const uint8_t* kb = pb + k_head + sub * g.k_tile;
-    const uint8_t* vb = pb + v_head + sub * g.v_tile;
-#pragma unroll
-    for (int k = 0; k < CPT; k++) {
-      lds_dma16(kb, voff + k * 1024, stage + my_off + k * 1024);
-      lds_dma16(vb, voff + k * 1024, stage + 4 * TILE + my_off + k * 1024);
-    }
-  };
-  // After this wave's share of tile ti has landed: widen its V rows from bf16 to f16 in place.
-  auto widen = [&](uint32_t ti) {
-    if constexpr (KVT == KV_BF16) {
-      uint8_t* v = kv_lds + (ti % NSTAGE) * 8 * TILE + 4 * TILE + my_off + lane * 16;
+    const uint8_t* base;
+    uint32_t sub;
+    if constexpr (!PAIR_V) {
+      page(ti, my_tile, base, sub);
+      const uint8_t* kb = base + k_head + sub * g.k_tile;
+      const uint8_t* vb = base + v_head + sub * g.v_tile;
 #pragma unroll
       for (int k = 0; k < CPT; k++) {
-        uint4* p = (uint4*)(v + k * 1024);
-        uint4 x = *p;
-        x.x = bf2_to_h2(x.x);
-        x.y = bf2_to_h2(x.y);
-        x.z = bf2_to_h2(x.z);
-        x.w = bf2_to_h2(x.w);
-        *p = x;
+        lds_dma16(kb, my_row + k * 1024 + lane * 16, stage + my_tile * TILE + my_row + k * 1024);
+        lds_dma16(vb, my_row + k * 1024 + lane * 16, stage + 4 * TILE + my_tile * TILE + my_row + k * 1024);
+      }
+      return;
+    }
+    if (do_k) {
+      page(ti, k_tile, base, sub);
+      const uint8_t* kb = base + k_head + sub * g.k_tile;
+      lds_dma16(kb, k_row + lane * 16, stage + k_tile * TILE + k_row);
+      lds_dma16(kb, k_row + 1024 + lane * 16, stage + k_tile * TILE + k_row + 1024);
+    }
+    if (do_v) {
+#pragma unroll
+      for (int t2 = 0; t2 < 2; t2++) {
+        const uint32_t tile = 2 * v_half + t2;
+        page(ti, tile, base, sub);
+        const uint8_t* vb = base + v_head + sub * g.v_tile;
+        lds_dma16(vb, v_row + lane * 16, stage + 4 * TILE + tile * TILE + v_row);
+      }
+    }
+  };
+  // After this thread's rows of tile ti have landed, bf16 only: K and V are widened to f16 in
+  // place (so both products run in f16 and Q keeps 11 bits), and the thread's two V chunks A
+  // (tile 2h) and B (tile 2h+1), each [4 keys of dim d | 4 keys of dim d+16], are rewritten as
+  // A' = [A keys of d | B keys of d] and B' = [A keys of d+16 | B keys of d+16], so one 16-byte
+  // read is a whole 32-key operand of the P.V product. f16 tiles are used as loaded (the extra
+  // LDS pass would cost more than the operand assembly it saves).
+  auto settle = [&](uint32_t ti) {
+    uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
+    if constexpr (KVT == KV_BF16) {
+      if (do_k) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+          uint4* p = (uint4*)(stage + k_tile * TILE + k_row + r * 1024 + lane * 16);
+          uint4 x = *p;
+          x.x = bf2_to_h2(x.x);
+          x.y = bf2_to_h2(x.y);
+          x.z = bf2_to_h2(x.z);
+          x.w = bf2_to_h2(x.w);
+          *p = x;
+        }
+      }
+    }
+    if constexpr (KVT == KV_BF16) {
+      if (do_v) {
+        uint4* pa = (uint4*)(stage + 4 * TILE + 2 * v_half * TILE + v_row + lane * 16);
+        uint4* pb = (uint4*)((uint8_t*)pa + TILE);
+        uint4 x = *pa, y = *pb;
+        x = make_uint4(bf2_to_h2(x.x), bf2_to_h2(x.y), bf2_to_h2(x.z), bf2_to_h2(x.w));
+        y = make_uint4(bf2_to_h2(y.x), bf2_to_h2(y.y), bf2_to_h2(y.z), bf2_to_h2(y.w));
+        *pa = make_uint4(x.x, x.y, y.x, y.y);
+        *pb = make_uint4(x.z, x.w, y.z, y.w);
       }
     }
   };
 
-  // Online-softmax state per column: reference max m (log2 domain), -m (0 while no key is
-  // visible), the threshold on raw scores above which m must move, row sum l, and O^T.
-  float m[NCB], nm[NCB], thr[NCB], l[NCB];
+  // Online-softmax state per column. Q carries the scale (q * scale * log2 e), so a product is a
+  // score in the log2 domain, and the reference max m rides in as the products' initial
+  // accumulator: nmv = {-m, -m, -m, -m}, making every score s - m directly (m = 0 while the column
+  // has seen no key). thr: the relative score above which m must move (8, or -inf while no key is
+  // visible). l: row sum; O^T.
+  float nm[NCB], thr[NCB], l[NCB];
+  f4 nmv[NCB];
   f4 O[NJ][NCB];
 #pragma unroll
   for (int cb = 0; cb < NCB; cb++) {
-    m[cb] = -INFINITY;
     nm[cb] = 0.f;
+    nmv[cb] = f4{0.f, 0.f, 0.f, 0.f};
     thr[cb] = -INFINITY;
     l[cb] = 0.f;
 #pragma unroll
@@ -201,26 +257,44 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
     wpos_max = it.pos0 + t1;
   }
   const uint32_t wlo_max = (pg.window > 0 && wpos_max + 1 > pg.window) ? wpos_max + 1 - pg.window : 0;
-  const float c = pg.scale_log2;  // > 0 (the host routes other scales to the decode kernel)
 
-  // S^T for the 32 keys of half kp of a tile (two 16-key page tiles) x this wave's 32 columns
-  auto qk = [&](f4 (&S)[2][NCB], const uint8_t* kt, int kp) {
+  // Matrix-core operands of one 32-key half, read from LDS ahead of the products that use them
+  // (the reads of one phase are in flight while the previous phase computes).
+  struct KOps { uint4 a[NC][2]; };   // K: chunk ch of page tile kk
+  struct VOps { uint4 a[NJ]; };      // V^T: dims 16j.. of both page tiles (8 bytes each)
+  auto load_k = [&](KOps& o, const uint8_t* kt, int kp) {
 #pragma unroll
-    for (int kk = 0; kk < 2; kk++) {
+    for (int ch = 0; ch < NC; ch++)
 #pragma unroll
-      for (int cb = 0; cb < NCB; cb++) S[kk][cb] = f4{0.f, 0.f, 0.f, 0.f};
+      for (int kk = 0; kk < 2; kk++) o.a[ch][kk] = *(const uint4*)(kt + (2 * kp + kk) * TILE + ch * 1024 + lane * 16);
+  };
+  // k index 8g+i of the P.V product is key 4g+i of the half's first 16-key page tile (i < 4) or
+  // key 4g+i-4 of its second: 8 bytes from each page tile (f16), or after settle (bf16) one
+  // 16-byte chunk (in the first tile's slot for even j, the second's for odd j).
+  auto load_v = [&](VOps& o, const uint8_t* vt, int kp) {
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      if constexpr (KVT == KV_BF16) {
+        o.a[j] = *(const uint4*)(vt + (2 * kp + (j & 1)) * TILE + (j >> 1) * 1024 + lane * 16);
+      } else {
+        const uint32_t off = (j >> 1) * 1024 + lane * 16 + (j & 1) * 8;
+        const uint2 v0 = *(const uint2*)(vt + (2 * kp) * TILE + off);
+        const uint2 v1 = *(const uint2*)(vt + (2 * kp + 1) * TILE + off);
+        o.a[j] = make_uint4(v0.x, v0.y, v1.x, v1.y);
+      }
     }
+  };
+  // S^T for the 32 keys of a half (two 16-key page tiles) x this wave's 32 columns
+  auto qk = [&](f4 (&S)[2][NCB], const KOps& ko) {
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
-        const MT a = __builtin_bit_cast(MT, *(const uint4*)(kt + (2 * kp + kk) * TILE + ch * 1024 + lane * 16));
+        const h8 a = __builtin_bit_cast(h8, ko.a[ch][kk]);
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++) {
-          if constexpr (KVT == KV_BF16)
-            S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qf[cb][ch], S[kk][cb], 0, 0, 0);
-          else
-            S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], S[kk][cb], 0, 0, 0);
+          const f4 acc = ch == 0 ? nmv[cb] : S[kk][cb];
+          S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], acc, 0, 0, 0);
         }
       }
     }
@@ -239,11 +313,11 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
       }
     }
   };
-  // Lazy reference max: m moves (rescaling O and l) only when a score exceeds it by more than 8 in
-  // the log2 domain, so p = 2^(s*c - m) <= 2^8 and O is rarely touched. Each lane checks its own 8
-  // scores per column; only when some lane needs a move is the column max reduced over the lane
-  // groups (the decision is then the same on every lane of a column).
-  auto rebase = [&](const f4 (&S)[2][NCB]) {
+  // Lazy reference max: m moves (rescaling O and l) only when a relative score exceeds 8, so
+  // p = 2^(s - m) <= 2^8 and O is rarely touched. Each lane checks its own 8 scores per column;
+  // only when some lane needs a move is the column max reduced over the lane groups (the decision
+  // is then the same on every lane of a column), and the half's scores are shifted to the new m.
+  auto rebase = [&](f4 (&S)[2][NCB]) {
     float lm[NCB];
     bool need = false;
 #pragma unroll
@@ -255,20 +329,23 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
     if (__ballot(need)) {
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) {
-        const float tmax = max_over_groups(lm[cb]) * c;
-        const bool mv = tmax > m[cb] + 8.0f;
-        // m = -inf (first visible key of this column): O and l are still zero
-        const float alpha = !mv ? 1.f : (m[cb] == -INFINITY ? 0.f : exp2_fast(m[cb] - tmax));
+        const float tmax = max_over_groups(lm[cb]);
+        const bool mv = tmax > thr[cb];
+        // no key seen yet (thr = -inf): O and l are zero, and tmax may be any finite value
+        const float alpha = !mv ? 1.f : (thr[cb] == -INFINITY ? 0.f : exp2_fast(-tmax));
+        const float sh = mv ? tmax : 0.f;
         l[cb] *= alpha;
 #pragma unroll
         for (int j = 0; j < NJ; j++) O[j][cb] *= alpha;
-        m[cb] = mv ? tmax : m[cb];
-        nm[cb] = m[cb] == -INFINITY ? 0.f : -m[cb];
-        thr[cb] = (m[cb] + 8.0f) / c;
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) S[kk][cb] -= sh;
+        nm[cb] -= sh;
+        nmv[cb] = f4{nm[cb], nm[cb], nm[cb], nm[cb]};
+        thr[cb] = mv ? 8.0f : thr[cb];
       }
     }
   };
-  // P = 2^(s*c - m) rounded to f16 (<= 2^8), row sums in f32
+  // P = 2^(s - m) rounded to f16 (<= 2^8), row sums in f32
   auto softmax = [&](const f4 (&S)[2][NCB], h8 (&P)[NCB]) {
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
@@ -276,23 +353,18 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) pv[kk * 4 + r] = exp2_fast(__builtin_fmaf(S[kk][cb][r], c, nm[cb]));
+        for (int r = 0; r < 4; r++) pv[kk * 4 + r] = exp2_fast(S[kk][cb][r]);
       }
       l[cb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
       P[cb] = h8{(_Float16)pv[0], (_Float16)pv[1], (_Float16)pv[2], (_Float16)pv[3],
                  (_Float16)pv[4], (_Float16)pv[5], (_Float16)pv[6], (_Float16)pv[7]};
     }
   };
-  // O^T += V^T P^T over half kp, 32 keys per MFMA: k index 8g+i is key 4g+i of the half's first
-  // 16-key page tile (i < 4) or key 4g+i-4 of its second; the V^T operand reads the same keys
-  // (8 bytes from each of the two page tiles).
-  auto pv = [&](const h8 (&P)[NCB], const uint8_t* vt, int kp) {
+  // O^T += V^T P^T over a half, 32 keys per MFMA
+  auto pv = [&](const h8 (&P)[NCB], const VOps& vo) {
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-      const uint32_t off = (j >> 1) * 1024 + lane * 16 + (j & 1) * 8;
-      const uint2 v0 = *(const uint2*)(vt + (2 * kp) * TILE + off);
-      const uint2 v1 = *(const uint2*)(vt + (2 * kp + 1) * TILE + off);
-      const h8 va = __builtin_bit_cast(h8, make_uint4(v0.x, v0.y, v1.x, v1.y));
+      const h8 va = __builtin_bit_cast(h8, vo.a[j]);
 #pragma unroll
       for (int cb = 0; cb < NCB; cb++) O[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, P[cb], O[j][cb], 0, 0, 0);
     }
@@ -316,15 +388,20 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    widen(ti);
+    settle(ti);
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
   f4 S0[2][NCB], S1[2][NCB];
   h8 P[NCB];
+  KOps ko;
+  VOps vo;
   issue(0);
   if (n_tiles > 1) issue(1);
   publish(0);
-  if (wave_active) qk(S0, kv_lds, 0);
+  if (wave_active) {
+    load_k(ko, kv_lds, 0);
+    qk(S0, ko);
+  }
   for (uint32_t ti = 0; ti < n_tiles; ti++) {
     if (ti + 2 < n_tiles) issue(ti + 2);
     const uint8_t* kt = kv_lds + (ti % NSTAGE) * 8 * TILE;
@@ -332,20 +409,26 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
     const uint32_t key0 = (page0 + ti * 4) * 16;
     const bool need_mask = key0 + BK - 1 > wpos_min || key0 < wlo_max || key0 + BK - 1 > pos_last;
     if (wave_active) {
+      load_k(ko, kt, 1);
+      load_v(vo, vt, 0);
       if (need_mask) mask(S0, key0);
       rebase(S0);
-      qk(S1, kt, 1);
+      qk(S1, ko);
       softmax(S0, P);
-      pv(P, vt, 0);
+      pv(P, vo);
       if (need_mask) mask(S1, key0 + 32);
       rebase(S1);
     }
     if (ti + 1 < n_tiles) publish(ti + 1);
     if (wave_active) {
+      load_v(vo, vt, 1);
+      // first half of the next tile (after the last tile: a stale stage, never used), issued
+      // before this half's exponentials so its products overlap them and are complete when the
+      // next iteration reads S0
+      load_k(ko, kv_lds + ((ti + 1) % NSTAGE) * 8 * TILE, 0);
+      qk(S0, ko);
       softmax(S1, P);
-      pv(P, vt, 1);
-      // first half of the next tile (after the last tile: a stale stage, never used)
-      qk(S0, kv_lds + ((ti + 1) % NSTAGE) * 8 * TILE, 0);
+      pv(P, vo);
     }
   }
 
@@ -364,13 +447,16 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, const 
       *(float4*)(op + 16 * j + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }
+  // every wave is done with the stages and block ids before the next unit refills them
+  __syncthreads();
+  }
 }
 
 template <int KVT, int HD>
-hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_items,
-                    uint32_t max_pages, const float* q, float* out, hipStream_t s) {
-  const size_t lds = prefill_lds_bytes(HD, max_pages);
-  hipLaunchKernelGGL((prefill_kernel<KVT, HD>), dim3(n_items), dim3(NT), lds, s, g, pg, items, q, out);
+hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
+                    uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s) {
+  const size_t lds = prefill_lds_bytes(HD, max_pages, per_wg);
+  hipLaunchKernelGGL((prefill_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
   return hipGetLastError();
 }
 
@@ -378,8 +464,8 @@ hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem*
 
 uint32_t prefill_cols_per_unit() { return PW * COLS; }
 
-size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages) {
-  return NSTAGE * 8 * (16 * (size_t)hd * 2) + (size_t)max_pages * 4;
+size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg) {
+  return NSTAGE * 8 * (16 * (size_t)hd * 2) + (size_t)per_wg * sizeof(PrefillItem) + (size_t)max_pages * 4;
 }
 
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group) {
@@ -387,15 +473,15 @@ bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t gro
          group <= PW * COLS;
 }
 
-hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_items,
-                          uint32_t max_pages, const float* q, float* out, hipStream_t s) {
-  if (n_items == 0) return hipSuccess;
+hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
+                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s) {
+  if (n_wg == 0 || per_wg == 0) return hipSuccess;
   if (g.kv_type == KV_BF16) {
-    if (g.hd == 128) return launch_t<KV_BF16, 128>(g, pg, items, n_items, max_pages, q, out, s);
-    if (g.hd == 64) return launch_t<KV_BF16, 64>(g, pg, items, n_items, max_pages, q, out, s);
+    if (g.hd == 128) return launch_t<KV_BF16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
+    if (g.hd == 64) return launch_t<KV_BF16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
   } else if (g.kv_type == KV_F16) {
-    if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_items, max_pages, q, out, s);
-    if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_items, max_pages, q, out, s);
+    if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
+    if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
   }
   return hipErrorInvalidValue;
 }
