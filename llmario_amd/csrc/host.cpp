@@ -177,6 +177,8 @@ struct lmh_kv {
   // ---- device
   int device = 0;
   uint32_t n_cu = 0;                        // compute units of the device
+  hipStream_t side = nullptr;               // decode work running beside a prefill kernel
+  hipEvent_t fork = nullptr, join = nullptr;
   std::vector<uint32_t> decode_capacity;    // per layer: decode items resident at once (0 = not yet asked)
   uint8_t* d_pool = nullptr;
   int32_t* d_table = nullptr;
@@ -202,6 +204,9 @@ struct lmh_kv {
 
   ~lmh_kv() {
     if (d_pool || d_table) (void)hipDeviceSynchronize();
+    if (fork) (void)hipEventDestroy(fork);
+    if (join) (void)hipEventDestroy(join);
+    if (side) (void)hipStreamDestroy(side);
     if (d_pool) (void)hipFree(d_pool);
     if (d_table) (void)hipFree(d_table);
     for (auto& p : evs) {
@@ -621,6 +626,9 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, o->device);
   kv->n_cu = (uint32_t)std::max(n_cu, 1);
   kv->decode_capacity.assign(kv->layers.size(), 0);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->side, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->fork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_pool, kv->pool_blocks * kv->block_bytes);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
   if (e != hipSuccess) {
@@ -1040,8 +1048,22 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   const int32_t *rs, *rp;
   const uint8_t* ex;
   int slot;
-  if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
   hipError_t e;
+  // the split partials' buffer first: growing it synchronises the device
+  if (slots > 0) {
+    if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+  }
+  if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
+  // A mixed batch runs its decode items on a second stream, beside the prefill kernel (which
+  // holds one workgroup per CU it uses; the decode waves take the CUs it leaves free), and the
+  // caller's stream waits for both before the merge.
+  const bool overlap = !kv->pitems.empty() && !kv->items.empty();
+  hipStream_t ds = st;
+  if (overlap) {
+    if ((e = hipEventRecord(kv->fork, st)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = hipStreamWaitEvent(kv->side, kv->fork, 0)) != hipSuccess) return kv->hip_fail(e, "stream wait");
+    ds = kv->side;
+  }
   if (!kv->pitems.empty()) {
     PrefillGeom pg{};
     pg.n_head = y.n_head;
@@ -1055,9 +1077,6 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   if (kv->items.empty()) return kv->release_rows(slot, st);
-  if (slots > 0) {
-    if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
-  }
   const PageGeom g = kv->geom(layer);
   RowGeom r{};
   r.row_seq = rs;
@@ -1067,10 +1086,14 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   r.ng = ng;
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
-  if ((e = kv->time_begin(st, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
-  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, st);
+  if ((e = kv->time_begin(ds, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
+  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, ds);
   if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
-  if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  if ((e = kv->time_end(ds)) != hipSuccess) return kv->hip_fail(e, "event");
+  if (overlap) {
+    if ((e = hipEventRecord(kv->join, ds)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = hipStreamWaitEvent(st, kv->join, 0)) != hipSuccess) return kv->hip_fail(e, "stream wait");
+  }
   if (!kv->merges.empty()) {
     if ((e = kv->time_begin(st, LMH_KERNEL_MERGE)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_merge(r, y.hdv, (const MergeItem*)(ex + items_pad), (uint32_t)kv->merges.size(),
