@@ -130,6 +130,14 @@ __device__ inline float scale_at(const uint4* s, int r, int c) {
   return h_to_f((uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
 }
 
+// The first workgroup of a decode launch copies the call's merge list from the staged (host-mapped)
+// work list into device memory, beside its own work: the merge kernel that follows then starts
+// from device memory instead of a round trip over the bus.
+__device__ inline void copy_merges(const MergeCopy& mc) {
+  if (blockIdx.x != 0) return;
+  for (uint32_t i = threadIdx.x; i < mc.n_words; i += blockDim.x) mc.dst[i] = mc.src[i];
+}
+
 // Split-K merge (forward.rs:772-806), one wave per (task, query head), lanes over dims:
 // m* = max m_s, out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m in the log2 domain.
 // A separate launch: the kernel boundary makes every split's partials visible across XCDs.
@@ -152,14 +160,23 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
   for (int i = 0; i < NP; i++) acc[i] = 0.f;
   float M = -INFINITY, L = 0.f;
   // Up to 64 splits per round: lane s holds split s's (m, l); every lane then folds all of the
-  // round's partial rows into its NP dims (independent loads, issued together).
+  // round's partial rows into its NP dims. The first 16 rows are loaded together with (m, l), so
+  // a merge of up to 16 splits costs one memory round trip.
   for (uint32_t s0 = 0; s0 < mi.n_split; s0 += 64) {
     const uint32_t s = s0 + lane;
+    const uint32_t n = (mi.n_split - s0) < 64u ? (mi.n_split - s0) : 64u;
     float ms = -INFINITY, ls = 0.f;
     if (s < mi.n_split) {
       const float2 ml = *(const float2*)(base + s * stride + HDV);
       ms = ml.x;
       ls = ml.y;
+    }
+    float pre[16][NP];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const float* pp = base + (s0 + ((uint32_t)k < n ? k : 0)) * stride + lane * NP;
+#pragma unroll
+      for (int i = 0; i < NP; i++) pre[k][i] = pp[i];
     }
     float Mr = ms;
     for (int x = 32; x >= 1; x >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, x));
@@ -172,27 +189,17 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
 #pragma unroll
     for (int i = 0; i < NP; i++) acc[i] *= rescale;
     M = Mn;
-    const uint32_t n = (mi.n_split - s0) < 64u ? (mi.n_split - s0) : 64u;
-#pragma unroll 16
-    for (uint32_t k = 0; k < n; k++) {
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const float ck = (uint32_t)k < n ? __shfl(c, k) : 0.f;
+#pragma unroll
+      for (int i = 0; i < NP; i++) acc[i] += ck * pre[k][i];
+    }
+    for (uint32_t k = 16; k < n; k++) {
       const float ck = __shfl(c, (int)k);
       const float* pp = base + (s0 + k) * stride + lane * NP;
-      if constexpr (NP == 1) {
-        acc[0] += ck * pp[0];
-      } else if constexpr (NP == 2) {
-        const float2 v = *(const float2*)pp;
-        acc[0] += ck * v.x;
-        acc[1] += ck * v.y;
-      } else {
 #pragma unroll
-        for (int i = 0; i < NP; i += 4) {
-          const float4 v = *(const float4*)(pp + i);
-          acc[i] += ck * v.x;
-          acc[i + 1] += ck * v.y;
-          acc[i + 2] += ck * v.z;
-          acc[i + 3] += ck * v.w;
-        }
-      }
+      for (int i = 0; i < NP; i++) acc[i] += ck * pp[i];
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
@@ -204,12 +211,13 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
 template <int KVT, int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD>(), waves_per_eu<HD>())))
 void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q, float* out,
-                        float* part) {
+                        float* part, MergeCopy mc) {
   constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
   constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
   using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
+  copy_merges(mc);
   if (wi >= n_items) return;
   const DecodeItem it = items[wi];
   const int seq = (int)it.seq;
@@ -389,13 +397,14 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
 template <int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
                                                                 uint32_t n_items, const float* q, float* out,
-                                                                float* part) {
+                                                                float* part, MergeCopy mc) {
   constexpr int NG = 16;
   constexpr int ND = HDV / 64 > 0 ? HDV / 64 : 1;  // dims per lane in P.V
   __shared__ float qs[WAVES][NG][HD];
   __shared__ float ps[WAVES][NG][64];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t wi = blockIdx.x * WAVES + w;
+  copy_merges(mc);
   const bool active = wi < n_items;
   DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, 0, 0};
   const uint32_t ng = r.ng;
@@ -419,26 +428,59 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
 #pragma unroll
     for (int i = 0; i < ND; i++) o[h][i] = 0.f;
   }
+  // Per 64-key chunk: lane = key for Q.K, lane = dim for P.V. The memory round trips overlap: the
+  // chunk's block ids come from the previous chunk's prefetch, its first 16 V rows are requested
+  // with its K rows (before any score), and each later group of 16 V rows is requested while the
+  // previous one is being accumulated. Keys past the range re-read a valid key's row with
+  // weight 0.
+  auto blk_of = [&](uint32_t c0) {
+    const uint32_t key = c0 + lane;
+    return tab[(key < it.p1 ? key : it.p0) >> g.bt_shift];
+  };
+  int blk = blk_of(it.p0);
+  auto load_v16 = [&](float (&vv)[16][ND], uint32_t c0, uint32_t k0, uint32_t nk) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const uint32_t kq = (k0 + j < nk) ? k0 + j : nk - 1;
+      const int b2 = __builtin_amdgcn_readlane(blk, (int)kq);  // lane kq resolved key c0 + kq's block
+      const uint32_t ib = (c0 + kq) & bt_mask;
+      const float* vrow = (const float*)(g.pool + (size_t)b2 * g.block_bytes + g.v_off + it.kvh * g.v_head +
+                                         (ib >> 4) * g.v_tile) + (ib & 15u) * HDV;
+#pragma unroll
+      for (int i = 0; i < ND; i++) vv[j][i] = (lane + 64 * i < (uint32_t)HDV) ? vrow[lane + 64 * i] : 0.f;
+    }
+  };
   for (uint32_t c0 = it.p0; c0 < it.p1; c0 += 64) {
     const uint32_t key = c0 + lane;
     const bool valid = key < it.p1;
     const uint32_t kk = valid ? key : it.p0;
-    const int blk = tab[kk >> g.bt_shift];
     const uint32_t in_blk = kk & bt_mask;
     const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
     const float* krow = (const float*)(base + g.k_off + it.kvh * g.k_head + (in_blk >> 4) * g.k_tile) + (in_blk & 15u) * HD;
+    const uint32_t nk = (it.p1 - c0) < 64u ? (it.p1 - c0) : 64u;
+    // hd <= 128: K row and two groups of V rows in registers; hd 256 streams K and single-buffers V
+    constexpr bool PRE = HD <= 128;
+    float4 kr[PRE ? HD / 4 : 1];
+    if constexpr (PRE) {
+#pragma unroll
+      for (int d = 0; d < HD / 4; d++) kr[d] = *(const float4*)(krow + 4 * d);
+    }
+    float vv[PRE ? 2 : 1][16][ND];
+    load_v16(vv[0], c0, 0, nk);
+    const int blk_next = (c0 + 64 < it.p1) ? blk_of(c0 + 64) : blk;
     float s[NG];
 #pragma unroll
     for (int h = 0; h < NG; h++) s[h] = 0.f;
-    for (int d = 0; d < HD; d += 4) {
-      const float4 kv = *(const float4*)(krow + d);
+#pragma unroll
+    for (int d = 0; d < HD / 4; d++) {
+      const float4 kv = PRE ? kr[PRE ? d : 0] : *(const float4*)(krow + 4 * d);
 #pragma unroll
       for (int h = 0; h < NG; h++) {
         if (h < (int)nh) {
-          s[h] = fmaf(qs[w][h][d], kv.x, s[h]);
-          s[h] = fmaf(qs[w][h][d + 1], kv.y, s[h]);
-          s[h] = fmaf(qs[w][h][d + 2], kv.z, s[h]);
-          s[h] = fmaf(qs[w][h][d + 3], kv.w, s[h]);
+          s[h] = fmaf(qs[w][h][4 * d], kv.x, s[h]);
+          s[h] = fmaf(qs[w][h][4 * d + 1], kv.y, s[h]);
+          s[h] = fmaf(qs[w][h][4 * d + 2], kv.z, s[h]);
+          s[h] = fmaf(qs[w][h][4 * d + 3], kv.w, s[h]);
         }
       }
     }
@@ -463,22 +505,12 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // P.V in batches of 16 keys whose V rows are all loaded before any is used (independent loads
-    // in flight instead of one memory round trip per key). Keys past the range re-read the last
-    // valid key's row with weight 0.
-    const uint32_t nk = (it.p1 - c0) < 64u ? (it.p1 - c0) : 64u;
-    for (uint32_t k0 = 0; k0 < nk; k0 += 16) {
-      float vv[16][ND];
 #pragma unroll
-      for (int j = 0; j < 16; j++) {
-        const uint32_t kq = (k0 + j < nk) ? k0 + j : nk - 1;
-        const int b2 = __builtin_amdgcn_readlane(blk, (int)kq);  // lane kq resolved key c0 + kq's block
-        const uint32_t ib = (c0 + kq) & bt_mask;
-        const float* vrow = (const float*)(g.pool + (size_t)b2 * g.block_bytes + g.v_off + it.kvh * g.v_head +
-                                           (ib >> 4) * g.v_tile) + (ib & 15u) * HDV;
-#pragma unroll
-        for (int i = 0; i < ND; i++) vv[j][i] = (lane + 64 * i < (uint32_t)HDV) ? vrow[lane + 64 * i] : 0.f;
-      }
+    for (int bq = 0; bq < 4; bq++) {
+      const uint32_t k0 = 16 * bq;
+      if (k0 >= nk) break;
+      if (PRE && bq < 3 && k0 + 16 < nk) load_v16(vv[PRE ? (bq + 1) & 1 : 0], c0, k0 + 16, nk);
+      if (!PRE && bq > 0) load_v16(vv[0], c0, k0, nk);
 #pragma unroll
       for (int j = 0; j < 16; j++) {
 #pragma unroll
@@ -486,7 +518,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
           if (h < (int)nh) {
             const float pw = (k0 + j < nk) ? ps[w][h][k0 + j] : 0.f;
 #pragma unroll
-            for (int i = 0; i < ND; i++) o[h][i] = fmaf(pw, vv[j][i], o[h][i]);
+            for (int i = 0; i < ND; i++) o[h][i] = fmaf(pw, vv[PRE ? bq & 1 : 0][j][i], o[h][i]);
           }
         }
       }
@@ -494,6 +526,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    blk = blk_next;
   }
   if (it.slot == NO_SLOT) {
 #pragma unroll
@@ -525,22 +558,22 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
 
 template <int KVT, int HD, int HDV>
 hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                      const float* q, float* out, float* part, hipStream_t s) {
+                      const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s) {
   const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
   if constexpr (KVT == KV_F32) {
-    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
+    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part);
+    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
   }
   return hipGetLastError();
 }
 
 template <int KVT>
 hipError_t dispatch_hd(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                       const float* q, float* out, float* part, hipStream_t s) {
-  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, s);
-  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, s);
-  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, s);
+                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s) {
+  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, mc, s);
+  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, mc, s);
+  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, mc, s);
   return hipErrorInvalidValue;
 }
 
@@ -581,13 +614,13 @@ bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
 }
 
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const float* q, float* out, float* part, hipStream_t s) {
+                         const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s) {
   if (n_items == 0) return hipSuccess;
   switch (g.kv_type) {
-    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, s);
-    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, s);
-    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, s);
-    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, s);
+    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, mc, s);
+    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, mc, s);
+    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, mc, s);
+    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, mc, s);
   }
   return hipErrorInvalidValue;
 }

@@ -124,8 +124,15 @@ hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, cons
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.
+// The merge list of the call (src: staged, host-mapped; dst: device memory), copied by the decode
+// launch for the merge kernel that follows it (n_words = 0: nothing to copy).
+struct MergeCopy {
+  const uint32_t* src;
+  uint32_t* dst;
+  uint32_t n_words;
+};
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const float* q, float* out, float* part, hipStream_t s);
+                         const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s);
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
                         float* out, hipStream_t s);
 // Decode work items (waves) one CU holds at once for a layer's decode kernel (occupancy query).

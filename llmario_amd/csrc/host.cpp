@@ -186,7 +186,7 @@ struct lmh_kv {
   bool table_dirty = true;
   std::vector<PageOp> pending;
   Uploader up;
-  DevBuf part_buf, ops_buf;
+  DevBuf part_buf, ops_buf, merge_buf;
   // ---- per-call host scratch
   std::vector<int32_t> row_seq, row_pos;
   std::vector<DecodeItem> items;
@@ -994,7 +994,11 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   if (kv->decode_capacity[layer] == 0)
     kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd) * kv->n_cu;
   const uint64_t target = std::max<uint64_t>(env_u64("LMH_DECODE_TARGET_ITEMS", kv->decode_capacity[layer]), 1);
-  const uint64_t min_chunk = std::max<uint64_t>(env_u64("LMH_DECODE_MIN_TILES", 8), 1);
+  // Smallest chunk: 8 tiles for the matrix-core kernels (enough work per wave to stream at full
+  // rate); 2 tiles for f32 rows, whose VALU kernel walks keys with dependent loads (latency-bound:
+  // more, shorter items hide it better).
+  const uint64_t min_chunk =
+      std::max<uint64_t>(env_u64("LMH_DECODE_MIN_TILES", kv->kv_type == LMH_KV_F32 ? 2 : 8), 1);
   // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane);
   // grown until the rows' rounded-up split counts fit the target
   auto n_items_for = [&](uint64_t c) {
@@ -1052,6 +1056,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   // the split partials' buffer first: growing it synchronises the device
   if (slots > 0) {
     if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+    if ((e = kv->merge_buf.ensure(merges_bytes)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
   }
   if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
   // A mixed batch runs its decode items on a second stream, beside the prefill kernel (which
@@ -1087,7 +1092,9 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
   if ((e = kv->time_begin(ds, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
-  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, ds);
+  const MergeCopy mc{(const uint32_t*)(ex + items_pad), (uint32_t*)kv->merge_buf.p,
+                     kv->merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
+  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, ds);
   if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
   if ((e = kv->time_end(ds)) != hipSuccess) return kv->hip_fail(e, "event");
   if (overlap) {
@@ -1096,7 +1103,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   }
   if (!kv->merges.empty()) {
     if ((e = kv->time_begin(st, LMH_KERNEL_MERGE)) != hipSuccess) return kv->hip_fail(e, "event");
-    e = launch_merge(r, y.hdv, (const MergeItem*)(ex + items_pad), (uint32_t)kv->merges.size(),
+    e = launch_merge(r, y.hdv, (const MergeItem*)kv->merge_buf.p, (uint32_t)kv->merges.size(),
                      (const float*)kv->part_buf.p, out, st);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
     if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
