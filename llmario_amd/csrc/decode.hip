@@ -64,13 +64,17 @@ __device__ inline uint16_t bf16_rne(float x) {
 }
 
 // int8 x4 (packed in a uint32) -> f16 x4, exact.
+// Four int8 codes -> four f16, exactly: each byte biased to unsigned (q ^ 0x80 = q + 128) becomes
+// the low mantissa byte of f16 1024 (0x64xx = 1024 + u, exact for u < 256), then 1152 is
+// subtracted two lanes at a time (packed f16).
 __device__ inline h4 i8x4_to_h4(uint32_t w) {
-  h4 r;
-  r[0] = (_Float16)(float)(int8_t)(w & 0xff);
-  r[1] = (_Float16)(float)(int8_t)((w >> 8) & 0xff);
-  r[2] = (_Float16)(float)(int8_t)((w >> 16) & 0xff);
-  r[3] = (_Float16)(float)(int8_t)(w >> 24);
-  return r;
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t u = w ^ 0x80808080u;
+  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [b0, 0x64, b1, 0x64]
+  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [b2, 0x64, b3, 0x64]
+  const h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+  const h2 a = __builtin_bit_cast(h2, lo) - off, b = __builtin_bit_cast(h2, hi) - off;
+  return h4{a[0], a[1], b[0], b[1]};
 }
 
 // bf16 x4 (two uint32) -> f16 x4 (exact for normal f16 range).
@@ -317,24 +321,40 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
       const uint32_t key = kbase + rr;
       sc[rr] = (key >= it.p0 && key < it.p1) ? s[rr] * r.scale_log2 : -INFINITY;
     }
-    float tm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    tm = xmax_groups(tm);
-    const float mn = fmaxf(m, tm);
-    const float alpha = exp2_fast(m - mn);
+    // Lazy reference max: m (per head) moves only when a score exceeds it by more than 8, so
+    // p = 2^(s - m) <= 2^8 and O is rescaled on few tiles; each lane checks its own 4 scores and
+    // only a triggered tile reduces the head's max across the lane groups.
+    const float lm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
+    if (__ballot(lm > m + 8.0f)) {
+      const float tm = xmax_groups(lm);
+      const float mn = tm > m + 8.0f ? tm : m;
+      // no key of this head seen yet (m = -inf): O and lsum are still zero
+      const float alpha = mn == m ? 1.f : (m == -INFINITY ? 0.f : exp2_fast(m - mn));
+      lsum *= alpha;
+#pragma unroll
+      for (int j = 0; j < NJ; j++) O[j] *= alpha;
+      m = mn;
+    }
+    const float mref = m == -INFINITY ? 0.f : m;  // every score is -inf while m is
     float p[4];
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) p[rr] = exp2_fast(sc[rr] - mn);
-    lsum = lsum * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = mn;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) O[j] *= alpha;
+    for (int rr = 0; rr < 4; rr++) p[rr] = exp2_fast(sc[rr] - mref);
+    lsum += (p[0] + p[1]) + (p[2] + p[3]);
     // ---- O^T += V^T P^T
     if constexpr (KVT == KV_Q8) {
+      // P times the V scale of each (key, 32-dim block), in packed f16: the lane's scales sit as
+      // [key i][block b] halves, so keys (0, 1) and (2, 3) of block b pair up with one permute.
+      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      constexpr int NCH = HDV / 32;
+      const uint32_t* vsw = (const uint32_t*)cur.vs;
+      const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]}, p23 = h2{(_Float16)p[2], (_Float16)p[3]};
 #pragma unroll
       for (int b = 0; b < HDV / 32; b++) {
-        h4 pb;
-#pragma unroll
-        for (int i = 0; i < 4; i++) pb[i] = (_Float16)(p[i] * scale_at<HDV / 32>(cur.vs, i, b));
+        const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;
+        const uint32_t s01 = __builtin_amdgcn_perm(vsw[(NCH + b) >> 1], vsw[b >> 1], sel);
+        const uint32_t s23 = __builtin_amdgcn_perm(vsw[(3 * NCH + b) >> 1], vsw[(2 * NCH + b) >> 1], sel);
+        const h2 q01 = p01 * __builtin_bit_cast(h2, s01), q23 = p23 * __builtin_bit_cast(h2, s23);
+        const h4 pb = h4{q01[0], q01[1], q23[0], q23[1]};
 #pragma unroll
         for (int jj = 0; jj < 2; jj++) {
           const int j = 2 * b + jj;
