@@ -36,7 +36,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
+def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, warmup_s: float = 0.0):
+    """Time `steps` calls of one configuration after at least `warmup` untimed calls and at least
+    `warmup_s` seconds of them (matrix-core work runs at a lower clock for the first tens of
+    milliseconds of load, so the compute-bound configurations are warmed by time)."""
     import torch
 
     from llmario_amd import harness
@@ -53,10 +56,15 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True):
     segs = Segments(w.segments())
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
-    log(f"[bench] {name}: loaded in {time.perf_counter() - t_load:.1f}s; warmup {warmup}")
-    for _ in range(warmup):
+    t_w = time.perf_counter()
+    n_w = 0
+    while n_w < warmup or time.perf_counter() - t_w < warmup_s:
         hc.attend(0, segs, q, out, w.scale, w.window, sp)
+        n_w += 1
+        if n_w % 16 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
+    log(f"[bench] {name}: loaded in {t_w - t_load:.1f}s; warmup {n_w} calls in {time.perf_counter() - t_w:.3f}s")
 
     def timed(kernel_events: bool):
         """`steps` back-to-back calls between two synchronisations; the step time is the larger of
@@ -160,6 +168,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--extra", default="c1,c3,c4,c5,c5w", help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--extra-warmup-s", type=float, default=0.2,
+                    help="minimum warm-up time of each extra configuration (clock ramp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-config", default="",
                     help="only time this one config (c1..c5, c5w) and print its result dict: the "
@@ -188,14 +198,14 @@ def main():
         sys.exit(1)
     torch.cuda.set_device(0)
     if args.profile_config:
-        res = time_config(args.profile_config, args.steps, args.warmup)
+        res = time_config(args.profile_config, args.steps, args.warmup, warmup_s=args.extra_warmup_s)
         print(json.dumps(res), flush=True)
         return
 
     head = time_config("c2", args.steps, args.warmup)
     extra = {}
     for name in [x for x in args.extra.split(",") if x]:
-        extra[name] = time_config(name, max(5, min(args.steps, 20)), 3)
+        extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

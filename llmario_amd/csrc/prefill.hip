@@ -313,51 +313,64 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
       }
     }
   };
-  // Lazy reference max: m moves (rescaling O and l) only when a relative score exceeds 8, so
-  // p = 2^(s - m) <= 2^8 and O is rarely touched. Each lane checks its own 8 scores per column;
-  // only when some lane needs a move is the column max reduced over the lane groups (the decision
-  // is then the same on every lane of a column), and the half's scores are shifted to the new m.
-  auto rebase = [&](f4 (&S)[2][NCB]) {
-    float lm[NCB];
-    bool need = false;
+  // Lazy reference max: m moves (rescaling O and l) only when the weights of a half grow too
+  // large. Each lane sums its own 8 weights p = 2^(s - m) per column (the row-sum terms, needed
+  // anyway); a sum above 2^12 (some relative score above 9: every score <= 8 gives a sum <= 2^11)
+  // or a column with no visible key yet sends the wave to the rare path, where the column max is
+  // reduced over the lane groups and m moves to it if it exceeds m + 8 (or is the first finite
+  // score). So every weight converted to f16 is <= 2^12, and O is almost never rescaled. The
+  // scores of the next half, already computed against the old m, are shifted with it.
+  auto expo = [&](const f4 (&S)[2][NCB], float (&pw)[NCB][8], float (&ps)[NCB]) {
 #pragma unroll
     for (int cb = 0; cb < NCB; cb++) {
-      lm[cb] = fmaxf(fmaxf(fmaxf(S[0][cb][0], S[0][cb][1]), fmaxf(S[0][cb][2], S[0][cb][3])),
-                     fmaxf(fmaxf(S[1][cb][0], S[1][cb][1]), fmaxf(S[1][cb][2], S[1][cb][3])));
-      need |= lm[cb] > thr[cb];
-    }
-    if (__ballot(need)) {
-#pragma unroll
-      for (int cb = 0; cb < NCB; cb++) {
-        const float tmax = max_over_groups(lm[cb]);
-        const bool mv = tmax > thr[cb];
-        // no key seen yet (thr = -inf): O and l are zero, and tmax may be any finite value
-        const float alpha = !mv ? 1.f : (thr[cb] == -INFINITY ? 0.f : exp2_fast(-tmax));
-        const float sh = mv ? tmax : 0.f;
-        l[cb] *= alpha;
-#pragma unroll
-        for (int j = 0; j < NJ; j++) O[j][cb] *= alpha;
-#pragma unroll
-        for (int kk = 0; kk < 2; kk++) S[kk][cb] -= sh;
-        nm[cb] -= sh;
-        nmv[cb] = f4{nm[cb], nm[cb], nm[cb], nm[cb]};
-        thr[cb] = mv ? 8.0f : thr[cb];
-      }
-    }
-  };
-  // P = 2^(s - m) rounded to f16 (<= 2^8), row sums in f32
-  auto softmax = [&](const f4 (&S)[2][NCB], h8 (&P)[NCB]) {
-#pragma unroll
-    for (int cb = 0; cb < NCB; cb++) {
-      float pv[8];
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) pv[kk * 4 + r] = exp2_fast(S[kk][cb][r]);
+        for (int r = 0; r < 4; r++) pw[cb][kk * 4 + r] = exp2_fast(S[kk][cb][r]);
       }
-      l[cb] += ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-      P[cb] = h8{(_Float16)pv[0], (_Float16)pv[1], (_Float16)pv[2], (_Float16)pv[3],
-                 (_Float16)pv[4], (_Float16)pv[5], (_Float16)pv[6], (_Float16)pv[7]};
+      ps[cb] = ((pw[cb][0] + pw[cb][1]) + (pw[cb][2] + pw[cb][3])) +
+               ((pw[cb][4] + pw[cb][5]) + (pw[cb][6] + pw[cb][7]));
+    }
+  };
+  auto rebase = [&](f4 (&S)[2][NCB], f4 (&Sn)[2][NCB]) {
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      const float lm = fmaxf(fmaxf(fmaxf(S[0][cb][0], S[0][cb][1]), fmaxf(S[0][cb][2], S[0][cb][3])),
+                             fmaxf(fmaxf(S[1][cb][0], S[1][cb][1]), fmaxf(S[1][cb][2], S[1][cb][3])));
+      const float tmax = max_over_groups(lm);
+      const bool mv = tmax > thr[cb];
+      // no key seen yet (thr = -inf): O and l are zero, and tmax may be any finite value
+      const float alpha = !mv ? 1.f : (thr[cb] == -INFINITY ? 0.f : exp2_fast(-tmax));
+      const float sh = mv ? tmax : 0.f;
+      l[cb] *= alpha;
+#pragma unroll
+      for (int j = 0; j < NJ; j++) O[j][cb] *= alpha;
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++) {
+        S[kk][cb] -= sh;
+        Sn[kk][cb] -= sh;
+      }
+      nm[cb] -= sh;
+      nmv[cb] = f4{nm[cb], nm[cb], nm[cb], nm[cb]};
+      thr[cb] = mv ? 8.0f : thr[cb];
+    }
+  };
+  // P = 2^(s - m) rounded to f16, row sums in f32 (Sn: the next half's scores, see rebase)
+  auto softmax = [&](f4 (&S)[2][NCB], h8 (&P)[NCB], f4 (&Sn)[2][NCB]) {
+    float pw[NCB][8], ps[NCB];
+    expo(S, pw, ps);
+    bool need = false;
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) need |= !(ps[cb] <= 4096.f) || thr[cb] == -INFINITY;
+    if (__ballot(need)) {
+      rebase(S, Sn);
+      expo(S, pw, ps);
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++) {
+      l[cb] += ps[cb];
+      P[cb] = h8{(_Float16)pw[cb][0], (_Float16)pw[cb][1], (_Float16)pw[cb][2], (_Float16)pw[cb][3],
+                 (_Float16)pw[cb][4], (_Float16)pw[cb][5], (_Float16)pw[cb][6], (_Float16)pw[cb][7]};
     }
   };
   // O^T += V^T P^T over a half, 32 keys per MFMA
@@ -370,16 +383,19 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
     }
   };
 
-  // Pipeline. Tile ti's loads are issued at the start of iteration ti-2 and published (waited
-  // for, widened, barrier) in the middle of iteration ti-1, right before the block that finishes
-  // tile ti-1 (softmax + P.V of its second half) and starts tile ti (Q.K of its first half), so
-  // the matrix products of one half always have the other half's exponentials beside them.
+  // Pipeline. Tile ti's loads are issued at the start of iteration ti-2. In iteration ti-1
+  // each thread waits for its own share of them and widens it (bf16) inside the first block, where
+  // the conversions overlap that block's matrix products; the barrier in the middle of iteration
+  // ti-1 then publishes tile ti, right before the block that finishes tile ti-1 (softmax + P.V of
+  // its second half) and starts tile ti (Q.K of its first half), so the matrix products of one
+  // half always have the other half's exponentials beside them.
   // Stage reuse: tile ti+2 goes to stage (ti+2) % 4, last read while finishing tile ti-2, which
   // every wave completed before the barrier of iteration ti-1. A thread issues 2*CPT loads per
-  // tile, so "at most 2*CPT outstanding" means its share of the older tile has landed.
+  // tile, so "at most 2*CPT outstanding" means its share of the older tile has landed. The last
+  // iteration widens a stage no later tile uses (harmless), which keeps that block branch-free.
   // Every tile is computed (keys outside a column's range are masked), except by waves that own
   // no column at all.
-  auto publish = [&](uint32_t ti) {  // tile ti has landed for everyone after this
+  auto wait_tile = [&](uint32_t ti) {  // this thread's loads of tile ti have landed
     if (ti + 1 < n_tiles) {
       if constexpr (CPT == 1)
         asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
@@ -388,16 +404,17 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
     } else {
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     }
-    settle(ti);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
   };
+  auto sync = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
   f4 S0[2][NCB], S1[2][NCB];
   h8 P[NCB];
   KOps ko;
   VOps vo;
   issue(0);
   if (n_tiles > 1) issue(1);
-  publish(0);
+  wait_tile(0);
+  settle(0);
+  sync();
   if (wave_active) {
     load_k(ko, kv_lds, 0);
     qk(S0, ko);
@@ -412,14 +429,17 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
       load_k(ko, kt, 1);
       load_v(vo, vt, 0);
       if (need_mask) mask(S0, key0);
-      rebase(S0);
+      wait_tile(ti + 1);
+      settle(ti + 1);
       qk(S1, ko);
-      softmax(S0, P);
+      softmax(S0, P, S1);
       pv(P, vo);
       if (need_mask) mask(S1, key0 + 32);
-      rebase(S1);
+    } else {
+      wait_tile(ti + 1);
+      settle(ti + 1);
     }
-    if (ti + 1 < n_tiles) publish(ti + 1);
+    if (ti + 1 < n_tiles) sync();
     if (wave_active) {
       load_v(vo, vt, 1);
       // first half of the next tile (after the last tile: a stale stage, never used), issued
@@ -427,7 +447,7 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
       // next iteration reads S0
       load_k(ko, kv_lds + ((ti + 1) % NSTAGE) * 8 * TILE, 0);
       qk(S0, ko);
-      softmax(S1, P);
+      softmax(S1, P, S0);
       pv(P, vo);
     }
   }
