@@ -95,6 +95,8 @@ struct RowGeom {
 
 // One prefill work unit: KV head `kvh` of sequence `seq`, tokens at positions pos0 .. pos0+n_tok-1
 // which are stacked rows row0 .. row0+n_tok-1 (n_tok * group <= prefill_cols_per_unit()).
+// blk: the block ids of the unit's first 8 key pages (page i of its key range, clamped to the last
+// page), so the first K/V tiles are fetched without waiting for the block table.
 struct PrefillItem {
   uint32_t seq;
   uint32_t kvh;
@@ -102,6 +104,7 @@ struct PrefillItem {
   uint32_t pos0;
   uint32_t n_tok;
   uint32_t pad0, pad1, pad2;
+  uint32_t blk[8];
 };
 
 struct PrefillGeom {

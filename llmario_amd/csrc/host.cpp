@@ -873,7 +873,7 @@ static void assign_prefill_units(std::vector<PrefillItem>& items, uint64_t windo
     load.push({l + work(items[i]), b});
   }
   for (const auto& li : lists) per_wg = std::max<uint32_t>(per_wg, (uint32_t)li.size());
-  std::vector<PrefillItem> out((size_t)n_wg * per_wg, PrefillItem{0, 0, 0, 0, 0, 0, 0, 0});
+  std::vector<PrefillItem> out((size_t)n_wg * per_wg, PrefillItem{});
   for (uint32_t b = 0; b < n_wg; b++)
     for (size_t j = 0; j < lists[b].size(); j++) out[(size_t)b * per_wg + j] = items[lists[b][j]];
   items.swap(out);
@@ -964,8 +964,15 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
         const uint64_t pos0 = sg.pos0 + u, last = pos0 + n_tok - 1;
         const uint64_t lo = (window > 0 && pos0 + 1 > window) ? pos0 + 1 - window : 0;
         max_pages = std::max<uint32_t>(max_pages, (uint32_t)(last / 16 - lo / 16 + 1));
-        for (uint32_t kvh = 0; kvh < y.n_kv; kvh++)
-          kv->pitems.push_back(PrefillItem{(uint32_t)sg.seq, kvh, (uint32_t)(sg.start + u), (uint32_t)pos0, n_tok, 0, 0, 0});
+        PrefillItem it{(uint32_t)sg.seq, 0, (uint32_t)(sg.start + u), (uint32_t)pos0, n_tok, 0, 0, 0, {}};
+        const uint64_t page0 = lo / 16, n_pages = last / 16 - lo / 16 + 1;
+        const int32_t* row = kv->h_table.data() + sg.seq * kv->bps;
+        for (uint64_t b = 0; b < 8; b++)
+          it.blk[b] = (uint32_t)row[((page0 + std::min<uint64_t>(b, n_pages - 1)) << 4) >> kv->bt_shift];
+        for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
+          it.kvh = kvh;
+          kv->pitems.push_back(it);
+        }
       }
       for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
     }

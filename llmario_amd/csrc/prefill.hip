@@ -106,35 +106,6 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
   const uint32_t page0 = lo_first >> 4, page1 = pos_last >> 4;
   const uint32_t n_pages = page1 - page0 + 1;
 
-  // ---- block ids of every key page this unit reads
-  {
-    const int32_t* tab = g.table + (size_t)it.seq * g.bps;
-    for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
-  }
-
-  // ---- this lane's columns (one per 16-column block) and their Q fragments
-  uint32_t cpos[NCB], clo[NCB];
-  bool cval[NCB];
-  h8 qf[NCB][NC];
-#pragma unroll
-  for (int cb = 0; cb < NCB; cb++) {
-    const uint32_t c = w * COLS + cb * 16 + hq;
-    const uint32_t t = c / G, hh = c % G;
-    cval[cb] = t < it.n_tok;
-    cpos[cb] = it.pos0 + (cval[cb] ? t : 0);
-    clo[cb] = (pg.window > 0 && cpos[cb] + 1 > pg.window) ? cpos[cb] + 1 - pg.window : 0;
-    const float* qp = q + ((size_t)(it.row0 + (cval[cb] ? t : 0)) * pg.n_head + it.kvh * G + hh) * HD;
-#pragma unroll
-    for (int ch = 0; ch < NC; ch++) {
-      float4 a = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp) : make_float4(0, 0, 0, 0);
-      float4 b = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp + 4) : make_float4(0, 0, 0, 0);
-      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; i++) qf[cb][ch][i] = (_Float16)(x[i] * pg.scale_log2);
-    }
-  }
-  __syncthreads();
-
   // ---- K/V staging. Tile i covers keys (page0 + 4i)*16 .. +64: 4 K and 4 V page tiles, each
   // R rows of 1 KiB (one wave-wide DMA per row). Every wave issues 2*CPT DMAs per tile, so its
   // block ids are wave-uniform and the addresses scalar.
@@ -158,9 +129,11 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
   const uint64_t k_head = g.k_off + (uint64_t)it.kvh * g.k_head;
   const uint64_t v_head = g.v_off + (uint64_t)it.kvh * g.v_head;
   // block base and 16-token sub-tile index of page tile `tile` of tile ti
+  // (tiles 0 and 1 take their block ids from the unit descriptor, before the list is in LDS)
   auto page = [&](uint32_t ti, uint32_t tile, const uint8_t*& base, uint32_t& sub) {
     const uint32_t p = min(ti * 4 + tile, n_pages - 1);
-    const uint64_t blk = (uint32_t)__builtin_amdgcn_readfirstlane(blk_lds[p]);
+    const uint32_t id = ti < 2 ? units[unit].blk[ti * 4 + tile] : (uint32_t)blk_lds[p];
+    const uint64_t blk = (uint32_t)__builtin_amdgcn_readfirstlane(id);
     sub = (((page0 + p) << 4) & ((1u << g.bt_shift) - 1u)) >> 4;
     base = g.pool + blk * g.block_bytes;
   };
@@ -229,6 +202,48 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
       }
     }
   };
+
+  // ---- unit prologue: the first two tiles' loads go out first (block ids from the descriptor),
+  // then the Q loads and the block-id list, so their round trips overlap; the barrier that
+  // publishes tile 0 also publishes the list.
+  issue(0);
+  if (n_tiles > 1) issue(1);
+  // ---- this lane's columns (one per 16-column block); their Q rows are loaded here and
+  // converted after the block-id list is written, so both round trips overlap
+  uint32_t cpos[NCB], clo[NCB];
+  bool cval[NCB];
+  float4 qraw[NCB][NC][2];
+#pragma unroll
+  for (int cb = 0; cb < NCB; cb++) {
+    const uint32_t c = w * COLS + cb * 16 + hq;
+    const uint32_t t = c / G, hh = c % G;
+    cval[cb] = t < it.n_tok;
+    cpos[cb] = it.pos0 + (cval[cb] ? t : 0);
+    clo[cb] = (pg.window > 0 && cpos[cb] + 1 > pg.window) ? cpos[cb] + 1 - pg.window : 0;
+    const float* qp = q + ((size_t)(it.row0 + (cval[cb] ? t : 0)) * pg.n_head + it.kvh * G + hh) * HD;
+#pragma unroll
+    for (int ch = 0; ch < NC; ch++) {
+      qraw[cb][ch][0] = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp) : make_float4(0, 0, 0, 0);
+      qraw[cb][ch][1] = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp + 4) : make_float4(0, 0, 0, 0);
+    }
+  }
+  // ---- block ids of every key page this unit reads
+  {
+    const int32_t* tab = g.table + (size_t)it.seq * g.bps;
+    for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
+  }
+  // ---- Q fragments: q * scale * log2(e) in f16
+  h8 qf[NCB][NC];
+#pragma unroll
+  for (int cb = 0; cb < NCB; cb++) {
+#pragma unroll
+    for (int ch = 0; ch < NC; ch++) {
+      const float4 a = qraw[cb][ch][0], b = qraw[cb][ch][1];
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int i = 0; i < 8; i++) qf[cb][ch][i] = (_Float16)(x[i] * pg.scale_log2);
+    }
+  }
 
   // Online-softmax state per column. Q carries the scale (q * scale * log2 e), so a product is a
   // score in the log2 domain, and the reference max m rides in as the products' initial
@@ -410,8 +425,6 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
   h8 P[NCB];
   KOps ko;
   VOps vo;
-  issue(0);
-  if (n_tiles > 1) issue(1);
   wait_tile(0);
   settle(0);
   sync();
