@@ -157,6 +157,41 @@ int32_t lmh_kv_gather(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t 
 int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs,
                               void* k_rows, void* v_rows, void* stream);
 
+/* The producer side of the cache, fused: attention_block's per-row tail (forward.rs:427-453;
+ * the Metal sibling is qk_rope_kv_t, misc.metal:195-273). For every row t (sequence, position pos)
+ * of the segments, per head:
+ *   Q heads: optional per-head RMS norm with weight q_norm (per_head_norm, forward.rs:832-838 over
+ *            rms_norm, cpu/src/ops.rs:18-29), then RoPE at pos (rope, ops.rs:46-66), written to
+ *            q_out [n_rows][n_head][hd] f32;
+ *   K heads: the same with k_norm, then stored into the cache at (seq, pos) like lmh_kv_store;
+ *   V heads: optionally a weightless RMS norm (Metal's v_norm, misc.metal:218-226), then stored.
+ * q_in is [n_rows][n_head][q_stride] f32 (q_stride >= hd; the first hd values of each head are
+ * used), k_in [n_rows][n_kv][hd], v_in [n_rows][n_kv][hdv] (device). RoPE: pairs i < rot_dim/2,
+ * (2i, 2i+1) (Normal) or (i, i + rot_dim/2) (Neox), freq = theta^(-2i/rot_dim) in f32 as the
+ * reference computes it, angle = pos * freq_scale * freq (/ freq_div[i] when given: Metal's
+ * per-pair divisors), rotation scaled by attn_factor. q_out may not alias the inputs. */
+#define LMH_ROPE_Q_NORM 1u   /* q_norm weights given: RMS-norm each Q head */
+#define LMH_ROPE_K_NORM 2u   /* k_norm weights given: RMS-norm each K head */
+#define LMH_ROPE_V_NORM 4u   /* weightless RMS norm of each V head */
+#define LMH_ROPE_APPLY 8u    /* rotate (clear on NoPE layers) */
+#define LMH_ROPE_NEOX 16u    /* pair (i, i + rot_dim/2) instead of (2i, 2i+1) */
+typedef struct lmh_rope_params {
+  uint32_t abi_version;   /* LMH_ABI_VERSION */
+  uint32_t flags;         /* LMH_ROPE_* */
+  uint32_t rot_dim;       /* rotated dimensions: even, <= hd */
+  uint32_t q_stride;      /* floats between consecutive Q heads of a row in q_in (0 = hd) */
+  float eps;              /* RMS-norm epsilon */
+  float theta;
+  float freq_scale;       /* linear position scale (1 = none) */
+  float attn_factor;      /* scale of the rotated values (1 = none) */
+  const float* q_norm;    /* device [hd] (LMH_ROPE_Q_NORM) */
+  const float* k_norm;    /* device [hd] (LMH_ROPE_K_NORM) */
+  const float* freq_div;  /* device [rot_dim/2] per-pair angle divisors, or NULL */
+} lmh_rope_params;
+int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs,
+                          const float* q_in, const float* k_in, const float* v_in, float* q_out,
+                          const lmh_rope_params* params, void* stream);
+
 /* attend (forward.rs:585-678) + attend_split (forward.rs:688-807) in one call: every row t of
  * the segments (sequence segs[i].seq, position pos0+j) attends causally to positions
  * p_lo..=pos of its own sequence (p_lo = pos+1-window when window > 0 and pos+1 > window, else 0),
@@ -166,12 +201,13 @@ int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, u
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
-/* Timing hook for benchmarks: when enabled, lmh_attend brackets each kernel it launches with HIP
+/* Timing hook for benchmarks: when enabled, lmh_attend and lmh_qk_rope_store bracket each kernel they launch with HIP
  * events on `stream`; lmh_kv_kernel_time returns the accumulated milliseconds and launch count of
  * one kernel kind since its last read, and resets them (it waits for the recorded events). */
 #define LMH_KERNEL_DECODE 0u
 #define LMH_KERNEL_PREFILL 1u
 #define LMH_KERNEL_MERGE 2u
+#define LMH_KERNEL_ROPE_STORE 3u /* lmh_qk_rope_store's kernel */
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches);
 

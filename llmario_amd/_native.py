@@ -45,6 +45,15 @@ class Seg(C.Structure):
     _fields_ = [("seq", u64), ("start", u64), ("n", u64), ("pos0", u64)]
 
 
+ROPE_Q_NORM, ROPE_K_NORM, ROPE_V_NORM, ROPE_APPLY, ROPE_NEOX = 1, 2, 4, 8, 16
+
+
+class RopeParams(C.Structure):
+    _fields_ = [("abi_version", u32), ("flags", u32), ("rot_dim", u32), ("q_stride", u32),
+                ("eps", C.c_float), ("theta", C.c_float), ("freq_scale", C.c_float),
+                ("attn_factor", C.c_float), ("q_norm", P), ("k_norm", P), ("freq_div", P)]
+
+
 # name -> (restype, argtypes); the exported C ABI, in header order.
 SIGNATURES = {
     "lmh_kv_create": (i32, [C.POINTER(KvOptions), C.POINTER(P)]),
@@ -73,12 +82,13 @@ SIGNATURES = {
     "lmh_kv_store_encoded": (i32, [P, u32, P, u64, P, P, P]),
     "lmh_kv_gather": (i32, [P, u32, P, u64, P, P, P]),
     "lmh_kv_gather_encoded": (i32, [P, u32, P, u64, P, P, P]),
+    "lmh_qk_rope_store": (i32, [P, u32, P, u64, P, P, P, P, C.POINTER(RopeParams), P]),
     "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
     "lmh_kv_set_timing": (i32, [P, i32]),
     "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
 }
 
-KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE = 0, 1, 2
+KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE, KERNEL_ROPE_STORE = 0, 1, 2, 3
 
 _lib = None
 

@@ -113,6 +113,18 @@ struct PrefillGeom {
   uint32_t window;   // 0 = none
 };
 
+// Fused per-row tail of attention_block (see lmh_qk_rope_store): flags as LMH_ROPE_*.
+struct RopeGeom {
+  uint32_t n_head, q_stride, flags, half_rot;  // half_rot: rotated pairs (0 = no rotation)
+  float eps, freq_scale, attn_factor;
+  const float* q_norm;    // [hd] or null
+  const float* k_norm;    // [hd] or null
+  const float* freq_div;  // [half_rot] or null
+  const float* freq;      // [half_rot] theta^(-2i/rot_dim), computed on the host
+};
+constexpr uint32_t ROPE_Q_NORM = 1, ROPE_K_NORM = 2, ROPE_V_NORM = 4, ROPE_APPLY = 8, ROPE_NEOX = 16;
+constexpr uint32_t ROPE_MAX_DIM = 512;  // largest hd / hdv the fused kernel stages per wave
+
 // Launch wrappers (defined in the .hip files). Return hipSuccess or the launch error.
 hipError_t launch_store_f32(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
                             const float* k, const float* v, hipStream_t s);
@@ -124,6 +136,9 @@ hipError_t launch_gather(const PageGeom& g, const int32_t* row_seq, const int32_
 hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos,
                                  uint32_t n_rows, uint8_t* k, uint8_t* v, uint32_t k_row, uint32_t v_row,
                                  hipStream_t s);
+hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int32_t* row_seq, const int32_t* row_pos,
+                                uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
+                                hipStream_t s);
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.

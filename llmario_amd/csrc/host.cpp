@@ -196,8 +196,8 @@ struct lmh_kv {
   std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
   std::vector<uint32_t> ev_kind;
   size_t ev_used = 0;
-  double acc_ms[3] = {0, 0, 0};
-  uint64_t launches[3] = {0, 0, 0};
+  double acc_ms[4] = {0, 0, 0, 0};
+  uint64_t launches[4] = {0, 0, 0, 0};
   std::vector<PrefillItem> pitems;
   std::vector<uint8_t> payload;
   std::string err;
@@ -930,6 +930,51 @@ int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, u
   return kv_io(kv, layer, segs, n_segs, k, v, stream, 3);
 }
 
+int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q_in,
+                          const float* k_in, const float* v_in, float* q_out, const lmh_rope_params* p,
+                          void* stream) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  if (layer >= kv->layers.size()) return kv->fail(LMH_INVALID_ARGUMENT, "layer out of range");
+  if (!p || p->abi_version != LMH_ABI_VERSION) return kv->fail(LMH_INVALID_ARGUMENT, "rope params: null or ABI version");
+  const LayerLayout& y = kv->layers[layer];
+  const bool apply = (p->flags & LMH_ROPE_APPLY) != 0;
+  if (p->flags & ~(LMH_ROPE_Q_NORM | LMH_ROPE_K_NORM | LMH_ROPE_V_NORM | LMH_ROPE_APPLY | LMH_ROPE_NEOX))
+    return kv->fail(LMH_INVALID_ARGUMENT, "unknown rope flag");
+  if (apply && (p->rot_dim == 0 || p->rot_dim % 2 || p->rot_dim > y.hd))
+    return kv->fail(LMH_INVALID_ARGUMENT, "rot_dim must be even and in [2, hd]");
+  const uint32_t q_stride = p->q_stride ? p->q_stride : y.hd;
+  if (q_stride < y.hd) return kv->fail(LMH_INVALID_ARGUMENT, "q_stride < hd");
+  if (((p->flags & LMH_ROPE_Q_NORM) && !p->q_norm) || ((p->flags & LMH_ROPE_K_NORM) && !p->k_norm))
+    return kv->fail(LMH_INVALID_ARGUMENT, "norm flag without weights");
+  if (y.hd > ROPE_MAX_DIM || y.hdv > ROPE_MAX_DIM)
+    return kv->fail(LMH_UNSUPPORTED, "head dimension above 512");
+  uint64_t n_rows;
+  int32_t rc = kv->rows_from(segs, n_segs, n_rows);
+  if (rc != LMH_OK) return rc;
+  if (n_rows == 0) return LMH_OK;
+  if (!q_in || !k_in || !v_in || !q_out) return kv->fail(LMH_INVALID_ARGUMENT, "null data pointer");
+  // rope's per-pair frequency, as the reference forms it in f32 (ops.rs:52):
+  // theta.powf(-(2i as f32) / rot_dim as f32)
+  const uint32_t half_rot = apply ? p->rot_dim / 2 : 0;
+  std::vector<float> freq(std::max<uint32_t>(half_rot, 1), 0.f);
+  for (uint32_t i = 0; i < half_rot; i++) freq[i] = powf(p->theta, -(2.0f * (float)i) / (float)p->rot_dim);
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = kv->flush(st)) != LMH_OK) return rc;
+  const int32_t *rs, *rp;
+  const uint8_t* ex;
+  int slot;
+  if ((rc = kv->stage_rows(freq.data(), freq.size() * 4, nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
+  RopeGeom r{y.n_head, q_stride, p->flags, half_rot, p->eps, p->freq_scale, p->attn_factor,
+             (p->flags & LMH_ROPE_Q_NORM) ? p->q_norm : nullptr, (p->flags & LMH_ROPE_K_NORM) ? p->k_norm : nullptr,
+             apply ? p->freq_div : nullptr, (const float*)ex};
+  hipError_t e;
+  if ((e = kv->time_begin(st, LMH_KERNEL_ROPE_STORE)) != hipSuccess) return kv->hip_fail(e, "event");
+  e = launch_qk_rope_store(kv->geom(layer), r, rs, rp, (uint32_t)n_rows, q_in, k_in, v_in, q_out, st);
+  if (e != hipSuccess) return kv->hip_fail(e, "kernel launch");
+  if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  return kv->release_rows(slot, st);
+}
+
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q, float* out,
                    float scale, uint64_t window, void* stream) {
   if (!kv) return LMH_INVALID_ARGUMENT;
@@ -1125,7 +1170,7 @@ int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
 }
 
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches) {
-  if (!kv || kernel > LMH_KERNEL_MERGE) return LMH_INVALID_ARGUMENT;
+  if (!kv || kernel > LMH_KERNEL_ROPE_STORE) return LMH_INVALID_ARGUMENT;
   hipError_t e = kv->collect_times();
   if (e != hipSuccess) return kv->hip_fail(e, "event timing");
   if (ms) *ms = kv->acc_ms[kernel];

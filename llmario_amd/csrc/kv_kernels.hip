@@ -109,6 +109,113 @@ __global__ void store_f32_kernel(PageGeom g, const int32_t* row_seq, const int32
   store_side(g, sl, true, v + (size_t)row * g.n_kv * g.hdv);
 }
 
+// ---- fused per-row tail of attention_block (forward.rs:427-453; Metal qk_rope_kv_t,
+// misc.metal:195-273): per-head RMS norm, RoPE, Q written out, K and V stored into the pages.
+
+// Encode head h of one row side from the wave's staged values x[0 .. dim) into its page slot.
+// Lane L handles elements L, L+64, ...: a q8_0 block of 32 values is one half wave.
+__device__ void store_head_wave(const PageGeom& g, const Slot& sl, bool is_v, uint32_t h, const float* x,
+                                uint32_t lane) {
+  const Side sd = side(g, is_v);
+  uint8_t* head = sl.base + sd.off + h * sd.head;
+  for (uint32_t d = lane; d < sd.dim; d += 64) {
+    const float v = x[d];
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    switch (g.kv_type) {
+      case KV_F16: *(uint16_t*)(head + o) = f16_bits(v); break;
+      case KV_BF16: *(uint16_t*)(head + o) = bf16_bits(v); break;
+      case KV_F32: *(float*)(head + o) = v; break;
+      case KV_Q8: {
+        // quantize_q8_0 (kv.rs:156-171)
+        float amax = fabsf(v);
+        for (int w = 16; w >= 1; w >>= 1) amax = fmaxf(amax, __shfl_xor(amax, w, 32));
+        const float dsc = amax / 127.0f;
+        const float id = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+        head[o] = (uint8_t)(int8_t)(int32_t)rintf(v * id);
+        if ((d & 31u) == 0) {
+          uint8_t* sp = head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d >> 5)) * 2u;
+          *(uint16_t*)sp = f16_bits(dsc);
+        }
+        break;
+      }
+    }
+  }
+}
+
+// The wave's LDS writes are complete and visible to its other lanes (LDS executes one wave's
+// accesses in order; this also keeps the compiler from moving LDS accesses across it).
+__device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) x += __shfl_xor(x, w);
+  return x;
+}
+
+// One workgroup (4 waves) per row. The row's rotation factors are computed once: the angle in
+// f32 exactly as the reference forms it (pos * freq_scale * freq), its sine and cosine in double
+// and rounded (so they match a correctly rounded sinf/cosf), scaled by attn_factor. Each wave then
+// takes whole heads: stage the head in LDS, RMS-norm it (rms_norm: y = x * (1/sqrt(ss/n + eps)) * w),
+// rotate its pairs (disjoint, so lanes never read what another writes), and write it out.
+__global__ __launch_bounds__(256) void qk_rope_store_kernel(PageGeom g, RopeGeom r, const int32_t* row_seq,
+                                                            const int32_t* row_pos, const float* q, const float* k,
+                                                            const float* v, float* q_out) {
+  __shared__ float2 cs[ROPE_MAX_DIM / 2];
+  __shared__ float hb[4][ROPE_MAX_DIM];
+  const uint32_t row = blockIdx.x;
+  const uint32_t pos = (uint32_t)row_pos[row];
+  for (uint32_t i = threadIdx.x; i < r.half_rot; i += blockDim.x) {
+    float angle = (float)pos * r.freq_scale * r.freq[i];
+    if (r.freq_div) angle = angle / r.freq_div[i];
+    double sn, cn;
+    sincos((double)angle, &sn, &cn);
+    cs[i] = make_float2((float)cn * r.attn_factor, (float)sn * r.attn_factor);
+  }
+  __syncthreads();
+  const Slot sl = locate(g, row_seq[row], pos);
+  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  float* x = hb[w];
+  const uint32_t n_items = r.n_head + 2 * g.n_kv;
+  for (uint32_t it = w; it < n_items; it += 4) {
+    const bool is_q = it < r.n_head, is_v = it >= r.n_head + g.n_kv;
+    const uint32_t h = is_q ? it : is_v ? it - r.n_head - g.n_kv : it - r.n_head;
+    const uint32_t dim = is_v ? g.hdv : g.hd;
+    const float* src = is_q ? q + ((size_t)row * r.n_head + h) * r.q_stride
+                            : is_v ? v + ((size_t)row * g.n_kv + h) * g.hdv : k + ((size_t)row * g.n_kv + h) * g.hd;
+    const float* nw = is_q ? r.q_norm : is_v ? nullptr : r.k_norm;
+    const bool norm = is_q ? (r.flags & ROPE_Q_NORM) != 0 : is_v ? (r.flags & ROPE_V_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0;
+    float ss = 0.f;
+    for (uint32_t d = lane; d < dim; d += 64) {
+      const float val = src[d];
+      x[d] = val;
+      ss += val * val;
+    }
+    if (norm) {
+      const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)dim + r.eps);
+      for (uint32_t d = lane; d < dim; d += 64) x[d] = nw ? x[d] * scale * nw[d] : x[d] * scale;
+    }
+    wave_lds_sync();
+    if (!is_v && r.half_rot) {
+      const bool neox = (r.flags & ROPE_NEOX) != 0;
+      for (uint32_t i = lane; i < r.half_rot; i += 64) {
+        const uint32_t a = neox ? i : 2 * i, b = neox ? i + r.half_rot : 2 * i + 1;
+        const float2 c = cs[i];
+        const float x0 = x[a], x1 = x[b];
+        x[a] = x0 * c.x - x1 * c.y;
+        x[b] = x0 * c.y + x1 * c.x;
+      }
+      wave_lds_sync();
+    }
+    if (is_q) {
+      float* dst = q_out + ((size_t)row * r.n_head + h) * g.hd;
+      for (uint32_t d = lane; d < dim; d += 64) dst[d] = x[d];
+    } else {
+      store_head_wave(g, sl, is_v, h, x, lane);
+    }
+    wave_lds_sync();
+  }
+}
+
 // Reference row encoding -> page layout (bit copy, no re-rounding).
 __device__ void store_enc_side(const PageGeom& g, const Slot& sl, bool is_v, const uint8_t* src) {
   const Side sd = side(g, is_v);
@@ -254,6 +361,14 @@ hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, cons
   if (n_rows == 0) return hipSuccess;
   hipLaunchKernelGGL(gather_encoded_kernel, dim3(n_rows), dim3(256), 0, s, g, row_seq, row_pos, k, v, k_row,
                      v_row);
+  return hipGetLastError();
+}
+
+hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int32_t* row_seq, const int32_t* row_pos,
+                                uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
+                                hipStream_t s) {
+  if (n_rows == 0) return hipSuccess;
+  hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
   return hipGetLastError();
 }
 

@@ -210,6 +210,24 @@ class HipKvCache:
         self._check(N.lib().lmh_kv_gather_encoded(self.h, layer, arr, n, C.c_void_p(k_out.data_ptr()),
                                                   C.c_void_p(v_out.data_ptr()), _stream_ptr(stream)))
 
+    def qk_rope_store(self, layer: int, segs, q_in, k_in, v_in, q_out, *, rot_dim: int = 0,
+                      theta: float = 10000.0, neox: bool = False, rope: bool = True, q_norm=None,
+                      k_norm=None, v_norm: bool = False, eps: float = 1e-6, freq_scale: float = 1.0,
+                      attn_factor: float = 1.0, q_stride: int = 0, freq_div=None, stream=None):
+        """attention_block's per-row tail (forward.rs:427-453): QK-norm, RoPE at each row's position,
+        Q written to q_out [n_rows, n_head, hd], K and V stored into the cache. q_in is
+        [n_rows, n_head, q_stride or hd], k_in [n_rows, n_kv, hd], v_in [n_rows, n_kv, hdv] f32 cuda
+        tensors; q_norm / k_norm are [hd] weights (None = no norm), freq_div [rot_dim/2] or None."""
+        hd = self.layers[layer].hd if 0 <= layer < len(self.layers) else 0  # the library checks the layer
+        flags = (N.ROPE_APPLY if rope else 0) | (N.ROPE_NEOX if neox else 0) | (N.ROPE_V_NORM if v_norm else 0)
+        flags |= (N.ROPE_Q_NORM if q_norm is not None else 0) | (N.ROPE_K_NORM if k_norm is not None else 0)
+        ptr = lambda t: C.c_void_p(t.data_ptr()) if t is not None else None
+        p = N.RopeParams(N.ABI_VERSION, flags, int(rot_dim or hd), int(q_stride), float(eps), float(theta),
+                         float(freq_scale), float(attn_factor), ptr(q_norm), ptr(k_norm), ptr(freq_div))
+        arr, n = _segs(segs)
+        self._check(N.lib().lmh_qk_rope_store(self.h, layer, arr, n, ptr(q_in), ptr(k_in), ptr(v_in),
+                                              ptr(q_out), C.byref(p), _stream_ptr(stream)))
+
     def attend(self, layer: int, segs, q, out, scale: float, window: int = 0, stream=None):
         """q: [n_rows, n_head, hd] f32 cuda tensor; out: [n_rows, n_head, hdv] f32."""
         arr, n = _segs(segs)
@@ -223,7 +241,8 @@ class HipKvCache:
     def kernel_time(self, kernel: str = "decode"):
         """(milliseconds, launches) of one kernel kind ("decode" | "prefill" | "merge") since its
         last read (needs set_timing(True) while the calls ran)."""
-        kind = {"decode": N.KERNEL_DECODE, "prefill": N.KERNEL_PREFILL, "merge": N.KERNEL_MERGE}[kernel]
+        kind = {"decode": N.KERNEL_DECODE, "prefill": N.KERNEL_PREFILL, "merge": N.KERNEL_MERGE,
+                "rope_store": N.KERNEL_ROPE_STORE}[kernel]
         ms, n = C.c_double(), N.u64()
         self._check(N.lib().lmh_kv_kernel_time(self.h, kind, C.byref(ms), C.byref(n)))
         return ms.value, n.value

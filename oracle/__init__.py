@@ -50,6 +50,12 @@ class Seg(C.Structure):
     _fields_ = [("seq", u64), ("start", u64), ("n", u64), ("pos0", u64)]
 
 
+class RopeParams(C.Structure):
+    _fields_ = [("apply", C.c_int32), ("neox", C.c_int32), ("v_norm", C.c_int32), ("rot_dim", C.c_uint32),
+                ("eps", C.c_float), ("theta", C.c_float), ("freq_scale", C.c_float),
+                ("attn_factor", C.c_float), ("q_norm", P), ("k_norm", P), ("freq_div", P)]
+
+
 def build(force: bool = False) -> str:
     """Compile liboracle.so with the Makefile next to this file."""
     if force or not os.path.exists(LIB_PATH):
@@ -118,6 +124,10 @@ def lib():
             "orc_attend": (None, [P, u64, P, u64, P, u64, C.c_float, u64, u64, P]),
             "orc_attend_naive_f64": (None, [P, u64, P, u64, P, u64, C.c_double, u64, P]),
             "orc_dot": (C.c_float, [P, P, u64]),
+            "orc_rms_norm": (None, [P, P, C.c_float, P, C.c_size_t]),
+            "orc_rope_apply": (None, [P, C.c_size_t, C.c_size_t, C.c_uint32, C.POINTER(RopeParams)]),
+            "orc_qk_rope": (None, [P, P, P, P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
+                                   C.c_size_t, C.POINTER(RopeParams), P, P, P]),
             "orc_softmax": (None, [P, u64]),
         }
         for name, (res, args) in sig.items():
@@ -191,6 +201,49 @@ def softmax(x) -> np.ndarray:
     x = np.array(x, dtype=np.float32)
     lib().orc_softmax(_ptr(x), x.size)
     return x
+
+
+def rms_norm(x, w=None, eps: float = 0.0) -> np.ndarray:
+    """rms_norm (ops.rs:18-29); w=None: the weightless form."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    wa = None if w is None else np.ascontiguousarray(w, np.float32)
+    lib().orc_rms_norm(_ptr(x), None if wa is None else _ptr(wa), eps, _ptr(y), x.size)
+    return y
+
+
+def rope_params(rot_dim: int, theta: float = 10000.0, neox: bool = False, apply: bool = True,
+                freq_scale: float = 1.0, attn_factor: float = 1.0, eps: float = 1e-6, q_norm=None,
+                k_norm=None, v_norm: bool = False, freq_div=None):
+    """RopeParams plus the arrays it points to (kept alive in the returned tuple)."""
+    keep = [None if a is None else np.ascontiguousarray(a, np.float32) for a in (q_norm, k_norm, freq_div)]
+    p = RopeParams(int(apply), int(neox), int(v_norm), rot_dim, eps, theta, freq_scale, attn_factor,
+                   *[None if a is None else _ptr(a) for a in keep])
+    return p, keep
+
+
+def rope(x, n_heads: int, hd: int, pos: int, **kw) -> np.ndarray:
+    """rope (ops.rs:46-66) on a copy of x [n_heads * hd]."""
+    y = np.array(x, np.float32, copy=True)
+    p, keep = rope_params(kw.pop("rot_dim", hd), **kw)
+    lib().orc_rope_apply(_ptr(y), n_heads, hd, pos, C.byref(p))
+    return y
+
+
+def qk_rope(q_in, k_in, v_in, pos, n_head: int, n_kv: int, hd: int, hdv: int, q_stride: int = 0, **kw):
+    """attention_block's per-row tail (forward.rs:427-453): returns (q_out, k_out, v_out) f32."""
+    q_in = np.ascontiguousarray(q_in, np.float32)
+    k_in = np.ascontiguousarray(k_in, np.float32)
+    v_in = np.ascontiguousarray(v_in, np.float32)
+    pos = np.ascontiguousarray(pos, np.uint32)
+    n = len(pos)
+    q_out = np.empty((n, n_head, hd), np.float32)
+    k_out = np.empty((n, n_kv, hd), np.float32)
+    v_out = np.empty((n, n_kv, hdv), np.float32)
+    p, keep = rope_params(kw.pop("rot_dim", hd), **kw)
+    lib().orc_qk_rope(_ptr(q_in), _ptr(k_in), _ptr(v_in), _ptr(pos), n, n_head, n_kv, hd, hdv, q_stride or hd,
+                      C.byref(p), _ptr(q_out), _ptr(k_out), _ptr(v_out))
+    return q_out, k_out, v_out
 
 
 def attend_splits(n_rows: int, n_kv: int, threads: int, span: int) -> int:

@@ -489,6 +489,49 @@ void softmax(float* x, size_t n) {
   for (size_t i = 0; i < n; i++) x[i] *= inv;
 }
 
+// ---------------------------------------------------------------------------------------------
+// the cache's producer side: QK-norm and RoPE (cpu/src/ops.rs:18-66, forward.rs:427-453, 832-838)
+// ---------------------------------------------------------------------------------------------
+
+// rms_norm (ops.rs:18-29): y = x * (1 / sqrt(sum(x^2) / n + eps)) * w, the sum taken in order.
+// w == nullptr: the weightless form (Metal's v_norm, misc.metal:218-226).
+void rms_norm(const float* x, const float* w, float eps, float* y, size_t n) {
+  float ss = 0.0f;
+  for (size_t i = 0; i < n; i++) ss += x[i] * x[i];
+  const float scale = 1.0f / std::sqrt(ss / (float)n + eps);
+  for (size_t i = 0; i < n; i++) y[i] = w ? x[i] * scale * w[i] : x[i] * scale;
+}
+
+// per_head_norm (forward.rs:832-838): rms_norm of each hd-long head in place.
+void per_head_norm(float* x, size_t n_heads, size_t hd, const float* w, float eps) {
+  std::vector<float> tmp(hd);
+  for (size_t h = 0; h < n_heads; h++) {
+    rms_norm(x + h * hd, w, eps, tmp.data(), hd);
+    std::memcpy(x + h * hd, tmp.data(), hd * 4);
+  }
+}
+
+// rope (ops.rs:46-66): pairs i < rot_dim/2 rotate by angle = pos * freq_scale * freq with
+// freq = theta^(-2i/rot_dim) in f32; (2i, 2i+1) for Normal, (i, i + rot_dim/2) for Neox; the
+// rotation is scaled by attn_factor. freq_div (Metal's per-pair divisors, misc.metal:252-256)
+// divides the angle when given.
+void rope(float* x, size_t n_heads, size_t hd, uint32_t pos, const orc_rope_params* p) {
+  const size_t half = p->rot_dim / 2;
+  for (size_t h = 0; h < n_heads; h++) {
+    float* head = x + h * hd;
+    for (size_t i = 0; i < half; i++) {
+      const float freq = std::pow(p->theta, -(2.0f * (float)i) / (float)p->rot_dim);
+      float angle = (float)pos * p->freq_scale * freq;
+      if (p->freq_div) angle = angle / p->freq_div[i];
+      const float sn = std::sin(angle) * p->attn_factor, cs = std::cos(angle) * p->attn_factor;
+      const size_t a = p->neox ? i : 2 * i, b = p->neox ? i + half : 2 * i + 1;
+      const float x0 = head[a], x1 = head[b];
+      head[a] = x0 * cs - x1 * sn;
+      head[b] = x0 * sn + x1 * cs;
+    }
+  }
+}
+
 // ThreadPool::parallel_for (cpu/src/pool.rs:115-180): `n_chunks = threads` contiguous chunks of
 // ceil(n / n_chunks); the caller runs chunks too. Workers are spawned per call here (the
 // reference parks a persistent pool); the work split is the same.
@@ -836,6 +879,29 @@ uint64_t orc_attend_splits(uint64_t n_rows, uint64_t n_kv, uint64_t threads, uin
   return attend_splits(n_rows, n_kv, threads, span);
 }
 
+void orc_rms_norm(const float* x, const float* w, float eps, float* y, size_t n) { rms_norm(x, w, eps, y, n); }
+void orc_rope_apply(float* x, size_t n_heads, size_t hd, uint32_t pos, const orc_rope_params* p) { rope(x, n_heads, hd, pos, p); }
+// attention_block's per-row tail (forward.rs:427-453): QK-norm, RoPE at each row's position; q_out
+// [n][n_head][hd], k_out [n][n_kv][hd], v_out [n][n_kv][hdv] (f32, before the cache encoding).
+void orc_qk_rope(const float* q_in, const float* k_in, const float* v_in, const uint32_t* pos, size_t n_rows,
+                 size_t n_head, size_t n_kv, size_t hd, size_t hdv, size_t q_stride, const orc_rope_params* p,
+                 float* q_out, float* k_out, float* v_out) {
+  for (size_t t = 0; t < n_rows; t++) {
+    float* q = q_out + t * n_head * hd;
+    float* k = k_out + t * n_kv * hd;
+    float* v = v_out + t * n_kv * hdv;
+    for (size_t h = 0; h < n_head; h++) std::memcpy(q + h * hd, q_in + (t * n_head + h) * q_stride, hd * 4);
+    std::memcpy(k, k_in + t * n_kv * hd, n_kv * hd * 4);
+    std::memcpy(v, v_in + t * n_kv * hdv, n_kv * hdv * 4);
+    if (p->q_norm) per_head_norm(q, n_head, hd, p->q_norm, p->eps);
+    if (p->k_norm) per_head_norm(k, n_kv, hd, p->k_norm, p->eps);
+    if (p->v_norm) per_head_norm(v, n_kv, hdv, nullptr, p->eps);
+    if (p->apply) {
+      rope(q, n_head, hd, pos[t], p);
+      rope(k, n_kv, hd, pos[t], p);
+    }
+  }
+}
 float orc_dot(const float* a, const float* b, uint64_t n) { return dot(a, b, n); }
 void orc_softmax(float* x, uint64_t n) { softmax(x, n); }
 

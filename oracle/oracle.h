@@ -150,6 +150,23 @@ void orc_attend_naive_f64(const orc_cache* c, uint64_t l, const orc_seg* segs, u
 float orc_dot(const float* a, const float* b, uint64_t n);
 void orc_softmax(float* x, uint64_t n);
 
+/* ---- QK-norm + RoPE (cpu/src/ops.rs:18-66, model/src/forward.rs:427-453, 832-838) ---- */
+typedef struct orc_rope_params {
+  int32_t apply;        /* rotate (0 on NoPE layers) */
+  int32_t neox;         /* pair (i, i + rot_dim/2) instead of (2i, 2i+1) */
+  int32_t v_norm;       /* weightless RMS norm of each V head (Metal misc.metal:218-226) */
+  uint32_t rot_dim;
+  float eps, theta, freq_scale, attn_factor;
+  const float* q_norm;  /* [hd] or NULL */
+  const float* k_norm;  /* [hd] or NULL */
+  const float* freq_div; /* [rot_dim/2] or NULL */
+} orc_rope_params;
+void orc_rms_norm(const float* x, const float* w, float eps, float* y, size_t n);
+void orc_rope_apply(float* x, size_t n_heads, size_t hd, uint32_t pos, const orc_rope_params* p);
+void orc_qk_rope(const float* q_in, const float* k_in, const float* v_in, const uint32_t* pos, size_t n_rows,
+                 size_t n_head, size_t n_kv, size_t hd, size_t hdv, size_t q_stride, const orc_rope_params* p,
+                 float* q_out, float* k_out, float* v_out);
+
 #ifdef __cplusplus
 }
 #endif
