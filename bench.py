@@ -8,8 +8,9 @@ wall time per step, from a timed run without per-kernel events; `roofline` = the
 algorithmic bytes / its average duration from HIP events recorded around every launch on the
 launch stream during a second timed run of the same steps.
 
-Also reported (extra keys): every other configuration's throughput and roofline fraction, and the
-CPU baseline (the C++ restatement of the reference's CPU attention, oracle/, on host cores).
+Also reported (extra keys): every other configuration's throughput and roofline fraction, the
+fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, and the CPU baseline
+(the C++ restatement of the reference's CPU attention, oracle/, on host cores).
 """
 
 from __future__ import annotations
@@ -111,6 +112,64 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
     return res
 
 
+def time_rope_store(steps: int, warmup_s: float):
+    """The fused producer (lmh_qk_rope_store) on c3's rows: 4 x 2048 new tokens, 32 Q / 8 KV heads,
+    hd 128, bf16 pages; QK-norm on, Neox RoPE over all 128 dims (a Qwen3-style layer). One step =
+    one call over all 8192 rows. HBM-bound: algorithmic bytes per row = Q, K, V read (f32), Q out
+    written (f32), K and V written in the cache encoding."""
+    import torch
+
+    from llmario_amd.kv import HipKvCache, Layer, Segments
+    from llmario_amd.workloads import config
+
+    w = config("c3")
+    L = w.layer
+    hc = HipKvCache([Layer(L.n_head, L.n_kv, L.hd, L.hdv)], max_ctx=max(w.totals), n_seqs=w.n_seqs,
+                    kv_type=w.kv_type, block_tokens=16)
+    segs_l, n = hc.prepare_batch([(s, w.new[s]) for s in range(w.n_seqs)])
+    segs = Segments(segs_l)
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q = torch.randn((n, L.n_head, L.hd), device="cuda", generator=g)
+    k = torch.randn((n, L.n_kv, L.hd), device="cuda", generator=g)
+    v = torch.randn((n, L.n_kv, L.hdv), device="cuda", generator=g)
+    qw = 1 + torch.rand(L.hd, device="cuda", generator=g)
+    kw = 1 + torch.rand(L.hd, device="cuda", generator=g)
+    q_out = torch.empty_like(q)
+    stream = torch.cuda.current_stream()
+    args = dict(rot_dim=L.hd, theta=1e6, neox=True, q_norm=qw, k_norm=kw, eps=1e-6, stream=stream)
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < warmup_s:
+        for _ in range(8):
+            hc.qk_rope_store(0, segs, q, k, v, q_out, **args)
+        torch.cuda.synchronize()
+    kv_bytes = {"f16": 2, "bf16": 2, "f32": 4}.get(w.kv_type)
+    row = 4 * (2 * L.n_head * L.hd + L.n_kv * (L.hd + L.hdv)) + kv_bytes * L.n_kv * (L.hd + L.hdv)
+    res = {"config": "rope_c3", "rows": n, "bytes": row * n}
+    for events in (False, True):
+        hc.kernel_times()
+        hc.set_timing(events)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hc.qk_rope_store(0, segs, q, k, v, q_out, **args)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        hc.set_timing(False)
+        if events:
+            ms, c = hc.kernel_time("rope_store")
+            res["kernel_ms"] = ms / max(c, 1)
+        else:
+            res["ms_per_step"] = el * 1e3 / steps
+    res["GBps"] = res["bytes"] / (res["ms_per_step"] * 1e-3) / 1e9
+    res["kernel_GBps"] = res["bytes"] / (res["kernel_ms"] * 1e-3) / 1e9
+    res["hbm_frac"] = res["kernel_GBps"] / HBM_PEAK_GBS
+    log(f"[bench] rope_c3: {res['ms_per_step'] * 1e3:.1f} us/step, kernel {res['kernel_ms'] * 1e3:.1f} us, "
+        f"{res['kernel_GBps']:.0f} GB/s ({res['hbm_frac']:.1%} HBM)")
+    del hc
+    torch.cuda.empty_cache()
+    return res
+
+
 def physical_cores() -> int:
     try:
         cores = set()
@@ -166,7 +225,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w", help="other configs to report ('' = none)")
+    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3", help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--extra-warmup-s", type=float, default=0.2,
                     help="minimum warm-up time of each extra configuration (clock ramp)")
@@ -197,6 +256,9 @@ def main():
         print("no GPU visible", file=sys.stderr)
         sys.exit(1)
     torch.cuda.set_device(0)
+    if args.profile_config == "rope_c3":
+        print(json.dumps(time_rope_store(args.steps, args.extra_warmup_s)), flush=True)
+        return
     if args.profile_config:
         res = time_config(args.profile_config, args.steps, args.warmup, warmup_s=args.extra_warmup_s)
         print(json.dumps(res), flush=True)
@@ -205,7 +267,10 @@ def main():
     head = time_config("c2", args.steps, args.warmup)
     extra = {}
     for name in [x for x in args.extra.split(",") if x]:
-        extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
+        if name == "rope_c3":
+            extra[name] = time_rope_store(max(5, min(args.steps, 20)), args.extra_warmup_s)
+        else:
+            extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):

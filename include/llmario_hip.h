@@ -169,7 +169,9 @@ int32_t lmh_kv_gather_encoded(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, u
  * used), k_in [n_rows][n_kv][hd], v_in [n_rows][n_kv][hdv] (device). RoPE: pairs i < rot_dim/2,
  * (2i, 2i+1) (Normal) or (i, i + rot_dim/2) (Neox), freq = theta^(-2i/rot_dim) in f32 as the
  * reference computes it, angle = pos * freq_scale * freq (/ freq_div[i] when given: Metal's
- * per-pair divisors), rotation scaled by attn_factor. q_out may not alias the inputs. */
+ * per-pair divisors), rotation scaled by attn_factor. q_out may not alias the inputs. The layer
+ * must have hd == hdv <= 512 (LMH_UNSUPPORTED otherwise); q_stride is a multiple of 4 and the
+ * four arrays are 16-byte aligned (LMH_INVALID_ARGUMENT otherwise). */
 #define LMH_ROPE_Q_NORM 1u   /* q_norm weights given: RMS-norm each Q head */
 #define LMH_ROPE_K_NORM 2u   /* k_norm weights given: RMS-norm each K head */
 #define LMH_ROPE_V_NORM 4u   /* weightless RMS norm of each V head */

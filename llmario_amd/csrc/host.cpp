@@ -946,8 +946,10 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
   if (q_stride < y.hd) return kv->fail(LMH_INVALID_ARGUMENT, "q_stride < hd");
   if (((p->flags & LMH_ROPE_Q_NORM) && !p->q_norm) || ((p->flags & LMH_ROPE_K_NORM) && !p->k_norm))
     return kv->fail(LMH_INVALID_ARGUMENT, "norm flag without weights");
-  if (y.hd > ROPE_MAX_DIM || y.hdv > ROPE_MAX_DIM)
-    return kv->fail(LMH_UNSUPPORTED, "head dimension above 512");
+  if (y.hd > ROPE_MAX_DIM || y.hdv != y.hd)
+    return kv->fail(LMH_UNSUPPORTED, "the fused kernel takes hd == hdv <= 512");
+  if (q_stride % 4 || ((uintptr_t)q_in | (uintptr_t)k_in | (uintptr_t)v_in | (uintptr_t)q_out) % 16)
+    return kv->fail(LMH_INVALID_ARGUMENT, "q_stride must be a multiple of 4 and the arrays 16-byte aligned");
   uint64_t n_rows;
   int32_t rc = kv->rows_from(segs, n_segs, n_rows);
   if (rc != LMH_OK) return rc;

@@ -146,73 +146,269 @@ __device__ void store_head_wave(const PageGeom& g, const Slot& sl, bool is_v, ui
 // accesses in order; this also keeps the compiler from moving LDS accesses across it).
 __device__ inline void wave_lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
+// Encode head h from per-lane values: lane L holds elements L*VPL .. L*VPL+VPL-1 (dim = 64*VPL).
+// f16/bf16 K: the VPL values are consecutive bytes of one 16-byte operand row (VPL <= 8), one
+// store; V and f32: per element. q8_0: a block of 32 values spans 32/VPL lanes (amax over them).
+template <int VPL>
+__device__ void store_head_lanes(const PageGeom& g, const Slot& sl, bool is_v, uint32_t h, const float (&x)[VPL],
+                                 uint32_t lane) {
+  const Side sd = side(g, is_v);
+  uint8_t* head = sl.base + sd.off + h * sd.head + sl.tile * sd.tile;
+  const uint32_t d0 = lane * VPL;
+  switch (g.kv_type) {
+    case KV_F16:
+    case KV_BF16: {
+      uint16_t b[VPL];
+#pragma unroll
+      for (int c = 0; c < VPL; c++) b[c] = g.kv_type == KV_F16 ? f16_bits(x[c]) : bf16_bits(x[c]);
+      if (!is_v && VPL >= 2) {
+        uint8_t* dst = head + k16_off(sl.m, d0);
+        if constexpr (VPL == 2) *(uint32_t*)dst = b[0] | ((uint32_t)b[1] << 16);
+        else {
+#pragma unroll
+          for (int c = 0; c < VPL; c += 2) *(uint32_t*)(dst + 2 * c) = b[c] | ((uint32_t)b[c + 1] << 16);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < VPL; c++) *(uint16_t*)(head + elem_off(g.kv_type, is_v, sl.m, d0 + c, sd.dim)) = b[c];
+      }
+      break;
+    }
+    case KV_F32: {
+#pragma unroll
+      for (int c = 0; c < VPL; c++) *(float*)(head + elem_off(KV_F32, is_v, sl.m, d0 + c, sd.dim)) = x[c];
+      break;
+    }
+    case KV_Q8: {
+      // quantize_q8_0 (kv.rs:156-171) over blocks of 32 values = 32/VPL lanes
+      float amax = 0.f;
+#pragma unroll
+      for (int c = 0; c < VPL; c++) amax = fmaxf(amax, fabsf(x[c]));
+      for (int m = 16 / VPL; m >= 1; m >>= 1) amax = fmaxf(amax, __shfl_xor(amax, m));
+      const float dsc = amax / 127.0f;
+      const float id = dsc != 0.0f ? 1.0f / dsc : 0.0f;
+#pragma unroll
+      for (int c = 0; c < VPL; c++) head[elem_off(KV_Q8, is_v, sl.m, d0 + c, sd.dim)] = (uint8_t)(int8_t)(int32_t)rintf(x[c] * id);
+      if ((d0 & 31u) == 0) {
+        uint8_t* sp = sl.base + sd.off + h * sd.head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d0 >> 5)) * 2u;
+        *(uint16_t*)sp = f16_bits(dsc);
+      }
+      break;
+    }
+  }
+}
+
 __device__ inline float wave_sum(float x) {
 #pragma unroll
   for (int w = 32; w >= 1; w >>= 1) x += __shfl_xor(x, w);
   return x;
 }
 
-// One workgroup (4 waves) per row. The row's rotation factors are computed once: the angle in
-// f32 exactly as the reference forms it (pos * freq_scale * freq), its sine and cosine in double
-// and rounded (so they match a correctly rounded sinf/cosf), scaled by attn_factor. Each wave then
-// takes whole heads: stage the head in LDS, RMS-norm it (rms_norm: y = x * (1/sqrt(ss/n + eps)) * w),
-// rotate its pairs (disjoint, so lanes never read what another writes), and write it out.
+// One workgroup (4 waves) per row. The row's heads (Q, then K, then V; hd == hdv) are pulled into
+// LDS in chunks of up to ROPE_LDS_FLOATS floats with 16-byte loads spread over all threads, so one
+// round trip fetches a whole row. Meanwhile the rotation factors are computed once per row: the
+// angle in f32 exactly as the reference forms it (pos * freq_scale * freq), its sine and cosine in
+// double and rounded (so they match a correctly rounded sinf/cosf), scaled by attn_factor. Each
+// wave then takes whole heads from LDS: RMS norm (rms_norm: y = x * (1/sqrt(ss/n + eps)) * w),
+// rotation of its pairs (disjoint, so lanes never read what another writes), and the output (Q as
+// f32 rows, K and V encoded into their page slot).
+constexpr uint32_t ROPE_LDS_FLOATS = 8192;  // 32 KiB of staged head values per workgroup
 __global__ __launch_bounds__(256) void qk_rope_store_kernel(PageGeom g, RopeGeom r, const int32_t* row_seq,
                                                             const int32_t* row_pos, const float* q, const float* k,
                                                             const float* v, float* q_out) {
   __shared__ float2 cs[ROPE_MAX_DIM / 2];
-  __shared__ float hb[4][ROPE_MAX_DIM];
-  const uint32_t row = blockIdx.x;
+  __shared__ float wq[ROPE_MAX_DIM], wk[ROPE_MAX_DIM];
+  __shared__ __attribute__((aligned(16))) float buf[ROPE_LDS_FLOATS];
+  const uint32_t row = blockIdx.x, tid = threadIdx.x;
   const uint32_t pos = (uint32_t)row_pos[row];
-  for (uint32_t i = threadIdx.x; i < r.half_rot; i += blockDim.x) {
+  const uint32_t hd = g.hd, f4 = hd / 4;  // float4s per head
+  const uint32_t n_items = r.n_head + 2 * g.n_kv, per_chunk = ROPE_LDS_FLOATS / hd;
+  const uint32_t w = tid >> 6, lane = tid & 63u;
+  auto src_of = [&](uint32_t it) -> const float* {
+    if (it < r.n_head) return q + ((size_t)row * r.n_head + it) * r.q_stride;
+    if (it < r.n_head + g.n_kv) return k + ((size_t)row * g.n_kv + it - r.n_head) * hd;
+    return v + ((size_t)row * g.n_kv + it - r.n_head - g.n_kv) * hd;
+  };
+  Slot sl;  // the row's page slot, looked up once the first loads are in flight
+  const bool neox = (r.flags & ROPE_NEOX) != 0;
+  // A chunk is at most ROPE_LDS_FLOATS / 4 float4s: LPT per thread, all requested before any is
+  // written to LDS (one round trip per chunk); the first chunk's loads overlap the set-up.
+  constexpr uint32_t LPT = ROPE_LDS_FLOATS / 4 / 256;
+  for (uint32_t i0 = 0; i0 < n_items; i0 += per_chunk) {
+    const uint32_t n = min(n_items - i0, per_chunk);
+    if (i0 > 0) __syncthreads();  // every wave is done with the previous chunk
+    float4 tmp[LPT];
+#pragma clang loop unroll(full)
+    for (uint32_t u = 0; u < LPT; u++) {
+      const uint32_t f = tid + u * 256;
+      const bool live = f < n * f4;
+      const float* p = src_of(i0 + (live ? f / f4 : 0)) + (live ? 4 * (f % f4) : 0);
+      tmp[u] = live ? *(const float4*)p : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (i0 == 0) {
+      sl = locate(g, row_seq[row], pos);
+      for (uint32_t i = tid; i < r.half_rot; i += blockDim.x) {
+        float angle = (float)pos * r.freq_scale * r.freq[i];
+        if (r.freq_div) angle = angle / r.freq_div[i];
+        double sn, cn;
+        sincos((double)angle, &sn, &cn);
+        cs[i] = make_float2((float)cn * r.attn_factor, (float)sn * r.attn_factor);
+      }
+      for (uint32_t d = tid; d < hd; d += blockDim.x) {
+        wq[d] = r.q_norm ? r.q_norm[d] : 1.0f;
+        wk[d] = r.k_norm ? r.k_norm[d] : 1.0f;
+      }
+    }
+#pragma clang loop unroll(full)
+    for (uint32_t u = 0; u < LPT; u++) {
+      const uint32_t f = tid + u * 256;
+      if (f < n * f4) *(float4*)(buf + 4 * f) = tmp[u];
+    }
+    __syncthreads();
+    for (uint32_t j = w; j < n; j += 4) {
+      const uint32_t it = i0 + j;
+      const bool is_q = it < r.n_head, is_v = it >= r.n_head + g.n_kv;
+      const bool norm = is_q ? (r.flags & ROPE_Q_NORM) != 0
+                             : is_v ? (r.flags & ROPE_V_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0;
+      float* x = buf + (size_t)j * hd;
+      if (norm) {
+        float ss = 0.f;
+        for (uint32_t d = lane; d < hd; d += 64) ss += x[d] * x[d];
+        const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)hd + r.eps);
+        const float* nw = is_q ? wq : wk;
+        for (uint32_t d = lane; d < hd; d += 64) x[d] = is_v ? x[d] * scale : x[d] * scale * nw[d];
+        wave_lds_sync();
+      }
+      if (!is_v && r.half_rot) {
+        for (uint32_t i = lane; i < r.half_rot; i += 64) {
+          const uint32_t a = neox ? i : 2 * i, b = neox ? i + r.half_rot : 2 * i + 1;
+          const float2 c = cs[i];
+          const float x0 = x[a], x1 = x[b];
+          x[a] = x0 * c.x - x1 * c.y;
+          x[b] = x0 * c.y + x1 * c.x;
+        }
+        wave_lds_sync();
+      }
+      if (is_q) {
+        float4* dst = (float4*)(q_out + ((size_t)row * r.n_head + it) * hd);
+        for (uint32_t o = lane; o < f4; o += 64) dst[o] = *(const float4*)(x + 4 * o);
+      } else {
+        store_head_wave(g, sl, is_v, is_v ? it - r.n_head - g.n_kv : it - r.n_head, x, lane);
+      }
+    }
+  }
+}
+
+// Register fast path of the same computation, for hd == hdv = 64*VPL and a rotated fraction that
+// keeps pair partners a power-of-two lane distance apart (rot_dim*32/hd a power of two, or no
+// rotation): lane L holds elements L*VPL .. L*VPL+VPL-1 of a head, so a head is one vector load
+// per lane, the RMS norm a wave reduction, and a pair partner sits in the same lane (Normal, VPL >=
+// 2) or in lane L ^ m (Neox: m = rot_dim*32/hd; Normal with VPL == 1: m = 1). Each wave loads all
+// its heads of a group before processing any (one round trip per group). The rotation factors are
+// computed once per row in f32 (sincosf, correctly range-reduced; within an ulp of the
+// reference's sinf/cosf) and read by each lane once.
+template <int VPL>
+__global__ __launch_bounds__(256) void qk_rope_store_reg_kernel(PageGeom g, RopeGeom r, const int32_t* row_seq,
+                                                                const int32_t* row_pos, const float* q, const float* k,
+                                                                const float* v, float* q_out) {
+  constexpr uint32_t HD = 64 * VPL;
+  constexpr int GRP = 16;  // heads a wave requests before processing them
+  typedef float fv __attribute__((ext_vector_type(VPL)));
+  __shared__ float2 cs[ROPE_MAX_DIM / 2];
+  const uint32_t row = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+  const uint32_t pos = (uint32_t)row_pos[row];
+  const uint32_t n_items = r.n_head + 2 * g.n_kv;
+  auto src_of = [&](uint32_t it) -> const float* {
+    if (it < r.n_head) return q + ((size_t)row * r.n_head + it) * r.q_stride;
+    if (it < r.n_head + g.n_kv) return k + ((size_t)row * g.n_kv + it - r.n_head) * HD;
+    return v + ((size_t)row * g.n_kv + it - r.n_head - g.n_kv) * HD;
+  };
+  // first group's heads in flight before anything else
+  fv xs[GRP];
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    const uint32_t it = w + 4 * j;
+    xs[j] = it < n_items ? *(const fv*)(src_of(it) + lane * VPL) : fv{};
+  }
+  for (uint32_t i = tid; i < r.half_rot; i += blockDim.x) {
     float angle = (float)pos * r.freq_scale * r.freq[i];
     if (r.freq_div) angle = angle / r.freq_div[i];
-    double sn, cn;
-    sincos((double)angle, &sn, &cn);
-    cs[i] = make_float2((float)cn * r.attn_factor, (float)sn * r.attn_factor);
+    float sn, cn;
+    sincosf(angle, &sn, &cn);
+    cs[i] = make_float2(cn * r.attn_factor, sn * r.attn_factor);
+  }
+  const Slot sl = locate(g, row_seq[row], pos);
+  fv wq, wk;
+#pragma unroll
+  for (int c = 0; c < VPL; c++) {
+    wq[c] = r.q_norm ? r.q_norm[lane * VPL + c] : 1.0f;
+    wk[c] = r.k_norm ? r.k_norm[lane * VPL + c] : 1.0f;
   }
   __syncthreads();
-  const Slot sl = locate(g, row_seq[row], pos);
-  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-  float* x = hb[w];
-  const uint32_t n_items = r.n_head + 2 * g.n_kv;
-  for (uint32_t it = w; it < n_items; it += 4) {
-    const bool is_q = it < r.n_head, is_v = it >= r.n_head + g.n_kv;
-    const uint32_t h = is_q ? it : is_v ? it - r.n_head - g.n_kv : it - r.n_head;
-    const uint32_t dim = is_v ? g.hdv : g.hd;
-    const float* src = is_q ? q + ((size_t)row * r.n_head + h) * r.q_stride
-                            : is_v ? v + ((size_t)row * g.n_kv + h) * g.hdv : k + ((size_t)row * g.n_kv + h) * g.hd;
-    const float* nw = is_q ? r.q_norm : is_v ? nullptr : r.k_norm;
-    const bool norm = is_q ? (r.flags & ROPE_Q_NORM) != 0 : is_v ? (r.flags & ROPE_V_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0;
-    float ss = 0.f;
-    for (uint32_t d = lane; d < dim; d += 64) {
-      const float val = src[d];
-      x[d] = val;
-      ss += val * val;
-    }
-    if (norm) {
-      const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)dim + r.eps);
-      for (uint32_t d = lane; d < dim; d += 64) x[d] = nw ? x[d] * scale * nw[d] : x[d] * scale;
-    }
-    wave_lds_sync();
-    if (!is_v && r.half_rot) {
-      const bool neox = (r.flags & ROPE_NEOX) != 0;
-      for (uint32_t i = lane; i < r.half_rot; i += 64) {
-        const uint32_t a = neox ? i : 2 * i, b = neox ? i + r.half_rot : 2 * i + 1;
-        const float2 c = cs[i];
-        const float x0 = x[a], x1 = x[b];
-        x[a] = x0 * c.x - x1 * c.y;
-        x[b] = x0 * c.y + x1 * c.x;
+  // this lane's rotation factor per element, and whether the element is the pair's first
+  const bool neox = (r.flags & ROPE_NEOX) != 0;
+  const uint32_t half = r.half_rot;
+  const uint32_t pmask = neox ? half / VPL : 1;  // lane distance to the partner when not in-lane
+  float2 cf[VPL];
+  bool first[VPL], rot[VPL];
+#pragma unroll
+  for (int c = 0; c < VPL; c++) {
+    const uint32_t e = lane * VPL + c;
+    rot[c] = e < 2 * half;
+    first[c] = neox ? e < half : (e & 1) == 0;
+    const uint32_t i = neox ? (e < half ? e : e - half) : e >> 1;
+    cf[c] = rot[c] ? cs[i] : make_float2(1.f, 0.f);
+  }
+  for (uint32_t g0 = 0; g0 * 4 < n_items; g0 += GRP) {
+    if (g0 > 0) {
+#pragma unroll
+      for (int j = 0; j < GRP; j++) {
+        const uint32_t it = w + 4 * (g0 + j);
+        xs[j] = it < n_items ? *(const fv*)(src_of(it) + lane * VPL) : fv{};
       }
-      wave_lds_sync();
     }
-    if (is_q) {
-      float* dst = q_out + ((size_t)row * r.n_head + h) * g.hd;
-      for (uint32_t d = lane; d < dim; d += 64) dst[d] = x[d];
-    } else {
-      store_head_wave(g, sl, is_v, h, x, lane);
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      const uint32_t it = w + 4 * (g0 + j);
+      if (it >= n_items) continue;
+      const bool is_q = it < r.n_head, is_v = it >= r.n_head + g.n_kv;
+      const bool norm = is_q ? (r.flags & ROPE_Q_NORM) != 0
+                             : is_v ? (r.flags & ROPE_V_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0;
+      fv x = xs[j];
+      if (norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < VPL; c++) ss += x[c] * x[c];
+        const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)HD + r.eps);
+        const fv nw = is_q ? wq : wk;
+#pragma unroll
+        for (int c = 0; c < VPL; c++) x[c] = is_v ? x[c] * scale : x[c] * scale * nw[c];
+      }
+      if (!is_v && half) {
+        fv p;  // each element's pair partner
+#pragma unroll
+        for (int c = 0; c < VPL; c++) {
+          if (neox || VPL == 1)
+            p[c] = __shfl_xor(x[c], (int)pmask);
+          else
+            p[c] = x[c ^ 1];
+        }
+#pragma unroll
+        for (int c = 0; c < VPL; c++) {
+          if (!rot[c]) continue;
+          // (x0, x1) = (x[a], x[b]): x[a] = x0 cos - x1 sin, x[b] = x0 sin + x1 cos
+          x[c] = first[c] ? x[c] * cf[c].x - p[c] * cf[c].y : p[c] * cf[c].y + x[c] * cf[c].x;
+        }
+      }
+      if (is_q) {
+        *(fv*)(q_out + ((size_t)row * r.n_head + it) * HD + lane * VPL) = x;
+      } else {
+        float xa[VPL];
+#pragma unroll
+        for (int c = 0; c < VPL; c++) xa[c] = x[c];
+        store_head_lanes<VPL>(g, sl, is_v, is_v ? it - r.n_head - g.n_kv : it - r.n_head, xa, lane);
+      }
     }
-    wave_lds_sync();
   }
 }
 
@@ -368,7 +564,22 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
                                 uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
                                 hipStream_t s) {
   if (n_rows == 0) return hipSuccess;
-  hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
+  // register path: hd == hdv = 64*VPL; Normal pairs are always in-lane (VPL >= 2) or one lane
+  // apart; Neox partners are half_rot/VPL lanes apart, which must be a whole power of two
+  const uint32_t vpl = g.hd / 64, half = r.half_rot;
+  const bool neox = (r.flags & ROPE_NEOX) != 0;
+  const bool pairs_ok = half == 0 || !neox || (half % vpl == 0 && ((half / vpl) & (half / vpl - 1)) == 0);
+  const bool reg = g.hd == g.hdv && g.hd % 64 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) && pairs_ok;
+  if (reg) {
+    switch (vpl) {
+      case 1: hipLaunchKernelGGL(qk_rope_store_reg_kernel<1>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 2: hipLaunchKernelGGL(qk_rope_store_reg_kernel<2>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 4: hipLaunchKernelGGL(qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      default: hipLaunchKernelGGL(qk_rope_store_reg_kernel<8>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+    }
+  } else {
+    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
+  }
   return hipGetLastError();
 }
 

@@ -55,6 +55,9 @@ CASES = [
     ("f32", 8, 8, 64, 64, 64, False, True, False, False, 0, True, 1e4),
     ("f16", 4, 1, 256, 256, 128, True, False, True, True, 0, True, 1e6),
     ("bf16", 6, 2, 64, 64, 32, False, True, True, False, 128, False, 1e4),
+    # Neox over 96 of 128 dims: partners 24 lanes apart, so the LDS-staged kernel runs
+    ("f16", 8, 2, 128, 128, 96, True, True, True, True, 0, False, 1e4),
+    ("q8_0", 8, 4, 128, 128, 96, True, False, True, False, 0, True, 1e6),
 ]
 
 
@@ -148,6 +151,7 @@ def test_qk_rope_store_rejects_bad_parameters(cuda):
     assert call(rot_dim=63) == N.INVALID_ARGUMENT
     assert call(rot_dim=66) == N.INVALID_ARGUMENT
     assert call(q_stride=32) == N.INVALID_ARGUMENT
+    assert call(q_stride=66) == N.INVALID_ARGUMENT     # rows must stay 16-byte aligned
     assert call(flags=N.ROPE_APPLY | N.ROPE_Q_NORM) == N.INVALID_ARGUMENT
     assert call(flags=0, rot_dim=0) == N.OK      # NoPE layer: no rotation, rot_dim unused
     with pytest.raises(LmhError):
