@@ -124,6 +124,20 @@ int32_t lmh_kv_block_table(const lmh_kv* kv, uint64_t seq, uint32_t* out, uint64
 /* Test and benchmark hook: give an empty sequence exactly these free blocks, in order (e.g. a
  * seeded permutation of the pool), as if reserve had handed them out. */
 int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, uint64_t n);
+/* ---- snapshots (KvCache::snapshot_bytes / write_seq / read_seq, kv.rs:1009-1130; the disk tier,
+ * server/src/kvtier.rs) ----
+ * A sequence's state is its first ceil(len / block_tokens) blocks in the reference's block format
+ * (per layer K rows then V rows, each in the reference's row encoding), so a snapshot is
+ * byte-identical to the one the reference's CPU cache writes for the same contents (stale slots
+ * past len included). Pair snapshots with lmh_kv_fingerprint, as the reference does. */
+int32_t lmh_kv_snapshot_bytes(const lmh_kv* kv, uint64_t len, uint64_t* bytes);
+/* Writes snapshot_bytes(len(seq)) bytes to `dst` (device memory, `cap` bytes); *written = size. */
+int32_t lmh_kv_write_seq(lmh_kv* kv, uint64_t seq, void* dst, uint64_t cap, uint64_t* written, void* stream);
+/* Replaces the sequence with `len` tokens of snapshot `src` (device memory, n_bytes ==
+ * snapshot_bytes(len)). The sequence's own unshared blocks count as free; without room it fails
+ * with LMH_KV_FULL (needed / free reported) and nothing changes. */
+int32_t lmh_kv_read_seq(lmh_kv* kv, uint64_t seq, uint64_t len, const void* src, uint64_t n_bytes,
+                        uint64_t* needed, uint64_t* free_blocks, void* stream);
 /* BlockPool per-block state (kv/src/lib.rs:146-167) and prefix-cache hooks (lib.rs:112-143). */
 int32_t lmh_pool_refs(const lmh_kv* kv, uint32_t block, uint32_t* refs);
 int32_t lmh_pool_set_hash(lmh_kv* kv, uint32_t block, const uint8_t hash[32]);

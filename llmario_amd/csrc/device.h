@@ -139,6 +139,10 @@ hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, cons
 hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int32_t* row_seq, const int32_t* row_pos,
                                 uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
                                 hipStream_t s);
+// One layer's share of a sequence's snapshot (write: pages -> reference block format; read: the
+// reverse), positions 0 .. n_pos-1.
+hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t n_pos, uint32_t bt, uint64_t bb,
+                           uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s);
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.

@@ -728,6 +728,70 @@ int32_t lmh_kv_clear(lmh_kv* kv, uint64_t seq) {
   return LMH_OK;
 }
 
+// ---- snapshots (kv.rs:1009-1130), paged layers: whole blocks in the reference's block format ----
+int32_t lmh_kv_snapshot_bytes(const lmh_kv* kv, uint64_t len, uint64_t* bytes) {
+  if (!kv || !bytes) return LMH_INVALID_ARGUMENT;
+  *bytes = len == 0 ? 0 : (len + kv->bt - 1) / kv->bt * kv->block_bytes;
+  return LMH_OK;
+}
+
+// One launch per layer over the positions of the sequence's first n_blocks blocks; the layer's
+// region of a reference block starts after the earlier layers' bt*(k_row + v_row) bytes
+// (KvLayout::new, kv.rs:402-497).
+static int32_t snapshot_layers(lmh_kv* kv, bool write, uint64_t seq, uint64_t n_blocks, uint8_t* bytes,
+                               hipStream_t st) {
+  uint64_t ref_off = 0;
+  for (uint32_t l = 0; l < kv->layers.size(); l++) {
+    const LayerLayout& y = kv->layers[l];
+    hipError_t e = launch_snapshot(write, kv->geom(l), (uint32_t)seq, (uint32_t)(n_blocks * kv->bt), kv->bt,
+                                   kv->block_bytes, ref_off, (uint32_t)y.k_row, (uint32_t)y.v_row, bytes, st);
+    if (e != hipSuccess) return kv->hip_fail(e, "snapshot kernel");
+    ref_off += kv->bt * (y.k_row + y.v_row);
+  }
+  return LMH_OK;
+}
+
+int32_t lmh_kv_write_seq(lmh_kv* kv, uint64_t seq, void* dst, uint64_t cap, uint64_t* written, void* stream) {
+  if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  const uint64_t len = kv->seqs[seq].len;
+  uint64_t bytes;
+  lmh_kv_snapshot_bytes(kv, len, &bytes);
+  if (written) *written = bytes;
+  if (bytes == 0) return LMH_OK;
+  if (!dst || cap < bytes) return kv->fail(LMH_INVALID_ARGUMENT, "snapshot destination smaller than snapshot_bytes(len)");
+  hipStream_t st = (hipStream_t)stream;
+  int32_t rc = kv->flush(st);
+  if (rc != LMH_OK) return rc;
+  return snapshot_layers(kv, true, seq, (len + kv->bt - 1) / kv->bt, (uint8_t*)dst, st);
+}
+
+int32_t lmh_kv_read_seq(lmh_kv* kv, uint64_t seq, uint64_t len, const void* src, uint64_t n_bytes, uint64_t* needed,
+                        uint64_t* free_blocks, void* stream) {
+  if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  if (len > kv->max_ctx) return kv->fail(LMH_INVALID_ARGUMENT, "snapshot longer than the context");
+  uint64_t bytes;
+  lmh_kv_snapshot_bytes(kv, len, &bytes);
+  if (n_bytes != bytes || (bytes && !src)) return kv->fail(LMH_INVALID_ARGUMENT, "snapshot size");
+  // room first: clearing frees this sequence's unshared blocks, so they count as available
+  const uint64_t nb = (len + kv->bt - 1) / kv->bt;
+  uint64_t own = 0;
+  for (uint32_t b : kv->seqs[seq].blocks) own += kv->meta[b].refs == 1 ? 1 : 0;
+  if (nb > kv->free_q.size() + own) {
+    if (needed) *needed = nb;
+    if (free_blocks) *free_blocks = kv->free_q.size() + own;
+    return kv->fail(LMH_KV_FULL, "KV cache full: snapshot needs " + std::to_string(nb) + " blocks");
+  }
+  kv->clear(seq);
+  if (len == 0) return LMH_OK;
+  int32_t rc = kv->reserve(seq, len, needed, free_blocks);
+  if (rc != LMH_OK) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if ((rc = kv->flush(st)) != LMH_OK) return rc;
+  if ((rc = snapshot_layers(kv, false, seq, nb, (uint8_t*)src, st)) != LMH_OK) return rc;
+  kv->seqs[seq].len = len;
+  return LMH_OK;
+}
+
 int32_t lmh_kv_block_table(const lmh_kv* kv, uint64_t seq, uint32_t* out, uint64_t cap, uint64_t* n) {
   if (!kv || !n || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
   const auto& b = kv->seqs[seq].blocks;

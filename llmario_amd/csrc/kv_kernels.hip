@@ -516,6 +516,28 @@ __global__ void gather_encoded_kernel(PageGeom g, const int32_t* row_seq, const 
   gather_enc_side(g, sl, true, v + (size_t)row * v_row);
 }
 
+// ---- snapshots (KvCache::write_seq / read_seq, kv.rs:1030-1130): one layer's share of a
+// sequence's blocks in the reference's block format. Snapshot block i is the sequence's block i;
+// inside it, the layer's K rows then V rows (ref_off + slot*k_row, ref_off + bt*k_row + slot*v_row)
+// in the row encoding. One workgroup per position of the covered blocks (every slot, written or
+// not, so the bytes equal the reference's block byte for byte).
+__global__ void snapshot_write_kernel(PageGeom g, uint32_t seq, uint32_t bt, uint64_t bb, uint64_t ref_off,
+                                      uint32_t k_row, uint32_t v_row, uint8_t* out) {
+  const uint32_t p = blockIdx.x, bi = p / bt, j = p % bt;
+  const Slot sl = locate(g, (int)seq, p);
+  uint8_t* blk = out + (size_t)bi * bb + ref_off;
+  gather_enc_side(g, sl, false, blk + (size_t)j * k_row);
+  gather_enc_side(g, sl, true, blk + (size_t)bt * k_row + (size_t)j * v_row);
+}
+__global__ void snapshot_read_kernel(PageGeom g, uint32_t seq, uint32_t bt, uint64_t bb, uint64_t ref_off,
+                                     uint32_t k_row, uint32_t v_row, const uint8_t* in) {
+  const uint32_t p = blockIdx.x, bi = p / bt, j = p % bt;
+  const Slot sl = locate(g, (int)seq, p);
+  const uint8_t* blk = in + (size_t)bi * bb + ref_off;
+  store_enc_side(g, sl, false, blk + (size_t)j * k_row);
+  store_enc_side(g, sl, true, blk + (size_t)bt * k_row + (size_t)j * v_row);
+}
+
 // Zero whole blocks (a newly backed block reads as zeros, like the reference's anonymous
 // mappings, kv.rs:29-37). block_bytes is a multiple of 16.
 __global__ void zero_blocks_kernel(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n) {
@@ -580,6 +602,17 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
   } else {
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t n_pos, uint32_t bt, uint64_t bb,
+                           uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s) {
+  if (n_pos == 0) return hipSuccess;
+  if (write)
+    hipLaunchKernelGGL(snapshot_write_kernel, dim3(n_pos), dim3(256), 0, s, g, seq, bt, bb, ref_off, k_row, v_row, bytes);
+  else
+    hipLaunchKernelGGL(snapshot_read_kernel, dim3(n_pos), dim3(256), 0, s, g, seq, bt, bb, ref_off, k_row, v_row,
+                       (const uint8_t*)bytes);
   return hipGetLastError();
 }
 

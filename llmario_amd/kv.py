@@ -154,6 +154,34 @@ class HipKvCache:
         arr = (N.u32 * max(len(blocks), 1))(*[int(b) for b in blocks])
         self._check(N.lib().lmh_kv_adopt_blocks(self.h, s, arr, len(blocks)))
 
+    # ---- snapshots (kv.rs:1009-1130) -------------------------------------------------------
+    def snapshot_bytes(self, length: int) -> int:
+        v = N.u64()
+        self._check(N.lib().lmh_kv_snapshot_bytes(self.h, length, C.byref(v)))
+        return v.value
+
+    def write_seq(self, s: int, dst=None, stream=None):
+        """The sequence's snapshot into `dst` (a uint8 cuda tensor of at least snapshot_bytes
+        bytes; allocated when None). Returns the tensor trimmed to the snapshot's size."""
+        import torch
+        n = self.snapshot_bytes(self.len(s))
+        if dst is None:
+            dst = torch.empty(max(n, 1), dtype=torch.uint8, device="cuda")
+        w = N.u64()
+        self._check(N.lib().lmh_kv_write_seq(self.h, s, C.c_void_p(dst.data_ptr()), dst.numel(), C.byref(w),
+                                             _stream_ptr(stream)))
+        return dst[:w.value]
+
+    def read_seq(self, s: int, length: int, src, stream=None):
+        """Replace sequence s with `length` tokens of snapshot `src` (uint8 cuda tensor); raises
+        KvFull (nothing changed) when the pool cannot hold it."""
+        nd, fr = N.u64(), N.u64()
+        rc = N.lib().lmh_kv_read_seq(self.h, s, length, C.c_void_p(src.data_ptr()) if src.numel() else None,
+                                     src.numel(), C.byref(nd), C.byref(fr), _stream_ptr(stream))
+        if rc == N.KV_FULL:
+            raise KvFull(nd.value, fr.value, N.lib().lmh_kv_last_error(self.h).decode())
+        self._check(rc)
+
     def refs(self, b: int) -> int:
         v = N.u32()
         self._check(N.lib().lmh_pool_refs(self.h, b, C.byref(v)))

@@ -124,6 +124,9 @@ def lib():
             "orc_attend": (None, [P, u64, P, u64, P, u64, C.c_float, u64, u64, P]),
             "orc_attend_naive_f64": (None, [P, u64, P, u64, P, u64, C.c_double, u64, P]),
             "orc_dot": (C.c_float, [P, P, u64]),
+            "orc_cache_snapshot_bytes": (u64, [P, u64]),
+            "orc_cache_write_seq": (None, [P, u64, P]),
+            "orc_cache_read_seq": (C.c_int, [P, u64, u64, P, u64, P, P]),
             "orc_rms_norm": (None, [P, P, C.c_float, P, C.c_size_t]),
             "orc_rope_apply": (None, [P, C.c_size_t, C.c_size_t, C.c_uint32, C.POINTER(RopeParams)]),
             "orc_qk_rope": (None, [P, P, P, P, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t, C.c_size_t,
@@ -409,6 +412,26 @@ class Cache:
         lib().orc_cache_load_k(self.h, s, l, pos, 0, n_kv * hd, _ptr(k))
         lib().orc_cache_load_v(self.h, s, l, pos, 0, n_kv * hdv, _ptr(v))
         return k, v
+
+    def snapshot_bytes(self, length: int) -> int:
+        return lib().orc_cache_snapshot_bytes(self.h, length)
+
+    def write_seq(self, s: int) -> np.ndarray:
+        """write_seq (kv.rs:1030-1056): the sequence's blocks as bytes."""
+        out = np.zeros(self.snapshot_bytes(self.len(s)), dtype=np.uint8)
+        lib().orc_cache_write_seq(self.h, s, _ptr(out) if out.size else None)
+        return out
+
+    def read_seq(self, s: int, length: int, data: np.ndarray):
+        """read_seq (kv.rs:1058-1130); raises KvFullError (nothing changed) or ValueError."""
+        data = np.ascontiguousarray(data, dtype=np.uint8)
+        nd, fr = u64(0), u64(0)
+        rc = lib().orc_cache_read_seq(self.h, s, length, _ptr(data) if data.size else None, data.size,
+                                      C.byref(nd), C.byref(fr))
+        if rc == KV_FULL:
+            raise KvFullError(nd.value, fr.value)
+        if rc != OK:
+            raise ValueError("invalid snapshot")
 
     def prepare_batch(self, batch):
         """batch: list of (seq, n_tokens). Returns (segs, n_rows) or raises KvFullError."""

@@ -412,6 +412,37 @@ struct orc_cache {
       release_block(b);
     }
   }
+  // snapshot_bytes (kv.rs:1009-1028), paged layers only: whole blocks covering len tokens
+  size_t snapshot_bytes(size_t len) const {
+    if (len == 0 || lay.block_bytes == 0) return 0;
+    return (len + lay.block_tokens - 1) / lay.block_tokens * lay.block_bytes;
+  }
+  // write_seq (kv.rs:1030-1056): the sequence's first ceil(len/bt) blocks, byte for byte
+  void write_seq(size_t s, uint8_t* out) const {
+    const size_t len = seqs[s].len, bt = lay.block_tokens, bb = lay.block_bytes;
+    if (len == 0 || bb == 0) return;
+    for (size_t i = 0; i < (len + bt - 1) / bt; i++) std::memcpy(out + i * bb, backing[seqs[s].blocks[i]].data(), bb);
+  }
+  // read_seq (kv.rs:1058-1130): room first (the sequence's own blocks count as available), else
+  // KvFull with nothing changed; then clear, reserve and copy the blocks in
+  int read_seq(size_t s, size_t len, const uint8_t* bytes, size_t n_bytes, uint64_t* needed, uint64_t* free_) {
+    if (len > lay.max_ctx || n_bytes != snapshot_bytes(len)) return ORC_INVALID;
+    const size_t bt = lay.block_tokens, bb = lay.block_bytes;
+    const size_t nb = bb > 0 ? (len + bt - 1) / bt : 0;
+    size_t own = 0;
+    for (uint32_t b : seqs[s].blocks) own += pool.meta[b].refs == 1 ? 1 : 0;
+    if (nb > pool.free.size() + own) {
+      if (needed) *needed = nb;
+      if (free_) *free_ = pool.free.size() + own;
+      return ORC_KV_FULL;
+    }
+    clear(s);
+    if (len == 0) return ORC_OK;
+    reserve(s, len, nullptr, nullptr);
+    for (size_t i = 0; i < seqs[s].blocks.size(); i++) std::memcpy(backing[seqs[s].blocks[i]].data(), bytes + i * bb, bb);
+    seqs[s].len = len;
+    return ORC_OK;
+  }
   // kv.rs:839-866 (paged branch)
   uint8_t* row_ptr(size_t s, size_t l, size_t pos, bool v) const {
     const Layer& y = lay.layers[l];
@@ -763,6 +794,12 @@ int orc_cache_reserve(orc_cache* c, uint64_t s, uint64_t n, uint64_t* needed, ui
 }
 void orc_cache_truncate(orc_cache* c, uint64_t s, uint64_t n) { c->truncate(s, n); }
 void orc_cache_clear(orc_cache* c, uint64_t s) { c->clear(s); }
+uint64_t orc_cache_snapshot_bytes(const orc_cache* c, uint64_t len) { return c->snapshot_bytes(len); }
+void orc_cache_write_seq(const orc_cache* c, uint64_t s, uint8_t* out) { c->write_seq(s, out); }
+int orc_cache_read_seq(orc_cache* c, uint64_t s, uint64_t len, const uint8_t* bytes, uint64_t n, uint64_t* needed,
+                       uint64_t* free_) {
+  return c->read_seq(s, len, bytes, n, needed, free_);
+}
 uint64_t orc_cache_resident_blocks(const orc_cache* c) {
   uint64_t n = 0;
   for (auto& b : c->backing) n += b.empty() ? 0 : 1;

@@ -150,6 +150,12 @@ void orc_attend_naive_f64(const orc_cache* c, uint64_t l, const orc_seg* segs, u
 float orc_dot(const float* a, const float* b, uint64_t n);
 void orc_softmax(float* x, uint64_t n);
 
+/* ---- snapshots (KvCache::snapshot_bytes / write_seq / read_seq, kv.rs:1009-1130) ---- */
+uint64_t orc_cache_snapshot_bytes(const orc_cache* c, uint64_t len);
+void orc_cache_write_seq(const orc_cache* c, uint64_t s, uint8_t* out);
+int orc_cache_read_seq(orc_cache* c, uint64_t s, uint64_t len, const uint8_t* bytes, uint64_t n, uint64_t* needed,
+                       uint64_t* free_);
+
 /* ---- QK-norm + RoPE (cpu/src/ops.rs:18-66, model/src/forward.rs:427-453, 832-838) ---- */
 typedef struct orc_rope_params {
   int32_t apply;        /* rotate (0 on NoPE layers) */
