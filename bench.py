@@ -9,7 +9,8 @@ algorithmic bytes / its average duration from HIP events recorded around every l
 launch stream during a second timed run of the same steps.
 
 Also reported (extra keys): every other configuration's throughput and roofline fraction, the
-fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, and the CPU baseline
+fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
+of a c4 sequence (`snapshot_c4`), and the CPU baseline
 (the C++ restatement of the reference's CPU attention, oracle/, on host cores).
 """
 
@@ -170,6 +171,54 @@ def time_rope_store(steps: int, warmup_s: float):
     return res
 
 
+def time_snapshot(steps: int, warmup_s: float):
+    """Snapshot write and read (lmh_kv_write_seq / lmh_kv_read_seq) of one c4 sequence: 32768
+    tokens of q8_0 pages, 64 Q / 8 KV heads, hd 128 (2048 blocks of 34,816 bytes = 71.3 MB). The
+    kernels transcode between the page layout and the reference's block format, device to device;
+    algorithmic bytes = the snapshot read once and written once."""
+    import torch
+
+    from llmario_amd import harness
+    from llmario_amd.workloads import Generator, config
+
+    w = config("c4")
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    n = hc.snapshot_bytes(hc.len(0))
+    buf = torch.empty(n, dtype=torch.uint8, device="cuda")
+    res = {"config": "snapshot_c4", "snapshot_bytes": n, "bytes": 2 * n}
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < warmup_s:
+        hc.write_seq(0, buf)
+        torch.cuda.synchronize()
+    for kind in ("write", "read"):
+        hc.kernel_times()
+        hc.set_timing(True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            if kind == "write":
+                hc.write_seq(0, buf)
+            else:
+                hc.read_seq(1, w.totals[0], buf)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        hc.set_timing(False)
+        ms, c = hc.kernel_time("snapshot")
+        k_ms = ms / max(c, 1)
+        res[f"{kind}_ms_per_call"] = el * 1e3 / steps
+        res[f"{kind}_kernel_ms"] = k_ms
+        res[f"{kind}_kernel_GBps"] = 2 * n / (k_ms * 1e-3) / 1e9
+    res["kernel_ms"] = res["write_kernel_ms"]
+    res["kernel_GBps"] = res["write_kernel_GBps"]
+    res["hbm_frac"] = res["kernel_GBps"] / HBM_PEAK_GBS
+    log(f"[bench] snapshot_c4: write {res['write_kernel_ms'] * 1e3:.1f} us ({res['write_kernel_GBps']:.0f} GB/s), "
+        f"read {res['read_kernel_ms'] * 1e3:.1f} us ({res['read_kernel_GBps']:.0f} GB/s) for {n / 1e6:.1f} MB")
+    del hc
+    torch.cuda.empty_cache()
+    return res
+
+
 def physical_cores() -> int:
     try:
         cores = set()
@@ -225,7 +274,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3", help="other configs to report ('' = none)")
+    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3,snapshot_c4",
+                    help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--extra-warmup-s", type=float, default=0.2,
                     help="minimum warm-up time of each extra configuration (clock ramp)")
@@ -259,6 +309,9 @@ def main():
     if args.profile_config == "rope_c3":
         print(json.dumps(time_rope_store(args.steps, args.extra_warmup_s)), flush=True)
         return
+    if args.profile_config == "snapshot_c4":
+        print(json.dumps(time_snapshot(args.steps, args.extra_warmup_s)), flush=True)
+        return
     if args.profile_config:
         res = time_config(args.profile_config, args.steps, args.warmup, warmup_s=args.extra_warmup_s)
         print(json.dumps(res), flush=True)
@@ -269,6 +322,8 @@ def main():
     for name in [x for x in args.extra.split(",") if x]:
         if name == "rope_c3":
             extra[name] = time_rope_store(max(5, min(args.steps, 20)), args.extra_warmup_s)
+        elif name == "snapshot_c4":
+            extra[name] = time_snapshot(max(5, min(args.steps, 20)), args.extra_warmup_s)
         else:
             extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
 

@@ -217,13 +217,14 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
-/* Timing hook for benchmarks: when enabled, lmh_attend and lmh_qk_rope_store bracket each kernel they launch with HIP
+/* Timing hook for benchmarks: when enabled, lmh_attend, lmh_qk_rope_store and the snapshot calls bracket each kernel they launch with HIP
  * events on `stream`; lmh_kv_kernel_time returns the accumulated milliseconds and launch count of
  * one kernel kind since its last read, and resets them (it waits for the recorded events). */
 #define LMH_KERNEL_DECODE 0u
 #define LMH_KERNEL_PREFILL 1u
 #define LMH_KERNEL_MERGE 2u
 #define LMH_KERNEL_ROPE_STORE 3u /* lmh_qk_rope_store's kernel */
+#define LMH_KERNEL_SNAPSHOT 4u   /* lmh_kv_write_seq / lmh_kv_read_seq kernels */
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches);
 

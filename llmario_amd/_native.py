@@ -91,7 +91,7 @@ SIGNATURES = {
     "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
 }
 
-KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE, KERNEL_ROPE_STORE = 0, 1, 2, 3
+KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE, KERNEL_ROPE_STORE, KERNEL_SNAPSHOT = 0, 1, 2, 3, 4
 
 _lib = None
 

@@ -196,8 +196,8 @@ struct lmh_kv {
   std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
   std::vector<uint32_t> ev_kind;
   size_t ev_used = 0;
-  double acc_ms[4] = {0, 0, 0, 0};
-  uint64_t launches[4] = {0, 0, 0, 0};
+  double acc_ms[5] = {0, 0, 0, 0, 0};
+  uint64_t launches[5] = {0, 0, 0, 0, 0};
   std::vector<PrefillItem> pitems;
   std::vector<uint8_t> payload;
   std::string err;
@@ -743,8 +743,11 @@ static int32_t snapshot_layers(lmh_kv* kv, bool write, uint64_t seq, uint64_t n_
   uint64_t ref_off = 0;
   for (uint32_t l = 0; l < kv->layers.size(); l++) {
     const LayerLayout& y = kv->layers[l];
-    hipError_t e = launch_snapshot(write, kv->geom(l), (uint32_t)seq, (uint32_t)(n_blocks * kv->bt), kv->bt,
-                                   kv->block_bytes, ref_off, (uint32_t)y.k_row, (uint32_t)y.v_row, bytes, st);
+    hipError_t e = kv->time_begin(st, LMH_KERNEL_SNAPSHOT);
+    if (e == hipSuccess)
+      e = launch_snapshot(write, kv->geom(l), (uint32_t)seq, (uint32_t)(n_blocks * kv->bt), kv->bt, kv->block_bytes,
+                          ref_off, (uint32_t)y.k_row, (uint32_t)y.v_row, bytes, st);
+    if (e == hipSuccess) e = kv->time_end(st);
     if (e != hipSuccess) return kv->hip_fail(e, "snapshot kernel");
     ref_off += kv->bt * (y.k_row + y.v_row);
   }
@@ -1236,7 +1239,7 @@ int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
 }
 
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches) {
-  if (!kv || kernel > LMH_KERNEL_ROPE_STORE) return LMH_INVALID_ARGUMENT;
+  if (!kv || kernel > LMH_KERNEL_SNAPSHOT) return LMH_INVALID_ARGUMENT;
   hipError_t e = kv->collect_times();
   if (e != hipSuccess) return kv->hip_fail(e, "event timing");
   if (ms) *ms = kv->acc_ms[kernel];

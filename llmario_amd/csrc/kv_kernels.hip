@@ -11,6 +11,8 @@
 // One workgroup per row; these kernels move ~n_kv*(hd+hdv) values per row and are HBM-bound.
 #include "device.h"
 
+#include <algorithm>
+
 namespace lmh {
 namespace {
 
@@ -538,6 +540,82 @@ __global__ void snapshot_read_kernel(PageGeom g, uint32_t seq, uint32_t bt, uint
   store_enc_side(g, sl, true, blk + (size_t)bt * k_row + (size_t)j * v_row);
 }
 
+// Tiled form (used when every head's row segment is a whole number of 4-byte words): one
+// workgroup per (snapshot block, 16-token tile, KV head, side). The page tile (and its q8_0
+// scales) and the tile's 16 row segments (head h of rows t*16 .. t*16+15, h*seg bytes into each
+// row) are staged in LDS; bytes are remapped between the two layouts there, so HBM sees 16-byte
+// accesses on the page side and 4-byte accesses running along each row segment.
+struct SnapGeom {
+  uint32_t seq, bt, k_row, v_row;
+  uint64_t bb, ref_off;
+  uint32_t seg_k, seg_v;  // bytes of one head's values in a K / V row of the reference encoding
+};
+// byte u of one head's segment of a row (token m) in the reference encoding, as a byte of the
+// staged page tile: element bytes for f16/bf16/f32, code or scale bytes for q8_0
+__device__ inline uint32_t seg_to_tile(uint32_t type, bool is_v, uint32_t m, uint32_t u, uint32_t dim, uint32_t tile_bytes) {
+  switch (type) {
+    case KV_F16:
+    case KV_BF16: return elem_off(type, is_v, m, u >> 1, dim) + (u & 1u);
+    case KV_F32: return elem_off(type, is_v, m, u >> 2, dim) + (u & 3u);
+    default: {
+      const uint32_t b = u / 34u, r = u % 34u;  // block b: [f16 scale][32 codes]
+      if (r < 2) return tile_bytes + (m * (dim >> 5) + b) * 2u + r;
+      return elem_off(KV_Q8, is_v, m, 32u * b + r - 2u, dim);
+    }
+  }
+}
+
+template <bool WRITE>
+__global__ __launch_bounds__(256) void snapshot_tiles_kernel(PageGeom g, SnapGeom sg, uint8_t* snap) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t tid = threadIdx.x;
+  uint32_t id = blockIdx.x;
+  const bool is_v = id & 1u;
+  id >>= 1;
+  const uint32_t h = id % g.n_kv;
+  id /= g.n_kv;
+  const uint32_t tpb = sg.bt >> 4, t = id % tpb, bi = id / tpb;
+  const Side sd = side(g, is_v);
+  const uint32_t tb = sd.tile, ts = g.kv_type == KV_Q8 ? sd.tile_s : 0, seg = is_v ? sg.seg_v : sg.seg_k;
+  const uint32_t row = is_v ? sg.v_row : sg.k_row;
+  const int blk = g.table[(size_t)sg.seq * g.bps + bi];
+  uint8_t* head = g.pool + (size_t)blk * g.block_bytes + sd.off + h * sd.head;
+  uint8_t* tile = head + t * tb;
+  uint8_t* scales = head + sd.scale + t * ts;
+  uint8_t* rows = snap + (size_t)bi * sg.bb + sg.ref_off + (is_v ? (size_t)sg.bt * sg.k_row : 0) +
+                  (size_t)(t * 16) * row + (size_t)h * seg;
+  uint8_t* lt = smem;                        // page tile [tb] + scales [ts]
+  uint8_t* ls = smem + ((tb + ts + 15) & ~15u);  // row segments [16][seg]
+  const uint32_t sw = seg >> 2;              // 4-byte words per segment
+  if (WRITE) {
+    for (uint32_t o = tid * 16; o < tb; o += 256 * 16) *(uint4*)(lt + o) = *(const uint4*)(tile + o);
+    for (uint32_t o = tid * 4; o < ts; o += 256 * 4) *(uint32_t*)(lt + tb + o) = *(const uint32_t*)(scales + o);
+    __syncthreads();
+    for (uint32_t i = tid; i < 16 * seg; i += 256) {
+      const uint32_t m = i / seg, u = i % seg;
+      ls[i] = lt[seg_to_tile(g.kv_type, is_v, m, u, sd.dim, tb)];
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < 16 * sw; i += 256) {
+      const uint32_t m = i / sw, wd = i % sw;
+      *(uint32_t*)(rows + (size_t)m * row + 4 * wd) = *(const uint32_t*)(ls + m * seg + 4 * wd);
+    }
+  } else {
+    for (uint32_t i = tid; i < 16 * sw; i += 256) {
+      const uint32_t m = i / sw, wd = i % sw;
+      *(uint32_t*)(ls + m * seg + 4 * wd) = *(const uint32_t*)(rows + (size_t)m * row + 4 * wd);
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < 16 * seg; i += 256) {
+      const uint32_t m = i / seg, u = i % seg;
+      lt[seg_to_tile(g.kv_type, is_v, m, u, sd.dim, tb)] = ls[i];
+    }
+    __syncthreads();
+    for (uint32_t o = tid * 16; o < tb; o += 256 * 16) *(uint4*)(tile + o) = *(const uint4*)(lt + o);
+    for (uint32_t o = tid * 4; o < ts; o += 256 * 4) *(uint32_t*)(scales + o) = *(const uint32_t*)(lt + tb + o);
+  }
+}
+
 // Zero whole blocks (a newly backed block reads as zeros, like the reference's anonymous
 // mappings, kv.rs:29-37). block_bytes is a multiple of 16.
 __global__ void zero_blocks_kernel(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n) {
@@ -608,6 +686,19 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
 hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t n_pos, uint32_t bt, uint64_t bb,
                            uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s) {
   if (n_pos == 0) return hipSuccess;
+  const uint32_t seg_k = k_row / g.n_kv, seg_v = v_row / g.n_kv;
+  if (seg_k % 4 == 0 && seg_v % 4 == 0 && bt % 16 == 0) {
+    const SnapGeom sg{seq, bt, k_row, v_row, bb, ref_off, seg_k, seg_v};
+    const uint32_t tb = std::max(g.k_tile + (g.kv_type == KV_Q8 ? g.k_tile_s : 0),
+                                 g.v_tile + (g.kv_type == KV_Q8 ? g.v_tile_s : 0));
+    const size_t lds = ((tb + 15) & ~15u) + 16 * (size_t)std::max(seg_k, seg_v);
+    const uint32_t n_wg = n_pos / 16 * g.n_kv * 2;
+    if (write)
+      hipLaunchKernelGGL(snapshot_tiles_kernel<true>, dim3(n_wg), dim3(256), lds, s, g, sg, bytes);
+    else
+      hipLaunchKernelGGL(snapshot_tiles_kernel<false>, dim3(n_wg), dim3(256), lds, s, g, sg, bytes);
+    return hipGetLastError();
+  }
   if (write)
     hipLaunchKernelGGL(snapshot_write_kernel, dim3(n_pos), dim3(256), 0, s, g, seq, bt, bb, ref_off, k_row, v_row, bytes);
   else

@@ -270,7 +270,7 @@ class HipKvCache:
         """(milliseconds, launches) of one kernel kind ("decode" | "prefill" | "merge") since its
         last read (needs set_timing(True) while the calls ran)."""
         kind = {"decode": N.KERNEL_DECODE, "prefill": N.KERNEL_PREFILL, "merge": N.KERNEL_MERGE,
-                "rope_store": N.KERNEL_ROPE_STORE}[kernel]
+                "rope_store": N.KERNEL_ROPE_STORE, "snapshot": N.KERNEL_SNAPSHOT}[kernel]
         ms, n = C.c_double(), N.u64()
         self._check(N.lib().lmh_kv_kernel_time(self.h, kind, C.byref(ms), C.byref(n)))
         return ms.value, n.value
