@@ -10,7 +10,8 @@ launch stream during a second timed run of the same steps.
 
 Also reported (extra keys): every other configuration's throughput and roofline fraction, the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
-of a c4 sequence (`snapshot_c4`), and the CPU baseline
+of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), and
+the CPU baseline
 (the C++ restatement of the reference's CPU attention, oracle/, on host cores).
 """
 
@@ -219,6 +220,98 @@ def time_snapshot(steps: int, warmup_s: float):
     return res
 
 
+def time_sched(steps: int, warmup_s: float):
+    """A serving loop driven by the scheduler bound to the cache (lmh_sched_*), on c5's layer (40 Q /
+    8 KV heads, hd 128, f16 pages) and c5's mix: 16 requests decoding at contexts drawn like c5's
+    (1024..8192) and a queue of 4608-token prompts prefilled in chunks, under a 1040-token budget
+    (16 decode rows + 2 x 512). One step = next_step -> prepare -> qk_rope_store -> attend ->
+    commit -> complete -> publish the prefilled prompt blocks -> finish / drain the queue, for one
+    layer. Reported: wall time per step, the host time of the scheduler calls (Python through the C
+    ABI) per step, rows per step and rows per second. Untimed first: the loop runs until every
+    decode request has prefilled its prompt, then for at least `warmup_s` seconds."""
+    import torch
+
+    from llmario_amd.kv import HipKvCache, Layer
+    from llmario_amd.sched import CacheKey, Decoding, Priority, Request, Scheduler
+
+    rng = np.random.default_rng(5)
+    ctx = [int(c) for c in rng.integers(1024, 8192, size=16, endpoint=True)]
+    L = Layer(40, 8, 128, 128)
+    max_ctx = 8192 + 1024
+    hc = HipKvCache([L], max_ctx=max_ctx, n_seqs=18, kv_type="f16", block_tokens=16)
+    budget = 16 + 2 * 512
+    sch = Scheduler.bound(hc, budget, 18, CacheKey(bytes([5]), "f16", "theta=1e6"))
+    vocab = 150000
+    long_ids = set()
+    for c in ctx:  # long-running decodes: the prompt, then generation up to the context limit
+        a = sch.admit(Request(rng.integers(0, vocab, size=c, dtype=np.uint32), max_ctx - c, Priority.Interactive))
+        long_ids.add(a.slot)
+    arrivals = [rng.integers(0, vocab, size=4608, dtype=np.uint32) for _ in range(64)]
+
+    def feed(n):
+        for _ in range(n):
+            sch.admit(Request(arrivals[acc["fed"] % len(arrivals)], 1, Priority.Api))
+            acc["fed"] += 1
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    q_in = torch.randn((budget, L.n_head, L.hd), device="cuda", generator=g)
+    k_in = torch.randn((budget, L.n_kv, L.hd), device="cuda", generator=g)
+    v_in = torch.randn((budget, L.n_kv, L.hdv), device="cuda", generator=g)
+    q_out = torch.empty_like(q_in)
+    out = torch.empty((budget, L.n_head, L.hdv), device="cuda")
+    stream = torch.cuda.current_stream()
+    scale = L.hd ** -0.5
+    acc = {"host": 0.0, "rows": 0, "decodes": 0, "steps": 0, "fed": 0}
+
+    def one_step():
+        t0 = time.perf_counter()
+        st = sch.next_step()
+        segs, n = sch.prepare(st)
+        t1 = time.perf_counter()
+        hc.qk_rope_store(0, segs, q_in, k_in, v_in, q_out, rot_dim=L.hd, theta=1e6, neox=True, stream=stream)
+        hc.attend(0, segs, q_out, out, scale, 0, stream)
+        t2 = time.perf_counter()
+        hc.commit_batch(segs)
+        sch.complete(st)
+        for (sid, _, end) in st.prefills:
+            sch.publish_prompt(sid, end)
+        for sid in st.decodes:  # a prompt request ends after its one generated token
+            if sid not in long_ids:
+                sch.finish(sid)
+        if sch.queued() < 2:
+            feed(4)
+        sch.drain_queue()
+        acc["host"] += (t1 - t0) + (time.perf_counter() - t2)
+        acc["rows"] += n
+        acc["decodes"] += len(st.decodes)
+        acc["steps"] += 1
+
+    feed(4)
+    t_w = time.perf_counter()
+    while sum(1 for i in long_ids if sch.slot(i).state == Decoding()) < 16 or time.perf_counter() - t_w < warmup_s:
+        one_step()
+        if acc["steps"] % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    log(f"[bench] sched_c5: {acc['steps']} warm-up steps in {time.perf_counter() - t_w:.2f}s")
+    acc.update(host=0.0, rows=0, decodes=0, steps=0)
+    assert all(sch.slot(i) is not None for i in long_ids), "a long decode request was retracted"
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one_step()
+    torch.cuda.synchronize()
+    el = time.perf_counter() - t0
+    res = {"config": "sched_c5", "steps": steps, "ms_per_step": el * 1e3 / steps,
+           "host_us_per_step": acc["host"] * 1e6 / steps, "rows_per_step": acc["rows"] / steps,
+           "decode_rows_per_step": acc["decodes"] / steps, "rows_per_s": acc["rows"] / el,
+           "pool": sch.pool_stats()}
+    log(f"[bench] sched_c5: {res['ms_per_step'] * 1e3:.1f} us/step, scheduler host {res['host_us_per_step']:.1f} us/step, "
+        f"{res['rows_per_step']:.0f} rows/step ({res['decode_rows_per_step']:.1f} decode), {res['rows_per_s']:.0f} rows/s")
+    del sch, hc
+    torch.cuda.empty_cache()
+    return res
+
+
 def physical_cores() -> int:
     try:
         cores = set()
@@ -274,7 +367,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3,snapshot_c4",
+    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--extra-warmup-s", type=float, default=0.2,
@@ -312,6 +405,9 @@ def main():
     if args.profile_config == "snapshot_c4":
         print(json.dumps(time_snapshot(args.steps, args.extra_warmup_s)), flush=True)
         return
+    if args.profile_config == "sched_c5":
+        print(json.dumps(time_sched(args.steps, args.extra_warmup_s)), flush=True)
+        return
     if args.profile_config:
         res = time_config(args.profile_config, args.steps, args.warmup, warmup_s=args.extra_warmup_s)
         print(json.dumps(res), flush=True)
@@ -324,6 +420,8 @@ def main():
             extra[name] = time_rope_store(max(5, min(args.steps, 20)), args.extra_warmup_s)
         elif name == "snapshot_c4":
             extra[name] = time_snapshot(max(5, min(args.steps, 20)), args.extra_warmup_s)
+        elif name == "sched_c5":
+            extra[name] = time_sched(max(5, min(args.steps, 40)), args.extra_warmup_s)
         else:
             extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
 

@@ -228,6 +228,154 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches);
 
+/* ---- request scheduler: the host side of the batch hand-off ----
+ * Scheduler (crates/engine/sched/src/lib.rs:75-282) over the block pool, with Sequence
+ * (kv/src/lib.rs:262-335) for admission. Each step takes every decoding slot's next token, then
+ * prompt chunks of the prefilling slots, both in (priority descending, arrival) order, up to
+ * token_budget tokens. Admission reserves blocks for the prompt plus ceil(max_new *
+ * conservativeness) tokens, reclaiming cached prefix blocks by their SHA-256 chain hash; when the
+ * pool is short a request retracts the lowest-priority, youngest running slot of strictly lower
+ * priority, which goes back to the queue head; with nothing to retract the request is queued.
+ *
+ * Standalone (kv NULL at creation): the scheduler owns BlockPool::new(n_blocks, block_tokens).
+ * Bound (kv given): it shares the handle's pool (n_blocks and block_tokens are the handle's);
+ * every admitted slot holds one empty sequence slot of the handle, whose block table becomes the
+ * slot's reserved blocks and whose length starts at the slot's cached tokens, and a reservation
+ * is capped at max_ctx positions. lmh_sched_prepare turns a step into lmh_batch_prepare's batch.
+ * A scheduler is single-threaded and, when bound, used from the handle's thread. */
+#define LMH_PRIORITY_BATCH 0u       /* Priority (sched/src/lib.rs:19-24) */
+#define LMH_PRIORITY_API 1u
+#define LMH_PRIORITY_INTERACTIVE 2u
+
+typedef struct lmh_sched lmh_sched;
+
+/* Scheduler::new (sched/src/lib.rs:89-101) plus the CacheKey (kv/src/lib.rs:189-197) every block
+ * hash covers. Strings are NUL-terminated (NULL = empty); byte fields are pointer + length. */
+typedef struct lmh_sched_options {
+  uint32_t abi_version;      /* LMH_ABI_VERSION */
+  uint32_t max_slots;        /* clamped to >= 1; bound: at most the handle's n_seqs */
+  uint64_t token_budget;     /* clamped to >= 1 */
+  double conservativeness;   /* multiplier on max_new when reserving (the reference starts at 1.0) */
+  uint64_t n_blocks;         /* standalone pool size */
+  uint32_t block_tokens;     /* standalone pool block size (> 0) */
+  uint32_t reserved0;
+  const uint8_t* model_digest;
+  uint64_t model_digest_len;
+  const char* kv_types;
+  const char* rope_params;
+  const char* template_hash;
+  const uint8_t* salt;       /* per-client salt: different salts never share blocks */
+  uint64_t salt_len;
+} lmh_sched_options;
+
+/* Request (sched/src/lib.rs:58-62). The prompt is copied. */
+typedef struct lmh_request {
+  const uint32_t* prompt;
+  uint64_t n_prompt;
+  uint64_t max_new;
+  uint32_t priority;         /* LMH_PRIORITY_* */
+  uint32_t reserved0;
+} lmh_request;
+
+/* Admission (sched/src/lib.rs:65-73): Admitted { slot, cached_tokens, retracted } or Queued. */
+typedef struct lmh_admission {
+  uint32_t admitted;         /* 1 = admitted, 0 = queued */
+  uint32_t slot;
+  uint64_t cached_tokens;    /* prompt tokens already in the cache (< the prompt length) */
+  uint64_t n_retracted;      /* slots retracted, in order; the first `cap` ids are written */
+} lmh_admission;
+
+/* Step (sched/src/lib.rs:48-55). The caller owns both arrays; lmh_sched_next_step fills at most
+ * max_slots entries of each. */
+typedef struct lmh_prefill_range {
+  uint32_t slot;
+  uint32_t reserved0;
+  uint64_t start;            /* prompt[start..end] is prefilled this step */
+  uint64_t end;
+} lmh_prefill_range;
+typedef struct lmh_step {
+  uint32_t* decodes;
+  uint64_t n_decodes;
+  lmh_prefill_range* prefills;
+  uint64_t n_prefills;
+  uint64_t tokens;
+} lmh_step;
+
+/* Slot (sched/src/lib.rs:34-45). */
+typedef struct lmh_slot_info {
+  uint32_t id;
+  uint32_t priority;
+  uint32_t decoding;         /* SlotState::Decoding (1) or Prefilling { done } (0) */
+  uint32_t reserved0;
+  uint64_t done;             /* prompt tokens prefilled */
+  uint64_t n_prompt;
+  uint64_t max_new;
+  uint64_t generated;
+  uint64_t seq_no;           /* arrival order */
+  uint64_t kv_seq;           /* bound: the handle's sequence slot; standalone: UINT64_MAX */
+  uint64_t n_blocks;         /* blocks in the slot's table */
+} lmh_slot_info;
+
+/* A queued request: (seq_no, Request) of the queue (sched/src/lib.rs:82). */
+typedef struct lmh_queued_info {
+  uint64_t seq_no;
+  uint64_t n_prompt;
+  uint64_t max_new;
+  uint32_t priority;
+  uint32_t reserved0;
+} lmh_queued_info;
+
+/* Scheduler counters plus PoolStats (kv/src/lib.rs:178-186) of the pool it admits from. */
+typedef struct lmh_sched_stats {
+  uint64_t slots, queued, retractions;
+  uint64_t n_blocks, free, cached_free, hits, misses, evictions;
+} lmh_sched_stats;
+
+int32_t lmh_sched_create(const lmh_sched_options* opt, lmh_kv* kv, lmh_sched** out);
+/* Bound: releases the blocks of every slot it still holds. A bound scheduler whose handle was
+ * destroyed first fails every call with LMH_INVALID_ARGUMENT and can only be destroyed. */
+void lmh_sched_destroy(lmh_sched* s);
+const char* lmh_sched_last_error(const lmh_sched* s);
+/* Scheduler::admit (sched/src/lib.rs:118-183). `retracted` holds `cap` ids (NULL when cap = 0);
+ * max_slots entries always suffice. Bound: a prompt longer than max_ctx is LMH_INVALID_ARGUMENT. */
+int32_t lmh_sched_admit(lmh_sched* s, const lmh_request* r, lmh_admission* out, uint32_t* retracted,
+                        uint64_t cap);
+/* Scheduler::drain_queue (sched/src/lib.rs:186-217): admits queued requests oldest first while
+ * they fit; the first `cap` admitted slot ids are written, *n is the count. */
+int32_t lmh_sched_drain_queue(lmh_sched* s, uint32_t* admitted, uint64_t cap, uint64_t* n);
+/* Scheduler::next_step (sched/src/lib.rs:220-249). */
+int32_t lmh_sched_next_step(const lmh_sched* s, lmh_step* step);
+/* Scheduler::complete (sched/src/lib.rs:253-268): prefill cursors advance (a slot whose end
+ * reaches its prompt length decodes from then on), each decode slot counts one generated token.
+ * Unknown slot ids are skipped. */
+int32_t lmh_sched_complete(lmh_sched* s, const lmh_step* step);
+/* Scheduler::finish (sched/src/lib.rs:277-281): the slot leaves and its blocks return to the
+ * pool (published blocks stay cached in the free queue). Unknown ids are a no-op. */
+int32_t lmh_sched_finish(lmh_sched* s, uint32_t slot);
+/* Sequence::publish (kv/src/lib.rs:320-328) for a slot: tokens[0..n] are the positions written so
+ * far (tokens NULL: the slot's own prompt[0..n], n <= its length); every full block among them
+ * gets its chain hash, so later admissions can reclaim it.
+ * Bound: the full blocks must already be written (n / block_tokens * block_tokens <= the
+ * sequence length), LMH_INVALID_ARGUMENT otherwise. */
+int32_t lmh_sched_publish(lmh_sched* s, uint32_t slot, const uint32_t* tokens, uint64_t n);
+/* Bound only: the step as a batch for lmh_batch_prepare, decodes first (one row each, so the
+ * decode rows are one contiguous range at the top) then the prefill chunks, in step order; the
+ * segments come back in that order with the handle's sequence ids. A prefill range must start at
+ * its sequence's length. LMH_KV_FULL (a slot outgrew its reservation) changes nothing. After the
+ * step's device work: lmh_batch_commit(kv, segs), then lmh_sched_complete. */
+int32_t lmh_sched_prepare(lmh_sched* s, const lmh_step* step, lmh_seg* segs_out, uint64_t* n_rows,
+                          uint64_t* needed, uint64_t* free_blocks);
+int32_t lmh_sched_get_stats(const lmh_sched* s, lmh_sched_stats* out);
+/* Running slot ids in admission order (the order next_step breaks ties by is seq_no). */
+int32_t lmh_sched_slots(const lmh_sched* s, uint32_t* ids, uint64_t cap, uint64_t* n);
+int32_t lmh_sched_slot(const lmh_sched* s, uint32_t slot, lmh_slot_info* out);
+int32_t lmh_sched_slot_blocks(const lmh_sched* s, uint32_t slot, uint32_t* out, uint64_t cap, uint64_t* n);
+int32_t lmh_sched_queued_at(const lmh_sched* s, uint64_t i, lmh_queued_info* out);
+/* chain_hashes (kv/src/lib.rs:216-239): one 32-byte SHA-256 per full block of tokens, under the
+ * CacheKey fields of `key` (other fields unused); `out` holds cap hashes, *n_hashes is the count. */
+int32_t lmh_chain_hashes(const uint32_t* tokens, uint64_t n, uint32_t block_tokens, const lmh_sched_options* key,
+                         uint8_t* out, uint64_t cap, uint64_t* n_hashes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -54,6 +54,49 @@ class RopeParams(C.Structure):
                 ("attn_factor", C.c_float), ("q_norm", P), ("k_norm", P), ("freq_div", P)]
 
 
+PRIORITY_BATCH, PRIORITY_API, PRIORITY_INTERACTIVE = 0, 1, 2
+
+
+class SchedOptions(C.Structure):
+    _fields_ = [("abi_version", u32), ("max_slots", u32), ("token_budget", u64),
+                ("conservativeness", C.c_double), ("n_blocks", u64), ("block_tokens", u32),
+                ("reserved0", u32), ("model_digest", P), ("model_digest_len", u64),
+                ("kv_types", C.c_char_p), ("rope_params", C.c_char_p), ("template_hash", C.c_char_p),
+                ("salt", P), ("salt_len", u64)]
+
+
+class Request(C.Structure):
+    _fields_ = [("prompt", P), ("n_prompt", u64), ("max_new", u64), ("priority", u32), ("reserved0", u32)]
+
+
+class Admission(C.Structure):
+    _fields_ = [("admitted", u32), ("slot", u32), ("cached_tokens", u64), ("n_retracted", u64)]
+
+
+class PrefillRange(C.Structure):
+    _fields_ = [("slot", u32), ("reserved0", u32), ("start", u64), ("end", u64)]
+
+
+class Step(C.Structure):
+    _fields_ = [("decodes", C.POINTER(u32)), ("n_decodes", u64), ("prefills", C.POINTER(PrefillRange)),
+                ("n_prefills", u64), ("tokens", u64)]
+
+
+class SlotInfo(C.Structure):
+    _fields_ = [("id", u32), ("priority", u32), ("decoding", u32), ("reserved0", u32), ("done", u64),
+                ("n_prompt", u64), ("max_new", u64), ("generated", u64), ("seq_no", u64), ("kv_seq", u64),
+                ("n_blocks", u64)]
+
+
+class QueuedInfo(C.Structure):
+    _fields_ = [("seq_no", u64), ("n_prompt", u64), ("max_new", u64), ("priority", u32), ("reserved0", u32)]
+
+
+class SchedStats(C.Structure):
+    _fields_ = [(f, u64) for f in ("slots", "queued", "retractions", "n_blocks", "free", "cached_free",
+                                   "hits", "misses", "evictions")]
+
+
 # name -> (restype, argtypes); the exported C ABI, in header order.
 SIGNATURES = {
     "lmh_kv_create": (i32, [C.POINTER(KvOptions), C.POINTER(P)]),
@@ -89,6 +132,22 @@ SIGNATURES = {
     "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
     "lmh_kv_set_timing": (i32, [P, i32]),
     "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
+    "lmh_sched_create": (i32, [C.POINTER(SchedOptions), P, C.POINTER(P)]),
+    "lmh_sched_destroy": (None, [P]),
+    "lmh_sched_last_error": (C.c_char_p, [P]),
+    "lmh_sched_admit": (i32, [P, C.POINTER(Request), C.POINTER(Admission), P, u64]),
+    "lmh_sched_drain_queue": (i32, [P, P, u64, C.POINTER(u64)]),
+    "lmh_sched_next_step": (i32, [P, C.POINTER(Step)]),
+    "lmh_sched_complete": (i32, [P, C.POINTER(Step)]),
+    "lmh_sched_finish": (i32, [P, u32]),
+    "lmh_sched_publish": (i32, [P, u32, P, u64]),
+    "lmh_sched_prepare": (i32, [P, C.POINTER(Step), P, C.POINTER(u64), C.POINTER(u64), C.POINTER(u64)]),
+    "lmh_sched_get_stats": (i32, [P, C.POINTER(SchedStats)]),
+    "lmh_sched_slots": (i32, [P, P, u64, C.POINTER(u64)]),
+    "lmh_sched_slot": (i32, [P, u32, C.POINTER(SlotInfo)]),
+    "lmh_sched_slot_blocks": (i32, [P, u32, P, u64, C.POINTER(u64)]),
+    "lmh_sched_queued_at": (i32, [P, u64, C.POINTER(QueuedInfo)]),
+    "lmh_chain_hashes": (i32, [P, u64, u32, C.POINTER(SchedOptions), P, u64, C.POINTER(u64)]),
 }
 
 KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE, KERNEL_ROPE_STORE, KERNEL_SNAPSHOT = 0, 1, 2, 3, 4

@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libllmario_hip.so")
-SOURCES = ["host.cpp", "kv_kernels.hip", "decode.hip", "prefill.hip"]
+SOURCES = ["host.cpp", "sched.cpp", "kv_kernels.hip", "decode.hip", "prefill.hip"]
 ARCH = os.environ.get("LMH_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

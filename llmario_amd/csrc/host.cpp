@@ -28,6 +28,8 @@
 
 #include "../../include/llmario_hip.h"
 #include "device.h"
+#include "kv_hooks.h"
+#include "pool.h"
 
 using namespace lmh;
 
@@ -139,14 +141,6 @@ struct DevBuf {  // grow-only device scratch
   }
 };
 
-using Hash = std::array<uint8_t, 32>;
-
-struct BlockMeta {
-  uint32_t refs = 0;
-  bool has_hash = false;
-  Hash hash{};
-};
-
 struct Seq {
   std::vector<uint32_t> blocks;
   uint64_t len = 0;
@@ -167,10 +161,7 @@ struct lmh_kv {
   uint64_t max_ctx = 0, n_seqs = 0, bps = 0, pool_blocks = 0, block_bytes = 0;
   std::vector<LayerLayout> layers;
   // ---- BlockPool (kv/src/lib.rs:36-176)
-  std::vector<BlockMeta> meta;
-  std::deque<uint32_t> free_q;
-  std::map<Hash, uint32_t> by_hash;
-  uint64_t hits = 0, misses = 0, evictions = 0;
+  BlockPool pool;
   std::vector<uint8_t> backed;
   // ---- sequences
   std::vector<Seq> seqs;
@@ -200,6 +191,7 @@ struct lmh_kv {
   uint64_t launches[5] = {0, 0, 0, 0, 0};
   std::vector<PrefillItem> pitems;
   std::vector<uint8_t> payload;
+  std::vector<lmh_sched*> scheds;           // schedulers bound to this handle
   std::string err;
 
   ~lmh_kv() {
@@ -225,34 +217,9 @@ struct lmh_kv {
   }
 
   // ---- BlockPool operations --------------------------------------------------------------
-  bool pool_alloc(uint64_t n, std::vector<uint32_t>& out) {  // lib.rs:93-109
-    if (free_q.size() < n) return false;
-    for (uint64_t i = 0; i < n; i++) {
-      const uint32_t b = free_q.front();
-      free_q.pop_front();
-      BlockMeta& m = meta[b];
-      if (m.has_hash) {
-        by_hash.erase(m.hash);
-        m.has_hash = false;
-        evictions++;
-      }
-      m.refs = 1;
-      out.push_back(b);
-    }
-    return true;
-  }
-  void pool_release(uint32_t b) {  // lib.rs:121-128
-    BlockMeta& m = meta[b];
-    if (m.refs == 0) return;
-    if (--m.refs == 0) free_q.push_back(b);
-  }
-  void pool_clear_hash(uint32_t b) {  // lib.rs:161-167
-    BlockMeta& m = meta[b];
-    if (!m.has_hash) return;
-    auto it = by_hash.find(m.hash);
-    if (it != by_hash.end() && it->second == b) by_hash.erase(it);
-    m.has_hash = false;
-  }
+  bool pool_alloc(uint64_t n, std::vector<uint32_t>& out) { return pool.alloc(n, out); }  // lib.rs:93-109
+  void pool_release(uint32_t b) { pool.release(b); }                                      // lib.rs:121-128
+  void pool_clear_hash(uint32_t b) { pool.clear_hash(b); }                                // lib.rs:161-167
   // ---- backing (kv.rs:690-712): a block is resident while referenced or cached
   void back(uint32_t b, bool zero) {
     if (!backed[b]) {
@@ -261,7 +228,7 @@ struct lmh_kv {
     }
   }
   void maybe_unback(uint32_t b) {
-    if (meta[b].refs == 0 && !meta[b].has_hash) backed[b] = 0;
+    if (pool.meta[b].refs == 0 && !pool.meta[b].has_hash) backed[b] = 0;
   }
   void release_block(uint32_t b) {
     pool_release(b);
@@ -279,7 +246,7 @@ struct lmh_kv {
     const Seq& q = seqs[s];
     const uint64_t want = (new_len + bt - 1) / bt;
     const uint64_t missing = want > q.blocks.size() ? want - q.blocks.size() : 0;
-    const bool cow = q.len % bt != 0 && q.len < new_len && meta[q.blocks[q.len / bt]].refs > 1;
+    const bool cow = q.len % bt != 0 && q.len < new_len && pool.meta[q.blocks[q.len / bt]].refs > 1;
     return missing + (cow ? 1 : 0);
   }
 
@@ -291,11 +258,11 @@ struct lmh_kv {
     const uint64_t missing = want > seqs[s].blocks.size() ? want - seqs[s].blocks.size() : 0;
     const uint64_t wanted = blocks_needed(s, new_len);
     const bool cow = wanted > missing;
-    if (free_q.size() < wanted) {
+    if (pool.free_q.size() < wanted) {
       if (needed) *needed = wanted;
-      if (free_blocks) *free_blocks = free_q.size();
+      if (free_blocks) *free_blocks = pool.free_q.size();
       return fail(LMH_KV_FULL, "KV cache full: " + std::to_string(wanted) + " more blocks needed, " +
-                                   std::to_string(free_q.size()) + " free");
+                                   std::to_string(pool.free_q.size()) + " free");
     }
     if (len % bt != 0 && len < new_len) {
       const uint64_t bi = len / bt;
@@ -521,6 +488,28 @@ struct Fnv {
 // C ABI
 // =============================================================================================
 
+// ---- hooks for the scheduler (kv_hooks.h) ----
+namespace lmh {
+BlockPool& kv_pool(lmh_kv* kv) { return kv->pool; }
+uint64_t kv_n_seqs(const lmh_kv* kv) { return kv->n_seqs; }
+uint64_t kv_max_ctx(const lmh_kv* kv) { return kv->max_ctx; }
+uint64_t kv_seq_len(const lmh_kv* kv, uint64_t seq) { return kv->seqs[seq].len; }
+bool kv_seq_empty(const lmh_kv* kv, uint64_t seq) { return kv->seqs[seq].blocks.empty() && kv->seqs[seq].len == 0; }
+const std::vector<uint32_t>& kv_seq_blocks(const lmh_kv* kv, uint64_t seq) { return kv->seqs[seq].blocks; }
+void kv_bind_seq(lmh_kv* kv, uint64_t seq, const std::vector<uint32_t>& blocks, uint64_t len) {
+  for (uint32_t b : blocks) kv->back(b, true);
+  kv->seqs[seq].blocks = blocks;
+  kv->seqs[seq].len = len;
+  kv->set_table(seq);
+}
+void kv_clear_seq(lmh_kv* kv, uint64_t seq) { kv->clear(seq); }
+void kv_set_error(lmh_kv* kv, const char* msg) { kv->err = msg; }
+void kv_attach(lmh_kv* kv, lmh_sched* s) { kv->scheds.push_back(s); }
+void kv_detach(lmh_kv* kv, lmh_sched* s) {
+  kv->scheds.erase(std::remove(kv->scheds.begin(), kv->scheds.end(), s), kv->scheds.end());
+}
+}  // namespace lmh
+
 extern "C" {
 
 const char* lmh_create_error(void) { return g_create_error.c_str(); }
@@ -615,8 +604,7 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
     g_create_error = "pool too large";
     return LMH_INVALID_ARGUMENT;
   }
-  kv->meta.assign(kv->pool_blocks, BlockMeta{});
-  for (uint64_t i = 0; i < kv->pool_blocks; i++) kv->free_q.push_back((uint32_t)i);
+  kv->pool.init(kv->pool_blocks, bt);
   kv->backed.assign(kv->pool_blocks, 0);
   kv->seqs.assign(kv->n_seqs, Seq{});
   kv->h_table.assign(kv->n_seqs * kv->bps, -1);
@@ -640,7 +628,11 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   return LMH_OK;
 }
 
-void lmh_kv_destroy(lmh_kv* kv) { delete kv; }
+void lmh_kv_destroy(lmh_kv* kv) {
+  if (!kv) return;
+  for (lmh_sched* s : kv->scheds) sched_kv_destroyed(s);
+  delete kv;
+}
 
 const char* lmh_kv_last_error(const lmh_kv* kv) { return kv ? kv->err.c_str() : "null handle"; }
 
@@ -693,7 +685,7 @@ int32_t lmh_kv_set_seq_len(lmh_kv* kv, uint64_t seq, uint64_t len) {
 
 int32_t lmh_kv_free_blocks(const lmh_kv* kv, uint64_t* n) {
   if (!kv || !n) return LMH_INVALID_ARGUMENT;
-  *n = kv->free_q.size();
+  *n = kv->pool.free_q.size();
   return LMH_OK;
 }
 
@@ -778,10 +770,10 @@ int32_t lmh_kv_read_seq(lmh_kv* kv, uint64_t seq, uint64_t len, const void* src,
   // room first: clearing frees this sequence's unshared blocks, so they count as available
   const uint64_t nb = (len + kv->bt - 1) / kv->bt;
   uint64_t own = 0;
-  for (uint32_t b : kv->seqs[seq].blocks) own += kv->meta[b].refs == 1 ? 1 : 0;
-  if (nb > kv->free_q.size() + own) {
+  for (uint32_t b : kv->seqs[seq].blocks) own += kv->pool.meta[b].refs == 1 ? 1 : 0;
+  if (nb > kv->pool.free_q.size() + own) {
     if (needed) *needed = nb;
-    if (free_blocks) *free_blocks = kv->free_q.size() + own;
+    if (free_blocks) *free_blocks = kv->pool.free_q.size() + own;
     return kv->fail(LMH_KV_FULL, "KV cache full: snapshot needs " + std::to_string(nb) + " blocks");
   }
   kv->clear(seq);
@@ -814,18 +806,18 @@ int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, ui
     want[blocks[i]] = 1;
   }
   uint64_t found = 0;
-  for (uint32_t b : kv->free_q) found += want[b];
+  for (uint32_t b : kv->pool.free_q) found += want[b];
   if (found != n) return kv->fail(LMH_INVALID_ARGUMENT, "a requested block is not free");
   std::deque<uint32_t> rest;
-  for (uint32_t b : kv->free_q)
+  for (uint32_t b : kv->pool.free_q)
     if (!want[b]) rest.push_back(b);
-  kv->free_q.swap(rest);
+  kv->pool.free_q.swap(rest);
   for (uint64_t i = 0; i < n; i++) {
-    BlockMeta& m = kv->meta[blocks[i]];
+    BlockMeta& m = kv->pool.meta[blocks[i]];
     if (m.has_hash) {
-      kv->by_hash.erase(m.hash);
+      kv->pool.by_hash.erase(m.hash);
       m.has_hash = false;
-      kv->evictions++;
+      kv->pool.evictions++;
     }
     m.refs = 1;
     kv->back(blocks[i], true);
@@ -837,7 +829,7 @@ int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, ui
 
 int32_t lmh_pool_refs(const lmh_kv* kv, uint32_t block, uint32_t* refs) {
   if (!kv || !refs || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
-  *refs = kv->meta[block].refs;
+  *refs = kv->pool.meta[block].refs;
   return LMH_OK;
 }
 
@@ -845,11 +837,7 @@ int32_t lmh_pool_set_hash(lmh_kv* kv, uint32_t block, const uint8_t hash[32]) { 
   if (!kv || !hash || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
   Hash h;
   std::memcpy(h.data(), hash, 32);
-  BlockMeta& m = kv->meta[block];
-  if (m.has_hash) kv->by_hash.erase(m.hash);
-  m.hash = h;
-  m.has_hash = true;
-  kv->by_hash[h] = block;
+  kv->pool.set_hash(block, h);
   return LMH_OK;
 }
 
@@ -862,7 +850,7 @@ int32_t lmh_pool_clear_hash(lmh_kv* kv, uint32_t block) {
 
 int32_t lmh_pool_is_cached(const lmh_kv* kv, uint32_t block, int32_t* cached) {
   if (!kv || !cached || block >= kv->pool_blocks) return LMH_INVALID_ARGUMENT;
-  *cached = kv->meta[block].has_hash ? 1 : 0;
+  *cached = kv->pool.meta[block].has_hash ? 1 : 0;
   return LMH_OK;
 }
 
@@ -883,11 +871,11 @@ int32_t lmh_batch_prepare(lmh_kv* kv, const lmh_seq_tokens* batch, uint64_t n, l
   }
   uint64_t need = 0;
   for (uint64_t i = 0; i < n; i++) need += kv->blocks_needed(batch[i].seq, kv->seqs[batch[i].seq].len + batch[i].n_tokens);
-  if (need > kv->free_q.size()) {
+  if (need > kv->pool.free_q.size()) {
     if (needed) *needed = need;
-    if (free_blocks) *free_blocks = kv->free_q.size();
+    if (free_blocks) *free_blocks = kv->pool.free_q.size();
     return kv->fail(LMH_KV_FULL, "KV cache full: " + std::to_string(need) + " more blocks needed, " +
-                                     std::to_string(kv->free_q.size()) + " free");
+                                     std::to_string(kv->pool.free_q.size()) + " free");
   }
   for (uint64_t i = 0; i < n; i++) kv->reserve(batch[i].seq, kv->seqs[batch[i].seq].len + batch[i].n_tokens, nullptr, nullptr);
   uint64_t start = 0;

@@ -94,6 +94,8 @@ def lib():
             "orc_pool_refs": (C.c_uint32, [P, C.c_uint32]),
             "orc_pool_is_cached": (C.c_int, [P, C.c_uint32]),
             "orc_pool_clear_hash": (None, [P, C.c_uint32]),
+            "orc_pool_note_miss": (None, [P]),
+            "orc_pool_block_tokens": (u64, [P]),
             "orc_pool_stats": (None, [P, P]),
             "orc_cache_new": (P, [P, P, u64]),
             "orc_cache_free": (None, [P]),
@@ -109,6 +111,7 @@ def lib():
             "orc_cache_resident_blocks": (u64, [P]),
             "orc_cache_seq_blocks": (u64, [P, u64, P, u64]),
             "orc_cache_adopt_blocks": (C.c_int, [P, u64, P, u64]),
+            "orc_cache_bind_seq": (C.c_int, [P, u64, P, u64, u64]),
             "orc_cache_store_k": (None, [P, u64, u64, u64, P]),
             "orc_cache_store_v": (None, [P, u64, u64, u64, P]),
             "orc_cache_store_k_raw": (None, [P, u64, u64, u64, P]),
@@ -297,6 +300,12 @@ class Pool:
     def clear_hash(self, b: int):
         lib().orc_pool_clear_hash(self.h, b)
 
+    def note_miss(self):
+        lib().orc_pool_note_miss(self.h)
+
+    def block_tokens(self) -> int:
+        return lib().orc_pool_block_tokens(self.h)
+
     def stats(self) -> dict:
         o = np.zeros(6, dtype=np.uint64)
         lib().orc_pool_stats(self.h, _ptr(o))
@@ -372,6 +381,11 @@ class Cache:
         b = np.ascontiguousarray(blocks, dtype=np.uint32)
         if lib().orc_cache_adopt_blocks(self.h, s, _ptr(b), b.size) != OK:
             raise ValueError("blocks not free or sequence not empty")
+
+    def bind_seq(self, s: int, blocks, length: int):
+        b = np.ascontiguousarray(blocks if len(blocks) else [0], dtype=np.uint32)
+        if lib().orc_cache_bind_seq(self.h, s, _ptr(b), len(blocks), length) != OK:
+            raise ValueError("sequence not empty or length beyond its blocks")
 
     def store(self, s: int, l: int, pos: int, k: np.ndarray, v: np.ndarray):
         k = np.ascontiguousarray(k, dtype=np.float32)

@@ -753,6 +753,8 @@ int orc_pool_reclaim(orc_pool* p, const uint8_t* h32, uint32_t* out) {
 uint32_t orc_pool_refs(const orc_pool* p, uint32_t b) { return p->meta[b].refs; }
 int orc_pool_is_cached(const orc_pool* p, uint32_t b) { return p->meta[b].has_hash ? 1 : 0; }
 void orc_pool_clear_hash(orc_pool* p, uint32_t b) { p->clear_hash(b); }
+void orc_pool_note_miss(orc_pool* p) { p->misses++; }  // lib.rs:145-147
+uint64_t orc_pool_block_tokens(const orc_pool* p) { return p->block_tokens; }
 void orc_pool_stats(const orc_pool* p, uint64_t* o) {
   o[0] = p->meta.size();
   o[1] = p->free.size();
@@ -829,6 +831,17 @@ int orc_cache_adopt_blocks(orc_cache* c, uint64_t s, const uint32_t* blocks, uin
     c->back(b);
     c->seqs[s].blocks.push_back(b);
   }
+  return ORC_OK;
+}
+// The scheduler driving this cache: sequence slot s takes the blocks Sequence::acquire referenced
+// for it (kv/src/lib.rs:272-316) as its table, and starts at len positions.
+int orc_cache_bind_seq(orc_cache* c, uint64_t s, const uint32_t* blocks, uint64_t n, uint64_t len) {
+  if (!c->seqs[s].blocks.empty() || c->seqs[s].len != 0 || len > n * c->lay.block_tokens) return ORC_INVALID;
+  for (uint64_t i = 0; i < n; i++) {
+    c->back(blocks[i]);
+    c->seqs[s].blocks.push_back(blocks[i]);
+  }
+  c->seqs[s].len = len;
   return ORC_OK;
 }
 void orc_cache_store_k(orc_cache* c, uint64_t s, uint64_t l, uint64_t pos, const float* k) {

@@ -85,6 +85,8 @@ int orc_pool_reclaim(orc_pool* p, const uint8_t* h32, uint32_t* out); /* 1 hit, 
 uint32_t orc_pool_refs(const orc_pool* p, uint32_t b);
 int orc_pool_is_cached(const orc_pool* p, uint32_t b);
 void orc_pool_clear_hash(orc_pool* p, uint32_t b);
+void orc_pool_note_miss(orc_pool* p);
+uint64_t orc_pool_block_tokens(const orc_pool* p);
 void orc_pool_stats(const orc_pool* p, uint64_t* out6); /* n_blocks free cached_free hits misses evictions */
 
 /* ---- KvCache (kv.rs:562-939) ---- */
@@ -105,6 +107,7 @@ uint64_t orc_cache_seq_blocks(const orc_cache* c, uint64_t s, uint32_t* out, uin
 /* Test hook: impose a block table (e.g. a seeded permutation). Takes the listed free blocks out of
  * the pool in that order; fails (ORC_INVALID) if any is not free or the sequence holds blocks. */
 int orc_cache_adopt_blocks(orc_cache* c, uint64_t s, const uint32_t* blocks, uint64_t n);
+int orc_cache_bind_seq(orc_cache* c, uint64_t s, const uint32_t* blocks, uint64_t n, uint64_t len);
 void orc_cache_store_k(orc_cache* c, uint64_t s, uint64_t l, uint64_t pos, const float* k);
 void orc_cache_store_v(orc_cache* c, uint64_t s, uint64_t l, uint64_t pos, const float* v);
 /* Write one row already in the cache's row encoding (row_bytes(kv_dim) bytes). */
