@@ -373,6 +373,9 @@ int32_t lmh_sched_slot_blocks(const lmh_sched* s, uint32_t slot, uint32_t* out, 
 int32_t lmh_sched_queued_at(const lmh_sched* s, uint64_t i, lmh_queued_info* out);
 /* chain_hashes (kv/src/lib.rs:216-239): one 32-byte SHA-256 per full block of tokens, under the
  * CacheKey fields of `key` (other fields unused); `out` holds cap hashes, *n_hashes is the count. */
+/* Test hook: SHA-256 of msg[0..n] (path -1: the path the library uses, 0: portable code, 1: the
+ * x86 SHA extensions, LMH_UNSUPPORTED where the host lacks them). */
+int32_t lmh_sha256(const uint8_t* msg, uint64_t n, int32_t path, uint8_t out[32]);
 int32_t lmh_chain_hashes(const uint32_t* tokens, uint64_t n, uint32_t block_tokens, const lmh_sched_options* key,
                          uint8_t* out, uint64_t cap, uint64_t* n_hashes);
 

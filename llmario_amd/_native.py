@@ -147,6 +147,7 @@ SIGNATURES = {
     "lmh_sched_slot": (i32, [P, u32, C.POINTER(SlotInfo)]),
     "lmh_sched_slot_blocks": (i32, [P, u32, P, u64, C.POINTER(u64)]),
     "lmh_sched_queued_at": (i32, [P, u64, C.POINTER(QueuedInfo)]),
+    "lmh_sha256": (i32, [P, u64, i32, P]),
     "lmh_chain_hashes": (i32, [P, u64, u32, C.POINTER(SchedOptions), P, u64, C.POINTER(u64)]),
 }
 

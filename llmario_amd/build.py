@@ -1,7 +1,7 @@
 """Build the HIP backend library in-tree: ``llmario_amd/libllmario_hip.so`` for gfx950.
 
-Every source compiles with hipcc (host.cpp too: it includes the device structures), objects in
-parallel, then one shared-library link. Packed FP32 instructions are disabled for all device
+Every source compiles with hipcc (host.cpp too: it includes the device structures; the scheduler
+and SHA-256 sources as plain host C++), objects in parallel, then one shared-library link. Packed FP32 instructions are disabled for all device
 code (``-target-feature -packed-fp32-ops``).
 """
 
@@ -16,7 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libllmario_hip.so")
-SOURCES = ["host.cpp", "sched.cpp", "kv_kernels.hip", "decode.hip", "prefill.hip"]
+SOURCES = ["host.cpp", "sched.cpp", "sha256.cpp", "kv_kernels.hip", "decode.hip", "prefill.hip"]
+# host-only sources (no device code): compiled as plain C++ by the same compiler
+HOST_ONLY = {"sched.cpp", "sha256.cpp"}
 ARCH = os.environ.get("LMH_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -36,7 +38,11 @@ EXTRA = {"prefill.hip": ["-fno-honor-nans", "-Wno-inline-asm"]}
 
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+    if src in HOST_ONLY:
+        cmd = [HIPCC, "-O3", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(HERE, "..", "include"),
+               "-x", "c++", "-c", os.path.join(CSRC, src), "-o", obj]
+    else:
+        cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
@@ -49,7 +55,7 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 4)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

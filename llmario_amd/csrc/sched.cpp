@@ -4,10 +4,9 @@
 //
 //   Scheduler   crates/engine/sched/src/lib.rs:75-282
 //   Sequence    crates/engine/kv/src/lib.rs:262-335 (acquire / publish / release)
-#include <string.h>
-
 #include <algorithm>
 #include <cmath>
+#include <cstring>
 #include <deque>
 #include <string>
 #include <vector>
@@ -30,6 +29,9 @@ struct Slot {
   uint64_t seq_no = 0;
   std::vector<uint32_t> blocks;  // standalone: the Sequence's block table (bound: the handle's)
   uint64_t kv_seq = UINT64_MAX;
+  // chain hashes already computed for this slot: chain[i] covers chain_tokens[0 .. (i+1)*bt]
+  std::vector<Hash> chain;
+  std::vector<uint32_t> chain_tokens;
 };
 
 struct Queued {
@@ -102,20 +104,24 @@ struct lmh_sched {
   }
 
   // Sequence::acquire (kv/src/lib.rs:272-316): reclaim the cached prefix blocks by chain hash
-  // (stopping at the first miss), then allocate the rest; on failure nothing is held.
+  // (stopping at the first miss), then allocate the rest; on failure nothing is held. The hashes
+  // are computed block by block up to the first miss (the ones after it are never looked up);
+  // `chain` returns those of the reclaimed blocks.
   bool acquire(const std::vector<uint32_t>& tokens, uint64_t reserve, std::vector<uint32_t>& blocks,
-               uint64_t& cached) {
+               uint64_t& cached, std::vector<Hash>& chain) {
     BlockPool& p = pool();
     const uint32_t bt = p.block_tokens;
-    const std::vector<Hash> hashes = chain_hashes(tokens.data(), tokens.size(), bt, extra);
     blocks.clear();
+    chain.clear();
     cached = 0;
-    for (const Hash& h : hashes) {
+    for (size_t i = 0; i + bt <= tokens.size(); i += bt) {
+      const Hash h = block_hash(chain.empty() ? nullptr : &chain.back(), tokens.data() + i, bt, extra);
       uint32_t b;
       if (!p.reclaim(h, b)) {
         p.note_miss();
         break;
       }
+      chain.push_back(h);
       blocks.push_back(b);
       cached += bt;
     }
@@ -124,6 +130,7 @@ struct lmh_sched {
     if (!p.alloc(fresh, blocks)) {
       for (uint32_t b : blocks) p.release(b);
       blocks.clear();
+      chain.clear();
       return false;
     }
     return true;
@@ -147,8 +154,9 @@ struct lmh_sched {
     const int64_t q = free_kv_seq();
     if (q < 0) return false;
     std::vector<uint32_t> blocks;
+    std::vector<Hash> chain;
     uint64_t cached = 0;
-    if (!acquire(prompt, reserve_tokens(prompt, max_new), blocks, cached)) return false;
+    if (!acquire(prompt, reserve_tokens(prompt, max_new), blocks, cached, chain)) return false;
     Slot s;
     s.id = id = next_id++;
     s.priority = priority;
@@ -156,6 +164,8 @@ struct lmh_sched {
     s.max_new = max_new;
     s.seq_no = next_seq++;
     s.done = done = std::min<uint64_t>(cached, prompt.empty() ? 0 : prompt.size() - 1);
+    s.chain = std::move(chain);
+    s.chain_tokens.assign(prompt.begin(), prompt.begin() + cached);
     if (kv) {
       s.kv_seq = (uint64_t)q;
       kv_bind_seq(kv, s.kv_seq, blocks, s.done);
@@ -347,8 +357,21 @@ int32_t lmh_sched_publish(lmh_sched* s, uint32_t slot, const uint32_t* tokens, u
   if (full > blocks.size()) return s->fail(LMH_INVALID_ARGUMENT, "more full blocks than the slot holds");
   if (s->kv && full * p.block_tokens > kv_seq_len(s->kv, q->kv_seq))
     return s->fail(LMH_INVALID_ARGUMENT, "publishing positions the sequence has not written");
-  const std::vector<Hash> h = chain_hashes(tokens, full * p.block_tokens, p.block_tokens, s->extra);
-  for (uint64_t i = 0; i < full; i++) p.set_hash(blocks[i], h[i]);
+  // Sequence::publish hashes every full block of tokens[0..n]; the slot's memo of earlier hashes
+  // stands in for the blocks whose tokens it covers unchanged.
+  const uint32_t bt = p.block_tokens;
+  size_t k = 0;
+  const size_t have = std::min<size_t>(q->chain.size(), full);
+  while (k < have && std::memcmp(q->chain_tokens.data() + k * bt, tokens + k * bt, bt * 4) == 0) k++;
+  if (k < have) {  // the tokens differ from the memo's from block k on
+    q->chain.resize(k);
+    q->chain_tokens.resize(k * bt);
+  }
+  for (size_t i = q->chain.size(); i < full; i++) {
+    q->chain.push_back(block_hash(i ? &q->chain[i - 1] : nullptr, tokens + i * bt, bt, s->extra));
+    q->chain_tokens.insert(q->chain_tokens.end(), tokens + i * bt, tokens + (i + 1) * bt);
+  }
+  for (uint64_t i = 0; i < full; i++) p.set_hash(blocks[i], q->chain[i]);
   return LMH_OK;
 }
 
@@ -441,6 +464,27 @@ int32_t lmh_sched_queued_at(const lmh_sched* s, uint64_t i, lmh_queued_info* o) 
   if (!s || !o || i >= s->queue.size()) return LMH_INVALID_ARGUMENT;
   const Queued& q = s->queue[i];
   *o = lmh_queued_info{q.seq_no, q.prompt.size(), q.max_new, q.priority, 0};
+  return LMH_OK;
+}
+
+int32_t lmh_sha256(const uint8_t* msg, uint64_t n, int32_t path, uint8_t out[32]) {
+  if ((n > 0 && !msg) || !out || path < -1 || path > 1) return LMH_INVALID_ARGUMENT;
+  if (path < 0) {
+    Sha256 h;
+    h.update(msg, n);
+    const Hash d = h.finish();
+    std::memcpy(out, d.data(), 32);
+    return LMH_OK;
+  }
+  // the same padding as Sha256::finish, compressed by the requested path
+  std::vector<uint8_t> m(msg, msg + n);
+  m.push_back(0x80);
+  while (m.size() % 64 != 56) m.push_back(0);
+  for (int i = 0; i < 8; i++) m.push_back((uint8_t)((uint64_t)n * 8 >> (56 - 8 * i)));
+  uint32_t st[8] = {0x6a09e667u, 0xbb67ae85u, 0x3c6ef372u, 0xa54ff53au, 0x510e527fu, 0x9b05688cu, 0x1f83d9abu, 0x5be0cd19u};
+  if (!sha256_compress_path(path, st, m.data(), m.size() / 64)) return LMH_UNSUPPORTED;
+  for (int i = 0; i < 8; i++)
+    for (int j = 0; j < 4; j++) out[4 * i + j] = (uint8_t)(st[i] >> (24 - 8 * j));
   return LMH_OK;
 }
 

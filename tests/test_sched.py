@@ -95,6 +95,46 @@ def test_chain_hashes_match_sha256():
         assert chain_hashes(toks, max(n, 1), CacheKey()) == OS.chain_hashes(toks, max(n, 1), OS.CacheKey())
 
 
+@pytest.mark.parametrize("path", [-1, 0, 1])
+def test_sha256_paths_match_hashlib(path):
+    """Both compression paths (portable, x86 SHA extensions) and the one the library picked give
+    hashlib's digest at every length around the 55/56/64-byte padding boundaries and for a long
+    message; FIPS 180-2's "abc" known answer."""
+    import ctypes as C
+    import hashlib
+    rng = random.Random(11)
+    out = (C.c_uint8 * 32)()
+    msgs = [bytes(rng.randrange(256) for _ in range(n)) for n in list(range(0, 130)) + [1000, 65536]]
+    msgs.append(b"abc")
+    for m in msgs:
+        buf = C.create_string_buffer(m, max(len(m), 1))
+        rc = N.lib().lmh_sha256(buf, len(m), path, out)
+        if rc == N.UNSUPPORTED:
+            pytest.skip("this host has no SHA extensions")
+        assert rc == N.OK and bytes(out) == hashlib.sha256(m).digest(), len(m)
+    assert bytes(out).hex() == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+
+
+def test_publish_memo_follows_changed_tokens():
+    """publish() with tokens that differ from an earlier call's (from some block on) hashes the
+    new tokens: the pool ends up as if every full block were hashed afresh (the oracle's state)."""
+    s = Scheduler(64, 2, key(), n_blocks=16, block_tokens=4)
+    pool = O.Pool(16, 4, 16)
+    o = OS.Scheduler(64, 2, OS.CacheKey(bytes([7]), "f16"), pool)
+    a = s.admit(req(20, 0, Priority.Api)).slot
+    assert o.admit(list(range(20)), 0, 1)[1] == a
+    for toks in [list(range(12)), list(range(20)), list(range(8)) + [99] * 12, list(range(16)), list(range(20))]:
+        s.publish(a, toks)
+        o.publish(a, toks)
+        assert s.pool_stats() == pool.stats()
+    s.finish(a)
+    o.finish(a)
+    b = s.admit(req(20, 0, Priority.Api))
+    rb = o.admit(list(range(20)), 0, 1)
+    assert (b.slot, b.cached_tokens) == (rb[1], rb[2]) and b.cached_tokens == 19
+    assert s.pool_stats() == pool.stats()
+
+
 def test_error_paths():
     s = Scheduler(8, 2, key(), n_blocks=8, block_tokens=4)
     with pytest.raises(LmhError):
