@@ -10,8 +10,8 @@ launch stream during a second timed run of the same steps.
 
 Also reported (extra keys): every other configuration's throughput and roofline fraction, the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
-of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), and
-the CPU baseline
+of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), c5w
+with its layer in the sliding-window pool (`window_c5w`), and the CPU baseline
 (the C++ restatement of the reference's CPU attention, oracle/, on host cores).
 """
 
@@ -312,6 +312,77 @@ def time_sched(steps: int, warmup_s: float):
     return res
 
 
+def time_window(steps: int, warmup_s: float):
+    """c5w's step with its layer as a sliding-window layer in the window pool (window 4096: the
+    blocks behind each sequence's window are released), beside one full-attention layer of the
+    same shape that the step does not touch. Reported: the window layer's attend step and kernel
+    time (to compare with c5w, whose layer is paged), and the window pool's bytes held against the
+    paged blocks the same contexts take."""
+    import torch
+
+    from llmario_amd import _native as N
+    from llmario_amd.kv import HipKvCache, Layer, Segments
+    from llmario_amd.workloads import config
+
+    w = config("c5w")
+    L = w.layer
+    win = Layer(L.n_head, L.n_kv, L.hd, L.hdv, w.window)
+    hc = HipKvCache([win, Layer(L.n_head, L.n_kv, L.hd, L.hdv)], max_ctx=w.max_ctx(), n_seqs=w.n_seqs,
+                    kv_type=w.kv_type, block_tokens=16, pool_tokens=w.pool_tokens(), n_batch=max(w.new))
+    g = torch.Generator(device="cuda").manual_seed(5)
+    for s in range(w.n_seqs):   # the prior context, grown in calls of at most n_batch positions
+        while hc.len(s) < w.prior[s]:
+            segs_c, _ = hc.prepare_batch([(s, min(max(w.new), w.prior[s] - hc.len(s)))])
+            hc.commit_batch(segs_c)
+    segs_l, n = hc.prepare_batch([(s, w.new[s]) for s in range(w.n_seqs)])
+    assert segs_l == w.segments()
+    for s in range(w.n_seqs):   # rows of every live window block (positions the step can see)
+        first = max(w.prior[s] + 1 - w.window, 0) // 16 * 16
+        m = w.totals[s] - first
+        k = torch.randn((m, L.n_kv * L.hd), device="cuda", generator=g)
+        v = torch.randn((m, L.n_kv * L.hdv), device="cuda", generator=g)
+        hc.store(0, [(s, 0, m, first)], k, v)
+    segs = Segments(segs_l)
+    q = torch.randn((n, L.n_head, L.hd), device="cuda", generator=g)
+    out = torch.empty((n, L.n_head, L.hdv), device="cuda")
+    stream = torch.cuda.current_stream()
+    t_w = time.perf_counter()
+    while time.perf_counter() - t_w < warmup_s:
+        for _ in range(8):
+            hc.attend(0, segs, q, out, w.scale, w.window, stream)
+        torch.cuda.synchronize()
+    res = {"config": "window_c5w", "rows": n, "bytes": w.algorithmic_bytes()}
+    for events in (False, True):
+        hc.kernel_times()
+        hc.set_timing(events)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            hc.attend(0, segs, q, out, w.scale, w.window, stream)
+        torch.cuda.synchronize()
+        el = time.perf_counter() - t0
+        hc.set_timing(False)
+        if events:
+            kt = hc.kernel_times()
+            res["prefill_ms"] = kt["prefill"][0] / max(kt["prefill"][1], 1)
+            res["decode_ms"] = kt["decode"][0] / max(kt["decode"][1], 1)
+        else:
+            res["ms_per_step"] = el * 1e3 / steps
+    import ctypes as C
+    wi = N.WindowInfo()
+    N.lib().lmh_kv_window_info(hc.h, C.byref(wi))
+    live = wi.pool_blocks - wi.free_blocks
+    paged_equiv = sum((t + 15) // 16 for t in w.totals)
+    res.update(window_blocks_live=live, window_pool_blocks=wi.pool_blocks, paged_blocks_same_contexts=paged_equiv,
+               window_pool_bytes=wi.pool_blocks * wi.block_bytes, paged_bytes_same_contexts=paged_equiv * wi.block_bytes)
+    res["GBps"] = res["bytes"] / (res["ms_per_step"] * 1e-3) / 1e9
+    log(f"[bench] window_c5w: {res['ms_per_step'] * 1e3:.1f} us/step (prefill {res['prefill_ms'] * 1e3:.1f} us, decode "
+        f"{res['decode_ms'] * 1e3:.1f} us); window blocks live {live} of {wi.pool_blocks}, paged equivalent {paged_equiv}")
+    del hc
+    torch.cuda.empty_cache()
+    return res
+
+
 def physical_cores() -> int:
     try:
         cores = set()
@@ -367,7 +438,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5",
+    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5,window_c5w",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--extra-warmup-s", type=float, default=0.2,
@@ -408,6 +479,9 @@ def main():
     if args.profile_config == "sched_c5":
         print(json.dumps(time_sched(args.steps, args.extra_warmup_s)), flush=True)
         return
+    if args.profile_config == "window_c5w":
+        print(json.dumps(time_window(args.steps, args.extra_warmup_s)), flush=True)
+        return
     if args.profile_config:
         res = time_config(args.profile_config, args.steps, args.warmup, warmup_s=args.extra_warmup_s)
         print(json.dumps(res), flush=True)
@@ -422,6 +496,8 @@ def main():
             extra[name] = time_snapshot(max(5, min(args.steps, 20)), args.extra_warmup_s)
         elif name == "sched_c5":
             extra[name] = time_sched(max(5, min(args.steps, 40)), args.extra_warmup_s)
+        elif name == "window_c5w":
+            extra[name] = time_window(max(5, min(args.steps, 20)), args.extra_warmup_s)
         else:
             extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define LMH_ABI_VERSION 1u
+#define LMH_ABI_VERSION 2u
 
 /* status codes */
 #define LMH_OK 0
@@ -49,12 +49,17 @@ extern "C" {
 typedef struct lmh_kv lmh_kv; /* opaque: the device page pool + host block bookkeeping */
 
 /* Per attention layer geometry: AttnGeom (model/src/arch.rs:73-95) restricted to what the cache
- * and the kernels read. */
+ * and the kernels read. A sliding-window layer (`window` > 0, the reference's `AttnGeom::window`)
+ * keeps its rows in the window pool (metal/src/kv.rs:13-17, 37-47): blocks addressed by absolute
+ * block number, each released once every position in it is at least `window` behind the
+ * sequence's next token. All window layers share one width; at least one layer is not windowed. */
 typedef struct lmh_layer_desc {
   uint32_t n_head;
   uint32_t n_kv;
   uint32_t hd;
   uint32_t hdv;
+  uint32_t window;      /* sliding-window width (0 = full attention, in the paged blocks) */
+  uint32_t reserved0;
 } lmh_layer_desc;
 
 /* KvOptions (kv.rs:328-375). */
@@ -68,7 +73,8 @@ typedef struct lmh_kv_options {
   uint64_t n_seqs;
   uint64_t pool_tokens; /* 0 = None: every sequence can hold max_ctx at once */
   int32_t device;       /* HIP device ordinal */
-  uint32_t reserved0;
+  uint32_t n_batch;     /* most positions one call appends to one sequence: sizes the window pool
+                           (metal/src/kv.rs:130-133); 0 = 512, the plan's default n_batch */
 } lmh_kv_options;
 
 /* KvLayout (kv.rs:377-400): sizes are the reference's for the same options. */
@@ -121,6 +127,16 @@ int32_t lmh_kv_clear(lmh_kv* kv, uint64_t seq);
 /* The sequence's block table (BlockTable::locate, kv/src/lib.rs:243-253): writes up to `cap`
  * ids, returns the count in *n. */
 int32_t lmh_kv_block_table(const lmh_kv* kv, uint64_t seq, uint32_t* out, uint64_t cap, uint64_t* n);
+/* The window pool (present when a layer has a window): its width, block bytes, blocks and free
+ * blocks; and a sequence's window blocks by absolute block number (-1: released or never taken). */
+typedef struct lmh_window_info {
+  uint64_t window;
+  uint64_t block_bytes;
+  uint64_t pool_blocks;
+  uint64_t free_blocks;
+} lmh_window_info;
+int32_t lmh_kv_window_info(const lmh_kv* kv, lmh_window_info* out);
+int32_t lmh_kv_window_table(const lmh_kv* kv, uint64_t seq, int32_t* out, uint64_t cap, uint64_t* n);
 /* Test and benchmark hook: give an empty sequence exactly these free blocks, in order (e.g. a
  * seeded permutation of the pool), as if reserve had handed them out. */
 int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, uint64_t n);

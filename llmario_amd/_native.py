@@ -17,24 +17,28 @@ STATUS_NAMES = {0: "OK", 1: "INVALID_ARGUMENT", 2: "KV_FULL", 3: "UNSUPPORTED", 
                 5: "OUT_OF_MEMORY"}
 KV_F16, KV_Q8_0, KV_F32, KV_BF16 = 0, 1, 2, 3
 KV_TYPES = {"f16": KV_F16, "q8_0": KV_Q8_0, "f32": KV_F32, "bf16": KV_BF16}
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 u32, u64, i32, P = C.c_uint32, C.c_uint64, C.c_int32, C.c_void_p
 
 
 class LayerDesc(C.Structure):
-    _fields_ = [("n_head", u32), ("n_kv", u32), ("hd", u32), ("hdv", u32)]
+    _fields_ = [("n_head", u32), ("n_kv", u32), ("hd", u32), ("hdv", u32), ("window", u32), ("reserved0", u32)]
 
 
 class KvOptions(C.Structure):
     _fields_ = [("abi_version", u32), ("kv_type", u32), ("block_tokens", u32), ("n_layers", u32),
                 ("layers", C.POINTER(LayerDesc)), ("max_ctx", u64), ("n_seqs", u64),
-                ("pool_tokens", u64), ("device", i32), ("reserved0", u32)]
+                ("pool_tokens", u64), ("device", i32), ("n_batch", u32)]
 
 
 class LayoutInfo(C.Structure):
     _fields_ = [("block_bytes", u64), ("blocks_per_seq", u64), ("n_seqs", u64), ("pool_blocks", u64),
                 ("max_ctx", u64), ("block_tokens", u32), ("kv_type", u32)]
+
+
+class WindowInfo(C.Structure):
+    _fields_ = [("window", u64), ("block_bytes", u64), ("pool_blocks", u64), ("free_blocks", u64)]
 
 
 class SeqTokens(C.Structure):
@@ -114,6 +118,8 @@ SIGNATURES = {
     "lmh_kv_truncate": (i32, [P, u64, u64]),
     "lmh_kv_clear": (i32, [P, u64]),
     "lmh_kv_block_table": (i32, [P, u64, P, u64, C.POINTER(u64)]),
+    "lmh_kv_window_info": (i32, [P, C.POINTER(WindowInfo)]),
+    "lmh_kv_window_table": (i32, [P, u64, P, u64, C.POINTER(u64)]),
     "lmh_kv_adopt_blocks": (i32, [P, u64, P, u64]),
     "lmh_kv_snapshot_bytes": (i32, [P, u64, C.POINTER(u64)]),
     "lmh_kv_write_seq": (i32, [P, u64, P, u64, C.POINTER(u64), P]),

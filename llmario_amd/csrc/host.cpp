@@ -39,6 +39,7 @@ thread_local std::string g_create_error;
 
 struct LayerLayout {
   uint32_t n_head, n_kv, hd, hdv;
+  bool win;               // sliding-window layer: offsets are inside a window-pool block
   uint64_t k_row, v_row;  // the reference's row bytes (encoded I/O)
   uint32_t k_off, v_off, k_head, v_head, k_tile, v_tile, k_scale, v_scale, k_tile_s, v_tile_s;
 };
@@ -143,6 +144,7 @@ struct DevBuf {  // grow-only device scratch
 
 struct Seq {
   std::vector<uint32_t> blocks;
+  std::vector<int32_t> wblocks;  // window-pool block by absolute block number (-1: released / none)
   uint64_t len = 0;
 };
 
@@ -151,6 +153,7 @@ struct Seq {
 // or copy a shared block for copy-on-write.
 struct PageOp {
   int32_t src, dst;
+  int32_t win = 0;  // 1: a block of the window pool (zeroing only)
 };
 
 }  // namespace
@@ -163,6 +166,14 @@ struct lmh_kv {
   // ---- BlockPool (kv/src/lib.rs:36-176)
   BlockPool pool;
   std::vector<uint8_t> backed;
+  // ---- window pool (metal/src/kv.rs:37-47): window layers' rows, blocks released behind the window
+  uint64_t window = 0;           // width shared by the window layers (0: none)
+  uint64_t wblock_bytes = 0, wpool_blocks = 0;
+  BlockPool wpool;
+  uint8_t* d_wpool = nullptr;
+  int32_t* d_wtable = nullptr;
+  std::vector<int32_t> h_wtable;
+  bool wtable_dirty = false;
   // ---- sequences
   std::vector<Seq> seqs;
   // ---- device
@@ -195,12 +206,14 @@ struct lmh_kv {
   std::string err;
 
   ~lmh_kv() {
-    if (d_pool || d_table) (void)hipDeviceSynchronize();
+    if (d_pool || d_table || d_wpool) (void)hipDeviceSynchronize();
     if (fork) (void)hipEventDestroy(fork);
     if (join) (void)hipEventDestroy(join);
     if (side) (void)hipStreamDestroy(side);
     if (d_pool) (void)hipFree(d_pool);
     if (d_table) (void)hipFree(d_table);
+    if (d_wpool) (void)hipFree(d_wpool);
+    if (d_wtable) (void)hipFree(d_wtable);
     for (auto& p : evs) {
       (void)hipEventDestroy(p.first);
       (void)hipEventDestroy(p.second);
@@ -241,6 +254,62 @@ struct lmh_kv {
     table_dirty = true;
   }
 
+  // ---- window pool (metal/src/kv.rs:304-372) ---------------------------------------------
+  // The query at position len sees keys p > len - window: window blocks before this one are dead.
+  uint64_t first_live(uint64_t len) const { return (len + 1 > window ? len + 1 - window : 0) / bt; }
+  void set_wtable(uint64_t s) {
+    int32_t* row = h_wtable.data() + s * bps;
+    const auto& wb = seqs[s].wblocks;
+    for (uint64_t i = 0; i < bps; i++) row[i] = i < wb.size() ? wb[i] : -1;
+    wtable_dirty = true;
+  }
+  // Window blocks reserve_window(s, len, new_len) releases and takes (whole calls are checked
+  // before any change, so a short window pool fails like a short paged pool: nothing changes).
+  void window_delta(uint64_t s, uint64_t len, uint64_t new_len, uint64_t& take, uint64_t& give) const {
+    take = give = 0;
+    if (!window) return;
+    const auto& wb = seqs[s].wblocks;
+    const uint64_t first = first_live(len), need = (new_len + bt - 1) / bt;
+    for (uint64_t i = 0; i < std::min<uint64_t>(first, wb.size()); i++) give += wb[i] >= 0 ? 1 : 0;
+    for (uint64_t i = std::max<uint64_t>(wb.size(), first); i < need; i++) take++;
+  }
+  void release_wblock(int32_t& slot) {
+    if (slot >= 0) wpool.release((uint32_t)slot);
+    slot = -1;
+  }
+  // Release the window blocks no query from position len on can see, then take blocks (zeroed
+  // before the next device call) for every block up to new_len. Checked by window_delta first.
+  void reserve_window(uint64_t s, uint64_t len, uint64_t new_len) {
+    if (!window) return;
+    auto& wb = seqs[s].wblocks;
+    const uint64_t first = first_live(len), need = (new_len + bt - 1) / bt;
+    for (uint64_t i = 0; i < std::min<uint64_t>(first, wb.size()); i++) release_wblock(wb[i]);
+    if (wb.size() < first && wb.size() < need) wb.resize(std::min(first, need), -1);
+    while (wb.size() < need) {
+      std::vector<uint32_t> nb;
+      wpool.alloc(1, nb);
+      pending.push_back({-1, (int32_t)nb[0], 1});
+      wb.push_back((int32_t)nb[0]);
+    }
+    set_wtable(s);
+  }
+  void release_window_from(uint64_t s, uint64_t from) {
+    auto& wb = seqs[s].wblocks;
+    while (wb.size() > from) {
+      release_wblock(wb.back());
+      wb.pop_back();
+    }
+    set_wtable(s);
+  }
+  // every window block a row at position pos of sequence s touches is live: its own (lo = pos)
+  // or those of its attention range [lo, pos]
+  bool window_live(uint64_t s, uint64_t lo, uint64_t hi) const {
+    const auto& wb = seqs[s].wblocks;
+    for (uint64_t b = lo / bt; b <= hi / bt; b++)
+      if (b >= wb.size() || wb[b] < 0) return false;
+    return true;
+  }
+
   // kv.rs:715-725
   uint64_t blocks_needed(uint64_t s, uint64_t new_len) const {
     const Seq& q = seqs[s];
@@ -251,7 +320,7 @@ struct lmh_kv {
   }
 
   // kv.rs:730-785
-  int32_t reserve(uint64_t s, uint64_t new_len, uint64_t* needed, uint64_t* free_blocks) {
+  int32_t reserve(uint64_t s, uint64_t new_len, uint64_t* needed, uint64_t* free_blocks, bool with_window = true) {
     if (new_len > max_ctx) return fail(LMH_INVALID_ARGUMENT, "context overflow");
     const uint64_t len = seqs[s].len;
     const uint64_t want = (new_len + bt - 1) / bt;
@@ -264,6 +333,15 @@ struct lmh_kv {
       return fail(LMH_KV_FULL, "KV cache full: " + std::to_string(wanted) + " more blocks needed, " +
                                    std::to_string(pool.free_q.size()) + " free");
     }
+    uint64_t w_take = 0, w_give = 0;
+    if (with_window) window_delta(s, len, new_len, w_take, w_give);
+    if (w_take > wpool.free_q.size() + w_give) {
+      if (needed) *needed = w_take;
+      if (free_blocks) *free_blocks = wpool.free_q.size() + w_give;
+      return fail(LMH_KV_FULL, "window pool full: " + std::to_string(w_take) + " window blocks needed, " +
+                                   std::to_string(wpool.free_q.size() + w_give) + " free");
+    }
+    if (with_window) reserve_window(s, len, new_len);
     if (len % bt != 0 && len < new_len) {
       const uint64_t bi = len / bt;
       const uint32_t old = seqs[s].blocks[bi];
@@ -293,6 +371,16 @@ struct lmh_kv {
   // kv.rs:792-816 (paged layers: no rings, no recurrent state)
   void truncate(uint64_t s, uint64_t n) {
     n = std::min(n, seqs[s].len);
+    // metal/src/kv.rs:393-405: when a window block the next query needs is already released,
+    // the whole sequence is cleared instead
+    if (window && n > 0) {
+      const uint64_t last = (n + bt - 1) / bt;
+      for (uint64_t i = first_live(n); i < last; i++)
+        if (i >= seqs[s].wblocks.size() || seqs[s].wblocks[i] < 0) {
+          n = 0;
+          break;
+        }
+    }
     seqs[s].len = n;
     const uint64_t keep = (n + bt - 1) / bt;
     while (seqs[s].blocks.size() > keep) {
@@ -301,6 +389,7 @@ struct lmh_kv {
       release_block(b);
     }
     set_table(s);
+    if (window) release_window_from(s, keep);
   }
   void clear(uint64_t s) {  // kv.rs:820-827
     seqs[s].len = 0;
@@ -310,6 +399,7 @@ struct lmh_kv {
       release_block(b);
     }
     set_table(s);
+    if (window) release_window_from(s, 0);
   }
 
   // ---- device helpers --------------------------------------------------------------------
@@ -321,15 +411,16 @@ struct lmh_kv {
       if (pending[i].src < 0) {
         size_t j = i;
         std::vector<int32_t> zb;
-        while (j < pending.size() && pending[j].src < 0) zb.push_back(pending[j++].dst);
+        const int32_t w = pending[i].win;
+        while (j < pending.size() && pending[j].src < 0 && pending[j].win == w) zb.push_back(pending[j++].dst);
         int idx;
         uint8_t* h;
         if ((e = up.acquire(zb.size() * 4, idx, h)) != hipSuccess) return hip_fail(e, "staging");
         std::memcpy(h, zb.data(), zb.size() * 4);
         if ((e = ops_buf.ensure(zb.size() * 4)) != hipSuccess) return hip_fail(e, "hipMalloc");
         if ((e = up.send(idx, ops_buf.p, zb.size() * 4, st)) != hipSuccess) return hip_fail(e, "upload");
-        if ((e = launch_zero_blocks(d_pool, block_bytes, (const int32_t*)ops_buf.p, (uint32_t)zb.size(), st)) !=
-            hipSuccess)
+        if ((e = launch_zero_blocks(w ? d_wpool : d_pool, w ? wblock_bytes : block_bytes, (const int32_t*)ops_buf.p,
+                                    (uint32_t)zb.size(), st)) != hipSuccess)
           return hip_fail(e, "zero kernel");
         i = j;
       } else {
@@ -349,14 +440,23 @@ struct lmh_kv {
       if ((e = up.send(idx, d_table, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
       table_dirty = false;
     }
+    if (wtable_dirty) {
+      int idx;
+      uint8_t* h;
+      const size_t bytes = h_wtable.size() * 4;
+      if ((e = up.acquire(bytes, idx, h)) != hipSuccess) return hip_fail(e, "staging");
+      std::memcpy(h, h_wtable.data(), bytes);
+      if ((e = up.send(idx, d_wtable, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
+      wtable_dirty = false;
+    }
     return LMH_OK;
   }
 
   PageGeom geom(uint32_t l) const {
     const LayerLayout& y = layers[l];
     PageGeom g{};
-    g.pool = d_pool;
-    g.block_bytes = block_bytes;
+    g.pool = y.win ? d_wpool : d_pool;
+    g.block_bytes = y.win ? wblock_bytes : block_bytes;
     g.k_off = y.k_off;
     g.v_off = y.v_off;
     g.k_head = y.k_head;
@@ -369,12 +469,28 @@ struct lmh_kv {
     g.v_tile_s = y.v_tile_s;
     g.bt_shift = bt_shift;
     g.bps = (uint32_t)bps;
-    g.table = d_table;
+    g.table = y.win ? d_wtable : d_table;
     g.kv_type = kv_type;
     g.n_kv = y.n_kv;
     g.hd = y.hd;
     g.hdv = y.hdv;
     return g;
+  }
+
+  // A window layer's rows exist only while their window blocks are live: every row of the segments
+  // must have its own block live (store / gather), or, with attn_window > 0, every block of its
+  // attention range [pos + 1 - attn_window, pos] (attend).
+  int32_t check_window_rows(uint32_t layer, const lmh_seg* segs, uint64_t n_segs, uint64_t attn_window) {
+    if (!layers[layer].win) return LMH_OK;
+    for (uint64_t i = 0; i < n_segs; i++) {
+      const lmh_seg& sg = segs[i];
+      if (sg.n == 0) continue;
+      const uint64_t first = sg.pos0, last = sg.pos0 + sg.n - 1;
+      const uint64_t lo = attn_window == 0 ? first : (first + 1 > attn_window ? first + 1 - attn_window : 0);
+      if (!window_live(sg.seq, lo, last))
+        return fail(LMH_INVALID_ARGUMENT, "window layer rows outside the sequence's live window blocks");
+    }
+    return LMH_OK;
   }
 
   // Validate segments against the tables; fill row_seq/row_pos. Rows must be stacked in segment
@@ -493,6 +609,7 @@ namespace lmh {
 BlockPool& kv_pool(lmh_kv* kv) { return kv->pool; }
 uint64_t kv_n_seqs(const lmh_kv* kv) { return kv->n_seqs; }
 uint64_t kv_max_ctx(const lmh_kv* kv) { return kv->max_ctx; }
+bool kv_has_window(const lmh_kv* kv) { return kv->window > 0; }
 uint64_t kv_seq_len(const lmh_kv* kv, uint64_t seq) { return kv->seqs[seq].len; }
 bool kv_seq_empty(const lmh_kv* kv, uint64_t seq) { return kv->seqs[seq].blocks.empty() && kv->seqs[seq].len == 0; }
 const std::vector<uint32_t>& kv_seq_blocks(const lmh_kv* kv, uint64_t seq) { return kv->seqs[seq].blocks; }
@@ -551,9 +668,17 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   kv->max_ctx = std::max<uint64_t>(o->max_ctx, 1);
   kv->n_seqs = std::max<uint64_t>(o->n_seqs, 1);
   // KvLayout::new (kv.rs:402-497): per layer K rows then V rows of bt positions; same byte totals.
-  uint64_t off = 0;
+  // Window layers (which the reference keeps in rings, outside the block) go to the window pool's
+  // blocks, laid out the same way (metal/src/kv.rs:111-126).
+  uint64_t off = 0, woff = 0;
   for (uint32_t l = 0; l < o->n_layers; l++) {
     const lmh_layer_desc& d = o->layers[l];
+    if (d.window > 0 && kv->window > 0 && d.window != kv->window) {
+      delete kv;
+      g_create_error = "sliding-window layers with different widths";
+      return LMH_UNSUPPORTED;
+    }
+    if (d.window > 0) kv->window = d.window;
     if (d.n_kv == 0 || d.n_head == 0 || d.n_head % d.n_kv != 0 || d.hd == 0 || d.hdv == 0) {
       delete kv;
       g_create_error = "bad layer geometry";
@@ -585,13 +710,21 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
     y.v_scale = tiles * y.v_tile;
     y.k_head = tiles * (y.k_tile + y.k_tile_s);
     y.v_head = tiles * (y.v_tile + y.v_tile_s);
-    y.k_off = (uint32_t)off;
-    off += (uint64_t)d.n_kv * y.k_head;
-    y.v_off = (uint32_t)off;
-    off += (uint64_t)d.n_kv * y.v_head;
+    y.win = d.window > 0;
+    uint64_t& o_ = y.win ? woff : off;
+    y.k_off = (uint32_t)o_;
+    o_ += (uint64_t)d.n_kv * y.k_head;
+    y.v_off = (uint32_t)o_;
+    o_ += (uint64_t)d.n_kv * y.v_head;
     kv->layers.push_back(y);
   }
+  if (off == 0) {
+    delete kv;
+    g_create_error = "every layer is a window layer (at least one full-attention layer is needed)";
+    return LMH_UNSUPPORTED;
+  }
   kv->block_bytes = off;
+  kv->wblock_bytes = woff;
   kv->bps = (kv->max_ctx + bt - 1) / bt;
   if (o->pool_tokens > 0) {
     const uint64_t t = o->pool_tokens;
@@ -608,6 +741,15 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   kv->backed.assign(kv->pool_blocks, 0);
   kv->seqs.assign(kv->n_seqs, Seq{});
   kv->h_table.assign(kv->n_seqs * kv->bps, -1);
+  if (kv->window) {
+    // metal/src/kv.rs:130-133: a sequence's live window blocks are the window behind its first new
+    // token plus one call's tokens, and a partial block at each end
+    const uint64_t n_batch = o->n_batch ? o->n_batch : 512;
+    kv->wpool_blocks = kv->n_seqs * std::min<uint64_t>((kv->window + n_batch + bt - 1) / bt + 1, kv->bps);
+    kv->wpool.init(kv->wpool_blocks, bt);
+    kv->h_wtable.assign(kv->n_seqs * kv->bps, -1);
+    kv->wtable_dirty = true;
+  }
   kv->device = o->device;
   hipError_t e = hipSetDevice(o->device);
   int n_cu = 0;
@@ -619,6 +761,8 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_pool, kv->pool_blocks * kv->block_bytes);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
+  if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wpool, kv->wpool_blocks * kv->wblock_bytes);
+  if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wtable, kv->h_wtable.size() * 4);
   if (e != hipSuccess) {
     g_create_error = std::string("device allocation failed: ") + hipGetErrorString(e);
     delete kv;
@@ -658,7 +802,10 @@ uint64_t lmh_kv_fingerprint(const lmh_kv* kv) {
   h.u64(kv->bt);
   h.u64(kv->block_bytes);
   h.u64(kv->max_ctx);
+  h.u64(kv->window);
+  h.u64(kv->wblock_bytes);
   for (const auto& y : kv->layers) {
+    h.u64(y.win ? 1 : 0);
     h.u64(y.n_kv);
     h.u64(y.hd);
     h.u64(y.hdv);
@@ -679,6 +826,12 @@ int32_t lmh_kv_seq_len(const lmh_kv* kv, uint64_t seq, uint64_t* len) {
 int32_t lmh_kv_set_seq_len(lmh_kv* kv, uint64_t seq, uint64_t len) {
   if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
   if (len > kv->seqs[seq].blocks.size() * kv->bt) return kv->fail(LMH_INVALID_ARGUMENT, "length beyond reserved blocks");
+  if (kv->window) {  // the window blocks the next query can see: [first_live(len), ceil(len / bt))
+    uint64_t take, give;
+    kv->window_delta(seq, len, len, take, give);
+    if (take > kv->wpool.free_q.size() + give) return kv->fail(LMH_KV_FULL, "window pool full");
+    kv->reserve_window(seq, len, len);
+  }
   kv->seqs[seq].len = len;
   return LMH_OK;
 }
@@ -721,27 +874,53 @@ int32_t lmh_kv_clear(lmh_kv* kv, uint64_t seq) {
 }
 
 // ---- snapshots (kv.rs:1009-1130), paged layers: whole blocks in the reference's block format ----
+// With window layers, the paged blocks are followed by the window blocks a query after len can
+// still see, [first_live(len), ceil(len / bt)), each in the same block format restricted to the
+// window layers (Metal's snapshot, metal/src/kv.rs:455-490).
+static void window_span(const lmh_kv* kv, uint64_t len, uint64_t& first, uint64_t& end) {
+  first = end = 0;
+  if (!kv->window) return;
+  first = kv->first_live(len);
+  end = std::max<uint64_t>((len + kv->bt - 1) / kv->bt, first);
+}
+
 int32_t lmh_kv_snapshot_bytes(const lmh_kv* kv, uint64_t len, uint64_t* bytes) {
   if (!kv || !bytes) return LMH_INVALID_ARGUMENT;
-  *bytes = len == 0 ? 0 : (len + kv->bt - 1) / kv->bt * kv->block_bytes;
+  uint64_t first, end;
+  window_span(kv, len, first, end);
+  *bytes = len == 0 ? 0 : (len + kv->bt - 1) / kv->bt * kv->block_bytes + (end - first) * kv->wblock_bytes;
   return LMH_OK;
 }
 
 // One launch per layer over the positions of the sequence's first n_blocks blocks; the layer's
 // region of a reference block starts after the earlier layers' bt*(k_row + v_row) bytes
 // (KvLayout::new, kv.rs:402-497).
+// Window layers: the same per block, over window blocks first..end of the window table (the
+// table row is entered at `first`, so the kernels' block index counts from there) after the paged part.
 static int32_t snapshot_layers(lmh_kv* kv, bool write, uint64_t seq, uint64_t n_blocks, uint8_t* bytes,
                                hipStream_t st) {
-  uint64_t ref_off = 0;
+  uint64_t first, end;
+  window_span(kv, kv->seqs[seq].len, first, end);
+  uint64_t ref_off = 0, wref_off = 0;
   for (uint32_t l = 0; l < kv->layers.size(); l++) {
     const LayerLayout& y = kv->layers[l];
+    PageGeom g = kv->geom(l);
+    uint64_t n_pos = n_blocks * kv->bt, bb = kv->block_bytes, off = ref_off;
+    uint8_t* at = bytes;
+    if (y.win) {
+      g.table += first;
+      n_pos = (end - first) * kv->bt;
+      bb = kv->wblock_bytes;
+      off = wref_off;
+      at = bytes + n_blocks * kv->block_bytes;
+    }
     hipError_t e = kv->time_begin(st, LMH_KERNEL_SNAPSHOT);
     if (e == hipSuccess)
-      e = launch_snapshot(write, kv->geom(l), (uint32_t)seq, (uint32_t)(n_blocks * kv->bt), kv->bt, kv->block_bytes,
-                          ref_off, (uint32_t)y.k_row, (uint32_t)y.v_row, bytes, st);
+      e = launch_snapshot(write, g, (uint32_t)seq, (uint32_t)n_pos, kv->bt, bb, off, (uint32_t)y.k_row, (uint32_t)y.v_row,
+                          at, st);
     if (e == hipSuccess) e = kv->time_end(st);
     if (e != hipSuccess) return kv->hip_fail(e, "snapshot kernel");
-    ref_off += kv->bt * (y.k_row + y.v_row);
+    (y.win ? wref_off : ref_off) += kv->bt * (y.k_row + y.v_row);
   }
   return LMH_OK;
 }
@@ -754,6 +933,10 @@ int32_t lmh_kv_write_seq(lmh_kv* kv, uint64_t seq, void* dst, uint64_t cap, uint
   if (written) *written = bytes;
   if (bytes == 0) return LMH_OK;
   if (!dst || cap < bytes) return kv->fail(LMH_INVALID_ARGUMENT, "snapshot destination smaller than snapshot_bytes(len)");
+  uint64_t first, end;
+  window_span(kv, len, first, end);
+  if (end > first && !kv->window_live(seq, first * kv->bt, end * kv->bt - 1))
+    return kv->fail(LMH_INVALID_ARGUMENT, "a window block the snapshot needs is not live");
   hipStream_t st = (hipStream_t)stream;
   int32_t rc = kv->flush(st);
   if (rc != LMH_OK) return rc;
@@ -776,14 +959,50 @@ int32_t lmh_kv_read_seq(lmh_kv* kv, uint64_t seq, uint64_t len, const void* src,
     if (free_blocks) *free_blocks = kv->pool.free_q.size() + own;
     return kv->fail(LMH_KV_FULL, "KV cache full: snapshot needs " + std::to_string(nb) + " blocks");
   }
+  uint64_t first, end;
+  window_span(kv, len, first, end);
+  uint64_t wown = 0;
+  for (int32_t b : kv->seqs[seq].wblocks) wown += b >= 0 ? 1 : 0;
+  if (end - first > kv->wpool.free_q.size() + wown) {
+    if (needed) *needed = end - first;
+    if (free_blocks) *free_blocks = kv->wpool.free_q.size() + wown;
+    return kv->fail(LMH_KV_FULL, "window pool full: snapshot needs " + std::to_string(end - first) + " window blocks");
+  }
   kv->clear(seq);
   if (len == 0) return LMH_OK;
-  int32_t rc = kv->reserve(seq, len, needed, free_blocks);
+  // paged blocks only; the window blocks go at their absolute numbers (metal/src/kv.rs:508-537)
+  int32_t rc = kv->reserve(seq, len, needed, free_blocks, false);
   if (rc != LMH_OK) return rc;
+  if (kv->window) {
+    auto& wb = kv->seqs[seq].wblocks;
+    wb.assign(first, -1);
+    for (uint64_t i = first; i < end; i++) {
+      std::vector<uint32_t> b1;
+      kv->wpool.alloc(1, b1);
+      wb.push_back((int32_t)b1[0]);
+    }
+    kv->set_wtable(seq);
+  }
   hipStream_t st = (hipStream_t)stream;
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
-  if ((rc = snapshot_layers(kv, false, seq, nb, (uint8_t*)src, st)) != LMH_OK) return rc;
   kv->seqs[seq].len = len;
+  return snapshot_layers(kv, false, seq, nb, (uint8_t*)src, st);
+}
+
+int32_t lmh_kv_window_info(const lmh_kv* kv, lmh_window_info* out) {
+  if (!kv || !out) return LMH_INVALID_ARGUMENT;
+  out->window = kv->window;
+  out->block_bytes = kv->wblock_bytes;
+  out->pool_blocks = kv->wpool_blocks;
+  out->free_blocks = kv->wpool.free_q.size();
+  return LMH_OK;
+}
+
+int32_t lmh_kv_window_table(const lmh_kv* kv, uint64_t seq, int32_t* out, uint64_t cap, uint64_t* n) {
+  if (!kv || !n || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
+  const auto& b = kv->seqs[seq].wblocks;
+  for (uint64_t i = 0; i < b.size() && i < cap && out; i++) out[i] = b[i];
+  *n = b.size();
   return LMH_OK;
 }
 
@@ -877,6 +1096,24 @@ int32_t lmh_batch_prepare(lmh_kv* kv, const lmh_seq_tokens* batch, uint64_t n, l
     return kv->fail(LMH_KV_FULL, "KV cache full: " + std::to_string(need) + " more blocks needed, " +
                                      std::to_string(kv->pool.free_q.size()) + " free");
   }
+  if (kv->window) {  // the window pool, entry by entry in batch order (each releases before it takes)
+    uint64_t free = kv->wpool.free_q.size(), w_need = 0;
+    bool short_ = false;
+    for (uint64_t i = 0; i < n; i++) {
+      uint64_t take, give;
+      const uint64_t len = kv->seqs[batch[i].seq].len;
+      kv->window_delta(batch[i].seq, len, len + batch[i].n_tokens, take, give);
+      free += give;
+      w_need += take;
+      if (take > free) short_ = true;
+      free -= std::min(take, free);
+    }
+    if (short_) {
+      if (needed) *needed = w_need;
+      if (free_blocks) *free_blocks = kv->wpool.free_q.size();
+      return kv->fail(LMH_KV_FULL, "window pool full: " + std::to_string(w_need) + " window blocks needed");
+    }
+  }
   for (uint64_t i = 0; i < n; i++) kv->reserve(batch[i].seq, kv->seqs[batch[i].seq].len + batch[i].n_tokens, nullptr, nullptr);
   uint64_t start = 0;
   for (uint64_t i = 0; i < n; i++) {
@@ -942,6 +1179,7 @@ static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n
   int32_t rc = kv->rows_from(segs, n_segs, n_rows);
   if (rc != LMH_OK) return rc;
   if (n_rows == 0) return LMH_OK;
+  if ((rc = kv->check_window_rows(layer, segs, n_segs, 0)) != LMH_OK) return rc;
   if (!a || !b) return kv->fail(LMH_INVALID_ARGUMENT, "null data pointer");
   hipStream_t st = (hipStream_t)stream;
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
@@ -1007,6 +1245,7 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
     return kv->fail(LMH_INVALID_ARGUMENT, "q_stride must be a multiple of 4 and the arrays 16-byte aligned");
   uint64_t n_rows;
   int32_t rc = kv->rows_from(segs, n_segs, n_rows);
+  if (rc == LMH_OK) rc = kv->check_window_rows(layer, segs, n_segs, 0);
   if (rc != LMH_OK) return rc;
   if (n_rows == 0) return LMH_OK;
   if (!q_in || !k_in || !v_in || !q_out) return kv->fail(LMH_INVALID_ARGUMENT, "null data pointer");
@@ -1043,6 +1282,10 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   if (n_rows == 0) return LMH_OK;
   if (!q || !out) return kv->fail(LMH_INVALID_ARGUMENT, "null q/out");
   const LayerLayout& y = kv->layers[layer];
+  // a window layer attends within its width: its pool holds nothing older
+  if (y.win && (window == 0 || window > kv->window))
+    return kv->fail(LMH_INVALID_ARGUMENT, "a window layer's attention window must be 1..its width");
+  if ((rc = kv->check_window_rows(layer, segs, n_segs, window)) != LMH_OK) return rc;
   const uint32_t group = y.n_head / y.n_kv;
   const uint32_t ng = std::min<uint32_t>(group, 16);
   const uint32_t head_blocks = (group + ng - 1) / ng;
@@ -1068,7 +1311,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
         max_pages = std::max<uint32_t>(max_pages, (uint32_t)(last / 16 - lo / 16 + 1));
         PrefillItem it{(uint32_t)sg.seq, 0, (uint32_t)(sg.start + u), (uint32_t)pos0, n_tok, 0, 0, 0, {}};
         const uint64_t page0 = lo / 16, n_pages = last / 16 - lo / 16 + 1;
-        const int32_t* row = kv->h_table.data() + sg.seq * kv->bps;
+        const int32_t* row = (y.win ? kv->h_wtable.data() : kv->h_table.data()) + sg.seq * kv->bps;
         for (uint64_t b = 0; b < 8; b++)
           it.blk[b] = (uint32_t)row[((page0 + std::min<uint64_t>(b, n_pages - 1)) << 4) >> kv->bt_shift];
         for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {

@@ -17,6 +17,8 @@ namespace lmh {
 BlockPool& kv_pool(lmh_kv* kv);
 uint64_t kv_n_seqs(const lmh_kv* kv);
 uint64_t kv_max_ctx(const lmh_kv* kv);
+// true when the handle has sliding-window layers (their rows are not kept for prefix reuse)
+bool kv_has_window(const lmh_kv* kv);
 uint64_t kv_seq_len(const lmh_kv* kv, uint64_t seq);
 // true when sequence `seq` holds no blocks and no positions (free for binding)
 bool kv_seq_empty(const lmh_kv* kv, uint64_t seq);

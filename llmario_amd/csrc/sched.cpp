@@ -114,7 +114,10 @@ struct lmh_sched {
     blocks.clear();
     chain.clear();
     cached = 0;
-    for (size_t i = 0; i + bt <= tokens.size(); i += bt) {
+    // a handle with window layers keeps no window rows behind its window, so a cached prefix
+    // cannot be resumed: nothing is reclaimed (and no lookup is counted)
+    const bool reuse = !(kv && kv_has_window(kv));
+    for (size_t i = 0; reuse && i + bt <= tokens.size(); i += bt) {
       const Hash h = block_hash(chain.empty() ? nullptr : &chain.back(), tokens.data() + i, bt, extra);
       uint32_t b;
       if (!p.reclaim(h, b)) {

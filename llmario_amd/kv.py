@@ -36,6 +36,7 @@ class Layer:
     n_kv: int
     hd: int
     hdv: int
+    window: int = 0   # sliding-window width (0: full attention)
 
 
 def _stream_ptr(stream):
@@ -69,14 +70,14 @@ class HipKvCache:
     """The device page pool of one model's attention layers (KvCache on the GPU)."""
 
     def __init__(self, layers, max_ctx: int, n_seqs: int = 1, kv_type: str = "f16",
-                 block_tokens: int = 16, pool_tokens: int = 0, device: int = 0):
+                 block_tokens: int = 16, pool_tokens: int = 0, device: int = 0, n_batch: int = 0):
         self.layers = [l if isinstance(l, Layer) else Layer(*l) for l in layers]
         self.kv_type = kv_type
-        descs = (N.LayerDesc * len(self.layers))(*[N.LayerDesc(l.n_head, l.n_kv, l.hd, l.hdv)
+        descs = (N.LayerDesc * len(self.layers))(*[N.LayerDesc(l.n_head, l.n_kv, l.hd, l.hdv, l.window, 0)
                                                      for l in self.layers])
         self._descs = descs
         o = N.KvOptions(N.ABI_VERSION, N.KV_TYPES[kv_type], block_tokens, len(self.layers),
-                        C.cast(descs, C.POINTER(N.LayerDesc)), max_ctx, n_seqs, pool_tokens, device, 0)
+                        C.cast(descs, C.POINTER(N.LayerDesc)), max_ctx, n_seqs, pool_tokens, device, n_batch)
         h = C.c_void_p()
         rc = N.lib().lmh_kv_create(C.byref(o), C.byref(h))
         if rc != N.OK:
