@@ -1259,13 +1259,38 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
   const int32_t *rs, *rp;
   const uint8_t* ex;
   int slot;
-  if ((rc = kv->stage_rows(freq.data(), freq.size() * 4, nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
+  // rows of f16 / bf16 segments in aligned runs of 4 positions go to the 4-token kernel (whole
+  // 8-byte V runs); the others (decode rows, segment edges) to the per-row kernel
+  std::vector<int32_t> lists;  // [quads..., rest...]
+  uint32_t n_quads = 0;
+  if (kv->kv_type == LMH_KV_F16 || kv->kv_type == LMH_KV_BF16) {
+    std::vector<int32_t> rest;
+    for (uint64_t i = 0; i < n_segs; i++) {
+      const lmh_seg& sg = segs[i];
+      for (uint64_t j = 0; j < sg.n;) {
+        if (((sg.pos0 + j) & 3) == 0 && j + 4 <= sg.n) {
+          lists.push_back((int32_t)(sg.start + j));
+          j += 4;
+        } else {
+          rest.push_back((int32_t)(sg.start + j));
+          j++;
+        }
+      }
+    }
+    n_quads = (uint32_t)lists.size();
+    lists.insert(lists.end(), rest.begin(), rest.end());
+  }
+  const size_t freq_bytes = freq.size() * 4;
+  if ((rc = kv->stage_rows(freq.data(), freq_bytes, lists.data(), lists.size() * 4, rs, rp, ex, slot)) != LMH_OK)
+    return rc;
+  const int32_t* d_lists = (const int32_t*)(ex + (freq_bytes + 255) / 256 * 256);
   RopeGeom r{y.n_head, q_stride, p->flags, half_rot, p->eps, p->freq_scale, p->attn_factor,
              (p->flags & LMH_ROPE_Q_NORM) ? p->q_norm : nullptr, (p->flags & LMH_ROPE_K_NORM) ? p->k_norm : nullptr,
              apply ? p->freq_div : nullptr, (const float*)ex};
   hipError_t e;
   if ((e = kv->time_begin(st, LMH_KERNEL_ROPE_STORE)) != hipSuccess) return kv->hip_fail(e, "event");
-  e = launch_qk_rope_store(kv->geom(layer), r, rs, rp, (uint32_t)n_rows, q_in, k_in, v_in, q_out, st);
+  e = launch_qk_rope_store(kv->geom(layer), r, rs, rp, (uint32_t)n_rows, q_in, k_in, v_in, q_out, d_lists, n_quads,
+                           d_lists + n_quads, (uint32_t)(lists.size() - n_quads), st);
   if (e != hipSuccess) return kv->hip_fail(e, "kernel launch");
   if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   return kv->release_rows(slot, st);

@@ -310,14 +310,15 @@ __global__ __launch_bounds__(256) void qk_rope_store_kernel(PageGeom g, RopeGeom
 // computed once per row in f32 (sincosf, correctly range-reduced; within an ulp of the
 // reference's sinf/cosf) and read by each lane once.
 template <int VPL>
-__global__ __launch_bounds__(256) void qk_rope_store_reg_kernel(PageGeom g, RopeGeom r, const int32_t* row_seq,
-                                                                const int32_t* row_pos, const float* q, const float* k,
-                                                                const float* v, float* q_out) {
+__global__ __launch_bounds__(256) void qk_rope_store_reg_kernel(PageGeom g, RopeGeom r, const int32_t* rows,
+                                                                const int32_t* row_seq, const int32_t* row_pos,
+                                                                const float* q, const float* k, const float* v,
+                                                                float* q_out) {
   constexpr uint32_t HD = 64 * VPL;
   constexpr int GRP = 16;  // heads a wave requests before processing them
   typedef float fv __attribute__((ext_vector_type(VPL)));
   __shared__ float2 cs[ROPE_MAX_DIM / 2];
-  const uint32_t row = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+  const uint32_t row = rows ? (uint32_t)rows[blockIdx.x] : blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
   const uint32_t pos = (uint32_t)row_pos[row];
   const uint32_t n_items = r.n_head + 2 * g.n_kv;
   auto src_of = [&](uint32_t it) -> const float* {
@@ -545,6 +546,142 @@ __global__ void snapshot_read_kernel(PageGeom g, uint32_t seq, uint32_t bt, uint
 // scales) and the tile's 16 row segments (head h of rows t*16 .. t*16+15, h*seg bytes into each
 // row) are staged in LDS; bytes are remapped between the two layouts there, so HBM sees 16-byte
 // accesses on the page side and 4-byte accesses running along each row segment.
+
+// Four consecutive tokens of one sequence, aligned to 4 positions (so they share a 16-token tile
+// and, in the V tile, one 8-byte run per dimension: v16_off interleaves 4 keys), per workgroup:
+// the f16 / bf16 rows of a prefill chunk. Each wave takes whole heads for all four tokens; K goes
+// out as in the row kernel (per token), V as one 8-byte store per dimension carrying the four
+// tokens' values, where the row kernel writes 2-byte pieces.
+template <int VPL>
+__global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, RopeGeom r, const int32_t* quads,
+                                                                 const int32_t* row_seq, const int32_t* row_pos,
+                                                                 const float* q, const float* k, const float* v,
+                                                                 float* q_out) {
+  constexpr uint32_t HD = 64 * VPL;
+  constexpr int GRP = 2;  // heads (x 4 tokens) a wave requests before processing them (more heads
+                          // cost occupancy: 2 keeps the kernel at 4 waves per SIMD)
+  typedef float fv __attribute__((ext_vector_type(VPL)));
+  __shared__ float2 cs[4][ROPE_MAX_DIM / 2];
+  const uint32_t row0 = (uint32_t)quads[blockIdx.x], tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+  const uint32_t pos0 = (uint32_t)row_pos[row0];
+  const uint32_t n_items = r.n_head + 2 * g.n_kv;
+  auto src_of = [&](uint32_t it, uint32_t t) -> const float* {
+    const size_t row = row0 + t;
+    if (it < r.n_head) return q + (row * r.n_head + it) * r.q_stride;
+    if (it < r.n_head + g.n_kv) return k + (row * g.n_kv + it - r.n_head) * HD;
+    return v + (row * g.n_kv + it - r.n_head - g.n_kv) * HD;
+  };
+  fv xs[GRP][4];
+#pragma unroll
+  for (int j = 0; j < GRP; j++) {
+    const uint32_t it = w + 4 * j;
+#pragma unroll
+    for (int t = 0; t < 4; t++) xs[j][t] = it < n_items ? *(const fv*)(src_of(it, t) + lane * VPL) : fv{};
+  }
+  const uint32_t half = r.half_rot;
+  for (uint32_t i = tid; i < 4 * half; i += blockDim.x) {
+    const uint32_t t = i / half, ii = i - t * half;
+    float angle = (float)(pos0 + t) * r.freq_scale * r.freq[ii];
+    if (r.freq_div) angle = angle / r.freq_div[ii];
+    float sn, cn;
+    sincosf(angle, &sn, &cn);
+    cs[t][ii] = make_float2(cn * r.attn_factor, sn * r.attn_factor);
+  }
+  const Slot sl0 = locate(g, row_seq[row0], pos0);
+  fv wq, wk;
+#pragma unroll
+  for (int c = 0; c < VPL; c++) {
+    wq[c] = r.q_norm ? r.q_norm[lane * VPL + c] : 1.0f;
+    wk[c] = r.k_norm ? r.k_norm[lane * VPL + c] : 1.0f;
+  }
+  __syncthreads();
+  const bool neox = (r.flags & ROPE_NEOX) != 0;
+  const uint32_t pmask = neox ? half / VPL : 1;
+  float2 cf[4][VPL];
+  bool first[VPL], rot[VPL];
+#pragma unroll
+  for (int c = 0; c < VPL; c++) {
+    const uint32_t e = lane * VPL + c;
+    rot[c] = e < 2 * half;
+    first[c] = neox ? e < half : (e & 1) == 0;
+    const uint32_t i = neox ? (e < half ? e : e - half) : e >> 1;
+#pragma unroll
+    for (int t = 0; t < 4; t++) cf[t][c] = rot[c] ? cs[t][i] : make_float2(1.f, 0.f);
+  }
+  const Side sv = side(g, true);
+  for (uint32_t g0 = 0; g0 * 4 < n_items; g0 += GRP) {
+    if (g0 > 0) {
+#pragma unroll
+      for (int j = 0; j < GRP; j++) {
+        const uint32_t it = w + 4 * (g0 + j);
+#pragma unroll
+        for (int t = 0; t < 4; t++) xs[j][t] = it < n_items ? *(const fv*)(src_of(it, t) + lane * VPL) : fv{};
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < GRP; j++) {
+      const uint32_t it = w + 4 * (g0 + j);
+      if (it >= n_items) continue;
+      const bool is_q = it < r.n_head, is_v = it >= r.n_head + g.n_kv;
+      const bool norm = is_q ? (r.flags & ROPE_Q_NORM) != 0
+                             : is_v ? (r.flags & ROPE_V_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0;
+      fv x[4];
+#pragma unroll
+      for (int t = 0; t < 4; t++) {
+        x[t] = xs[j][t];
+        if (norm) {
+          float ss = 0.f;
+#pragma unroll
+          for (int c = 0; c < VPL; c++) ss += x[t][c] * x[t][c];
+          const float scale = 1.0f / sqrtf(wave_sum(ss) / (float)HD + r.eps);
+          const fv nw = is_q ? wq : wk;
+#pragma unroll
+          for (int c = 0; c < VPL; c++) x[t][c] = is_v ? x[t][c] * scale : x[t][c] * scale * nw[c];
+        }
+        if (!is_v && half) {
+          fv p;
+#pragma unroll
+          for (int c = 0; c < VPL; c++) {
+            if (neox || VPL == 1)
+              p[c] = __shfl_xor(x[t][c], (int)pmask);
+            else
+              p[c] = x[t][c ^ 1];
+          }
+#pragma unroll
+          for (int c = 0; c < VPL; c++) {
+            if (!rot[c]) continue;
+            x[t][c] = first[c] ? x[t][c] * cf[t][c].x - p[c] * cf[t][c].y : p[c] * cf[t][c].y + x[t][c] * cf[t][c].x;
+          }
+        }
+      }
+      if (is_q) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) *(fv*)(q_out + ((size_t)(row0 + t) * r.n_head + it) * HD + lane * VPL) = x[t];
+      } else if (!is_v) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+          Slot sl = sl0;
+          sl.m += t;
+          float xa[VPL];
+#pragma unroll
+          for (int c = 0; c < VPL; c++) xa[c] = x[t][c];
+          store_head_lanes<VPL>(g, sl, false, it - r.n_head, xa, lane);
+        }
+      } else {
+        uint8_t* head = sl0.base + sv.off + (it - r.n_head - g.n_kv) * sv.head + sl0.tile * sv.tile;
+        const bool f16 = g.kv_type == KV_F16;
+#pragma unroll
+        for (int c = 0; c < VPL; c++) {
+          uint32_t b[4];
+#pragma unroll
+          for (int t = 0; t < 4; t++) b[t] = f16 ? f16_bits(x[t][c]) : bf16_bits(x[t][c]);
+          *(uint2*)(head + v16_off(sl0.m, lane * VPL + c)) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+        }
+      }
+    }
+  }
+}
+
 struct SnapGeom {
   uint32_t seq, bt, k_row, v_row;
   uint64_t bb, ref_off;
@@ -662,6 +799,7 @@ hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, cons
 
 hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int32_t* row_seq, const int32_t* row_pos,
                                 uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
+                                const int32_t* quads, uint32_t n_quads, const int32_t* rest, uint32_t n_rest,
                                 hipStream_t s) {
   if (n_rows == 0) return hipSuccess;
   // register path: hd == hdv = 64*VPL; Normal pairs are always in-lane (VPL >= 2) or one lane
@@ -671,11 +809,24 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
   const bool pairs_ok = half == 0 || !neox || (half % vpl == 0 && ((half / vpl) & (half / vpl - 1)) == 0);
   const bool reg = g.hd == g.hdv && g.hd % 64 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) && pairs_ok;
   if (reg) {
+    // aligned quads of consecutive f16 / bf16 rows (when the caller found any), then the other rows
+    if (n_quads > 0 && (g.kv_type == KV_F16 || g.kv_type == KV_BF16)) {
+      switch (vpl) {
+        case 1: hipLaunchKernelGGL(qk_rope_store_quad_kernel<1>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
+        case 2: hipLaunchKernelGGL(qk_rope_store_quad_kernel<2>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
+        case 4: hipLaunchKernelGGL(qk_rope_store_quad_kernel<4>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
+        default: hipLaunchKernelGGL(qk_rope_store_quad_kernel<8>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
+      }
+    } else {
+      rest = nullptr;
+      n_rest = n_rows;
+    }
+    if (n_rest == 0) return hipGetLastError();
     switch (vpl) {
-      case 1: hipLaunchKernelGGL(qk_rope_store_reg_kernel<1>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      case 2: hipLaunchKernelGGL(qk_rope_store_reg_kernel<2>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      case 4: hipLaunchKernelGGL(qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      default: hipLaunchKernelGGL(qk_rope_store_reg_kernel<8>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 1: hipLaunchKernelGGL(qk_rope_store_reg_kernel<1>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
+      case 2: hipLaunchKernelGGL(qk_rope_store_reg_kernel<2>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
+      case 4: hipLaunchKernelGGL(qk_rope_store_reg_kernel<4>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
+      default: hipLaunchKernelGGL(qk_rope_store_reg_kernel<8>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
     }
   } else {
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
