@@ -753,6 +753,109 @@ __global__ __launch_bounds__(256) void snapshot_tiles_kernel(PageGeom g, SnapGeo
   }
 }
 
+
+// One workgroup per (block, 16-token tile, side) covering every KV head: the page side of that
+// unit (each head's codes, then each head's q8_0 scales) and its reference side (16 rows of
+// n_kv * seg bytes, one contiguous run) are both staged whole, so HBM sees only 16-byte
+// accesses; the byte permutation between them runs in LDS with the geometry known at compile
+// time. WRITE: page -> rows (gathered from the staged page bytes); read: rows -> page (scattered
+// into a staged page image, then copied out).
+template <bool WRITE, int TYPE, int DIM, bool IS_V>
+__device__ inline void snapshot_side(const PageGeom& g, const SnapGeom& sg, uint8_t* snap, uint8_t* smem) {
+  constexpr uint32_t TB = TYPE == KV_Q8 ? 16 * DIM : TYPE == KV_F32 ? 64 * DIM : 32 * DIM;  // a tile's codes
+  constexpr uint32_t TS = TYPE == KV_Q8 ? 16 * (DIM / 32) * 2 : 0;                         // its q8_0 scales
+  constexpr uint32_t SEG = TYPE == KV_Q8 ? DIM / 32 * 34 : TYPE == KV_F32 ? 4 * DIM : 2 * DIM;  // a head's row bytes
+  constexpr uint32_t PH = TB + TS;  // staged page bytes per head
+  const uint32_t tid = threadIdx.x;
+  constexpr bool is_v = IS_V;
+  const uint32_t id = blockIdx.x >> 1, tpb = sg.bt >> 4, t = id % tpb, bi = id / tpb;
+  const Side sd = side(g, is_v);
+  const uint32_t nkv = g.n_kv, row = nkv * SEG, span = 16 * row;
+  const int blk = g.table[(size_t)sg.seq * g.bps + bi];
+  uint8_t* head0 = g.pool + (size_t)blk * g.block_bytes + sd.off;
+  uint8_t* rows = snap + (size_t)bi * sg.bb + sg.ref_off + (is_v ? (size_t)sg.bt * sg.k_row : 0) + (size_t)(t * 16) * row;
+  uint8_t* pg_l = smem;                                  // [nkv][PH] page image
+  uint8_t* rw_l = smem + ((nkv * PH + 15) & ~15u);       // [16 rows][row] (read direction)
+  // page byte of (token m, byte u of a head's row segment), relative to the head's staged bytes
+  auto page_byte = [&](uint32_t m, uint32_t u) -> uint32_t {
+    if constexpr (TYPE == KV_Q8) {
+      const uint32_t b = u / 34u, r = u % 34u;
+      if (r < 2) return TB + (m * (DIM / 32) + b) * 2u + r;
+      return elem_off(KV_Q8, is_v, m, 32u * b + r - 2u, DIM);
+    } else if constexpr (TYPE == KV_F32) {
+      return elem_off(KV_F32, is_v, m, u >> 2, DIM) + (u & 3u);
+    } else {
+      return elem_off(TYPE, is_v, m, u >> 1, DIM) + (u & 1u);
+    }
+  };
+  if (WRITE) {
+    for (uint32_t h = 0; h < nkv; h++) {
+      const uint8_t* src = head0 + (size_t)h * sd.head;
+      for (uint32_t o = tid * 16; o < TB; o += 256 * 16) *(uint4*)(pg_l + h * PH + o) = *(const uint4*)(src + t * TB + o);
+      if constexpr (TS > 0)
+        for (uint32_t o = tid * 4; o < TS; o += 256 * 4)
+          *(uint32_t*)(pg_l + h * PH + TB + o) = *(const uint32_t*)(src + sd.scale + t * TS + o);
+    }
+    __syncthreads();
+    for (uint32_t c = tid; c < span / 16; c += 256) {
+      const uint32_t x0 = c * 16;
+      uint32_t m = x0 / row, rem = x0 - m * row, h = rem / SEG, u = rem - h * SEG;
+      uint32_t w4[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        uint32_t acc = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+          acc |= (uint32_t)pg_l[h * PH + page_byte(m, u)] << (8 * j);
+          if (++u == SEG) {
+            u = 0;
+            if (++h == nkv) {
+              h = 0;
+              m++;
+            }
+          }
+        }
+        w4[k] = acc;
+      }
+      *(uint4*)(rows + x0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    }
+  } else {
+    for (uint32_t o = tid * 16; o < span; o += 256 * 16) *(uint4*)(rw_l + o) = *(const uint4*)(rows + o);
+    __syncthreads();
+    for (uint32_t c = tid; c < span / 16; c += 256) {
+      const uint32_t x0 = c * 16;
+      uint32_t m = x0 / row, rem = x0 - m * row, h = rem / SEG, u = rem - h * SEG;
+#pragma unroll
+      for (int j = 0; j < 16; j++) {
+        pg_l[h * PH + page_byte(m, u)] = rw_l[x0 + j];
+        if (++u == SEG) {
+          u = 0;
+          if (++h == nkv) {
+            h = 0;
+            m++;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    for (uint32_t h = 0; h < nkv; h++) {
+      uint8_t* dst = head0 + (size_t)h * sd.head;
+      for (uint32_t o = tid * 16; o < TB; o += 256 * 16) *(uint4*)(dst + t * TB + o) = *(const uint4*)(pg_l + h * PH + o);
+      if constexpr (TS > 0)
+        for (uint32_t o = tid * 4; o < TS; o += 256 * 4)
+          *(uint32_t*)(dst + sd.scale + t * TS + o) = *(const uint32_t*)(pg_l + h * PH + TB + o);
+    }
+  }
+}
+template <bool WRITE, int TYPE, int DIM>
+__global__ __launch_bounds__(256) void snapshot_side_kernel(PageGeom g, SnapGeom sg, uint8_t* snap) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  if (blockIdx.x & 1u)
+    snapshot_side<WRITE, TYPE, DIM, true>(g, sg, snap, smem);
+  else
+    snapshot_side<WRITE, TYPE, DIM, false>(g, sg, snap, smem);
+}
+
 // Zero whole blocks (a newly backed block reads as zeros, like the reference's anonymous
 // mappings, kv.rs:29-37). block_bytes is a multiple of 16.
 __global__ void zero_blocks_kernel(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n) {
@@ -838,6 +941,27 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
                            uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s) {
   if (n_pos == 0) return hipSuccess;
   const uint32_t seg_k = k_row / g.n_kv, seg_v = v_row / g.n_kv;
+  if (g.hd == g.hdv && bt % 16 == 0 && (g.kv_type == KV_F16 || g.kv_type == KV_BF16 || g.kv_type == KV_Q8) &&
+      (g.hd == 64 || g.hd == 128 || g.hd == 256)) {
+    const SnapGeom sg{seq, bt, k_row, v_row, bb, ref_off, seg_k, seg_v};
+    const uint32_t ph = g.k_tile + (g.kv_type == KV_Q8 ? g.k_tile_s : 0);
+    const size_t lds = ((g.n_kv * ph + 15) & ~15u) + (write ? 0 : 16 * (size_t)k_row);
+    if (lds <= 64 * 1024) {
+      const uint32_t n_wg = n_pos / 16 * 2;
+#define LMH_SNAP(T, D)                                                                                       \
+  if (g.kv_type == T && g.hd == D) {                                                                          \
+    if (write)                                                                                                \
+      hipLaunchKernelGGL((snapshot_side_kernel<true, T, D>), dim3(n_wg), dim3(256), lds, s, g, sg, bytes);    \
+    else                                                                                                      \
+      hipLaunchKernelGGL((snapshot_side_kernel<false, T, D>), dim3(n_wg), dim3(256), lds, s, g, sg, bytes);   \
+    return hipGetLastError();                                                                                 \
+  }
+      LMH_SNAP(KV_F16, 64) LMH_SNAP(KV_F16, 128) LMH_SNAP(KV_F16, 256)
+      LMH_SNAP(KV_BF16, 64) LMH_SNAP(KV_BF16, 128) LMH_SNAP(KV_BF16, 256)
+      LMH_SNAP(KV_Q8, 64) LMH_SNAP(KV_Q8, 128) LMH_SNAP(KV_Q8, 256)
+#undef LMH_SNAP
+    }
+  }
   if (seg_k % 4 == 0 && seg_v % 4 == 0 && bt % 16 == 0) {
     const SnapGeom sg{seq, bt, k_row, v_row, bb, ref_off, seg_k, seg_v};
     const uint32_t tb = std::max(g.k_tile + (g.kv_type == KV_Q8 ? g.k_tile_s : 0),
