@@ -788,6 +788,99 @@ __device__ inline void snapshot_side(const PageGeom& g, const SnapGeom& sg, uint
       return elem_off(TYPE, is_v, m, u >> 1, DIM) + (u & 1u);
     }
   };
+  if constexpr (TYPE == KV_Q8) {
+    // whole q8_0 row blocks ([f16 scale][32 codes], 34 bytes, 2-byte aligned in the row run):
+    // K codes of a block are 4 runs of 8 bytes in the tile; V codes hold 4 tokens per 4-byte
+    // word (one word per dimension), so V moves in groups of 4 tokens
+    constexpr uint32_t NB = DIM / 32;
+    auto scale_at = [&](uint32_t h, uint32_t m, uint32_t b) { return (uint16_t*)(pg_l + h * PH + TB + (m * NB + b) * 2u); };
+    auto row_at = [&](uint32_t h, uint32_t m, uint32_t b) { return (uint16_t*)(rw_l + m * row + h * SEG + b * 34u); };
+    if (WRITE) {
+      for (uint32_t h = 0; h < nkv; h++) {
+        const uint8_t* src = head0 + (size_t)h * sd.head;
+        for (uint32_t o = tid * 16; o < TB; o += 256 * 16) *(uint4*)(pg_l + h * PH + o) = *(const uint4*)(src + t * TB + o);
+        for (uint32_t o = tid * 4; o < TS; o += 256 * 4)
+          *(uint32_t*)(pg_l + h * PH + TB + o) = *(const uint32_t*)(src + sd.scale + t * TS + o);
+      }
+    } else {
+      for (uint32_t o = tid * 16; o < span; o += 256 * 16) *(uint4*)(rw_l + o) = *(const uint4*)(rows + o);
+    }
+    __syncthreads();
+    if constexpr (!IS_V) {
+      for (uint32_t un = tid; un < 16 * nkv * NB; un += 256) {
+        const uint32_t m = un / (nkv * NB), rem = un - m * (nkv * NB), h = rem / NB, b = rem - h * NB;
+        uint8_t* pb = pg_l + h * PH;
+        uint16_t* rb = row_at(h, m, b);
+        if (WRITE) {
+          uint32_t w[8];
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const uint2 x = *(const uint2*)(pb + kq8_off(m, 32 * b + 8 * r));
+            w[2 * r] = x.x;
+            w[2 * r + 1] = x.y;
+          }
+          rb[0] = *scale_at(h, m, b);
+#pragma unroll
+          for (int j = 0; j < 16; j++) rb[1 + j] = (uint16_t)(w[j >> 1] >> (16 * (j & 1)));
+        } else {
+          uint32_t w[8];
+#pragma unroll
+          for (int j = 0; j < 8; j++) w[j] = (uint32_t)rb[1 + 2 * j] | ((uint32_t)rb[2 + 2 * j] << 16);
+          *scale_at(h, m, b) = rb[0];
+#pragma unroll
+          for (int r = 0; r < 4; r++) *(uint2*)(pb + kq8_off(m, 32 * b + 8 * r)) = make_uint2(w[2 * r], w[2 * r + 1]);
+        }
+      }
+    } else {
+      for (uint32_t un = tid; un < 4 * nkv * NB; un += 256) {
+        const uint32_t qg = un / (nkv * NB), rem = un - qg * (nkv * NB), h = rem / NB, b = rem - h * NB;
+        uint8_t* pb = pg_l + h * PH;
+        uint32_t w[32];  // w[d]: the 4 tokens' codes of dimension 32b + d
+        if (WRITE) {
+#pragma unroll
+          for (int d = 0; d < 32; d++) w[d] = *(const uint32_t*)(pb + vq8_off(4 * qg, 32 * b + d));
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const uint32_t m = 4 * qg + k;
+            uint16_t* rb = row_at(h, m, b);
+            rb[0] = *scale_at(h, m, b);
+#pragma unroll
+            for (int j = 0; j < 16; j++)
+              rb[1 + j] = (uint16_t)(((w[2 * j] >> (8 * k)) & 0xffu) | (((w[2 * j + 1] >> (8 * k)) & 0xffu) << 8));
+          }
+        } else {
+#pragma unroll
+          for (int d = 0; d < 32; d++) w[d] = 0;
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const uint32_t m = 4 * qg + k;
+            const uint16_t* rb = row_at(h, m, b);
+            *scale_at(h, m, b) = rb[0];
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+              const uint32_t v2 = rb[1 + j];
+              w[2 * j] |= (v2 & 0xffu) << (8 * k);
+              w[2 * j + 1] |= (v2 >> 8) << (8 * k);
+            }
+          }
+#pragma unroll
+          for (int d = 0; d < 32; d++) *(uint32_t*)(pb + vq8_off(4 * qg, 32 * b + d)) = w[d];
+        }
+      }
+    }
+    __syncthreads();
+    if (WRITE) {
+      for (uint32_t o = tid * 16; o < span; o += 256 * 16) *(uint4*)(rows + o) = *(const uint4*)(rw_l + o);
+    } else {
+      for (uint32_t h = 0; h < nkv; h++) {
+        uint8_t* dst = head0 + (size_t)h * sd.head;
+        for (uint32_t o = tid * 16; o < TB; o += 256 * 16) *(uint4*)(dst + t * TB + o) = *(const uint4*)(pg_l + h * PH + o);
+        for (uint32_t o = tid * 4; o < TS; o += 256 * 4)
+          *(uint32_t*)(dst + sd.scale + t * TS + o) = *(const uint32_t*)(pg_l + h * PH + TB + o);
+      }
+    }
+    return;
+  }
   if (WRITE) {
     for (uint32_t h = 0; h < nkv; h++) {
       const uint8_t* src = head0 + (size_t)h * sd.head;
@@ -945,7 +1038,7 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
       (g.hd == 64 || g.hd == 128 || g.hd == 256)) {
     const SnapGeom sg{seq, bt, k_row, v_row, bb, ref_off, seg_k, seg_v};
     const uint32_t ph = g.k_tile + (g.kv_type == KV_Q8 ? g.k_tile_s : 0);
-    const size_t lds = ((g.n_kv * ph + 15) & ~15u) + (write ? 0 : 16 * (size_t)k_row);
+    const size_t lds = ((g.n_kv * ph + 15) & ~15u) + (write && g.kv_type != KV_Q8 ? 0 : 16 * (size_t)k_row);
     if (lds <= 64 * 1024) {
       const uint32_t n_wg = n_pos / 16 * 2;
 #define LMH_SNAP(T, D)                                                                                       \
