@@ -261,7 +261,7 @@ def time_sched(steps: int, warmup_s: float):
     out = torch.empty((budget, L.n_head, L.hdv), device="cuda")
     stream = torch.cuda.current_stream()
     scale = L.hd ** -0.5
-    acc = {"host": 0.0, "rows": 0, "decodes": 0, "steps": 0, "fed": 0}
+    acc = {"host": 0.0, "launch": 0.0, "rows": 0, "decodes": 0, "steps": 0, "fed": 0}
 
     def one_step():
         t0 = time.perf_counter()
@@ -282,6 +282,7 @@ def time_sched(steps: int, warmup_s: float):
             feed(4)
         sch.drain_queue()
         acc["host"] += (t1 - t0) + (time.perf_counter() - t2)
+        acc["launch"] += t2 - t1
         acc["rows"] += n
         acc["decodes"] += len(st.decodes)
         acc["steps"] += 1
@@ -294,7 +295,7 @@ def time_sched(steps: int, warmup_s: float):
             torch.cuda.synchronize()
     torch.cuda.synchronize()
     log(f"[bench] sched_c5: {acc['steps']} warm-up steps in {time.perf_counter() - t_w:.2f}s")
-    acc.update(host=0.0, rows=0, decodes=0, steps=0)
+    acc.update(host=0.0, launch=0.0, rows=0, decodes=0, steps=0)
     assert all(sch.slot(i) is not None for i in long_ids), "a long decode request was retracted"
     t0 = time.perf_counter()
     for _ in range(steps):
@@ -302,10 +303,12 @@ def time_sched(steps: int, warmup_s: float):
     torch.cuda.synchronize()
     el = time.perf_counter() - t0
     res = {"config": "sched_c5", "steps": steps, "ms_per_step": el * 1e3 / steps,
-           "host_us_per_step": acc["host"] * 1e6 / steps, "rows_per_step": acc["rows"] / steps,
+           "host_us_per_step": acc["host"] * 1e6 / steps, "launch_us_per_step": acc["launch"] * 1e6 / steps,
+           "rows_per_step": acc["rows"] / steps,
            "decode_rows_per_step": acc["decodes"] / steps, "rows_per_s": acc["rows"] / el,
            "pool": sch.pool_stats()}
     log(f"[bench] sched_c5: {res['ms_per_step'] * 1e3:.1f} us/step, scheduler host {res['host_us_per_step']:.1f} us/step, "
+        f"producer + attend calls {res['launch_us_per_step']:.1f} us/step, "
         f"{res['rows_per_step']:.0f} rows/step ({res['decode_rows_per_step']:.1f} decode), {res['rows_per_s']:.0f} rows/s")
     del sch, hc
     torch.cuda.empty_cache()

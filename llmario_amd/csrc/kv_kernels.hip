@@ -310,15 +310,14 @@ __global__ __launch_bounds__(256) void qk_rope_store_kernel(PageGeom g, RopeGeom
 // computed once per row in f32 (sincosf, correctly range-reduced; within an ulp of the
 // reference's sinf/cosf) and read by each lane once.
 template <int VPL>
-__global__ __launch_bounds__(256) void qk_rope_store_reg_kernel(PageGeom g, RopeGeom r, const int32_t* rows,
-                                                                const int32_t* row_seq, const int32_t* row_pos,
-                                                                const float* q, const float* k, const float* v,
-                                                                float* q_out) {
+__global__ __launch_bounds__(256) void qk_rope_store_reg_kernel(PageGeom g, RopeGeom r, const int32_t* row_seq,
+                                                                const int32_t* row_pos, const float* q, const float* k,
+                                                                const float* v, float* q_out) {
   constexpr uint32_t HD = 64 * VPL;
   constexpr int GRP = 16;  // heads a wave requests before processing them
   typedef float fv __attribute__((ext_vector_type(VPL)));
   __shared__ float2 cs[ROPE_MAX_DIM / 2];
-  const uint32_t row = rows ? (uint32_t)rows[blockIdx.x] : blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+  const uint32_t row = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
   const uint32_t pos = (uint32_t)row_pos[row];
   const uint32_t n_items = r.n_head + 2 * g.n_kv;
   auto src_of = [&](uint32_t it) -> const float* {
@@ -551,35 +550,34 @@ __global__ void snapshot_read_kernel(PageGeom g, uint32_t seq, uint32_t bt, uint
 // and, in the V tile, one 8-byte run per dimension: v16_off interleaves 4 keys), per workgroup:
 // the f16 / bf16 rows of a prefill chunk. Each wave takes whole heads for all four tokens; K goes
 // out as in the row kernel (per token), V as one 8-byte store per dimension carrying the four
-// tokens' values, where the row kernel writes 2-byte pieces.
-template <int VPL>
-__global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, RopeGeom r, const int32_t* quads,
-                                                                 const int32_t* row_seq, const int32_t* row_pos,
-                                                                 const float* q, const float* k, const float* v,
-                                                                 float* q_out) {
+// tokens' values, where the row kernel writes 2-byte pieces. NT = 1 is the same work for one row
+// (a decode row or a chunk's unaligned edge), V written per element as in the row kernel.
+// Items it0 .. n_items-1 of [Q heads][K heads][V heads] are the workgroup's share.
+template <int VPL, int NT>
+__device__ void rope_tokens(const PageGeom& g, const RopeGeom& r, float2 (*cs)[ROPE_MAX_DIM / 2], uint32_t row0,
+                            uint32_t it0, uint32_t n_items, const int32_t* row_seq, const int32_t* row_pos,
+                            const float* q, const float* k, const float* v, float* q_out) {
   constexpr uint32_t HD = 64 * VPL;
   constexpr int GRP = 2;  // heads (x 4 tokens) a wave requests before processing them (more heads
                           // cost occupancy: 2 keeps the kernel at 4 waves per SIMD)
   typedef float fv __attribute__((ext_vector_type(VPL)));
-  __shared__ float2 cs[4][ROPE_MAX_DIM / 2];
-  const uint32_t row0 = (uint32_t)quads[blockIdx.x], tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
+  const uint32_t tid = threadIdx.x, w = tid >> 6, lane = tid & 63u;
   const uint32_t pos0 = (uint32_t)row_pos[row0];
-  const uint32_t n_items = r.n_head + 2 * g.n_kv;
   auto src_of = [&](uint32_t it, uint32_t t) -> const float* {
     const size_t row = row0 + t;
     if (it < r.n_head) return q + (row * r.n_head + it) * r.q_stride;
     if (it < r.n_head + g.n_kv) return k + (row * g.n_kv + it - r.n_head) * HD;
     return v + (row * g.n_kv + it - r.n_head - g.n_kv) * HD;
   };
-  fv xs[GRP][4];
+  fv xs[GRP][NT];
 #pragma unroll
   for (int j = 0; j < GRP; j++) {
-    const uint32_t it = w + 4 * j;
+    const uint32_t it = it0 + w + 4 * j;
 #pragma unroll
-    for (int t = 0; t < 4; t++) xs[j][t] = it < n_items ? *(const fv*)(src_of(it, t) + lane * VPL) : fv{};
+    for (int t = 0; t < NT; t++) xs[j][t] = it < n_items ? *(const fv*)(src_of(it, t) + lane * VPL) : fv{};
   }
   const uint32_t half = r.half_rot;
-  for (uint32_t i = tid; i < 4 * half; i += blockDim.x) {
+  for (uint32_t i = tid; i < NT * half; i += blockDim.x) {
     const uint32_t t = i / half, ii = i - t * half;
     float angle = (float)(pos0 + t) * r.freq_scale * r.freq[ii];
     if (r.freq_div) angle = angle / r.freq_div[ii];
@@ -597,7 +595,7 @@ __global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, Rop
   __syncthreads();
   const bool neox = (r.flags & ROPE_NEOX) != 0;
   const uint32_t pmask = neox ? half / VPL : 1;
-  float2 cf[4][VPL];
+  float2 cf[NT][VPL];
   bool first[VPL], rot[VPL];
 #pragma unroll
   for (int c = 0; c < VPL; c++) {
@@ -606,28 +604,28 @@ __global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, Rop
     first[c] = neox ? e < half : (e & 1) == 0;
     const uint32_t i = neox ? (e < half ? e : e - half) : e >> 1;
 #pragma unroll
-    for (int t = 0; t < 4; t++) cf[t][c] = rot[c] ? cs[t][i] : make_float2(1.f, 0.f);
+    for (int t = 0; t < NT; t++) cf[t][c] = rot[c] ? cs[t][i] : make_float2(1.f, 0.f);
   }
   const Side sv = side(g, true);
-  for (uint32_t g0 = 0; g0 * 4 < n_items; g0 += GRP) {
+  for (uint32_t g0 = 0; it0 + g0 * 4 < n_items; g0 += GRP) {
     if (g0 > 0) {
 #pragma unroll
       for (int j = 0; j < GRP; j++) {
-        const uint32_t it = w + 4 * (g0 + j);
+        const uint32_t it = it0 + w + 4 * (g0 + j);
 #pragma unroll
-        for (int t = 0; t < 4; t++) xs[j][t] = it < n_items ? *(const fv*)(src_of(it, t) + lane * VPL) : fv{};
+        for (int t = 0; t < NT; t++) xs[j][t] = it < n_items ? *(const fv*)(src_of(it, t) + lane * VPL) : fv{};
       }
     }
 #pragma unroll
     for (int j = 0; j < GRP; j++) {
-      const uint32_t it = w + 4 * (g0 + j);
+      const uint32_t it = it0 + w + 4 * (g0 + j);
       if (it >= n_items) continue;
       const bool is_q = it < r.n_head, is_v = it >= r.n_head + g.n_kv;
       const bool norm = is_q ? (r.flags & ROPE_Q_NORM) != 0
                              : is_v ? (r.flags & ROPE_V_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0;
-      fv x[4];
+      fv x[NT];
 #pragma unroll
-      for (int t = 0; t < 4; t++) {
+      for (int t = 0; t < NT; t++) {
         x[t] = xs[j][t];
         if (norm) {
           float ss = 0.f;
@@ -656,16 +654,16 @@ __global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, Rop
       }
       if (is_q) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) *(fv*)(q_out + ((size_t)(row0 + t) * r.n_head + it) * HD + lane * VPL) = x[t];
-      } else if (!is_v) {
+        for (int t = 0; t < NT; t++) *(fv*)(q_out + ((size_t)(row0 + t) * r.n_head + it) * HD + lane * VPL) = x[t];
+      } else if (!is_v || NT == 1) {
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
+        for (int t = 0; t < NT; t++) {
           Slot sl = sl0;
           sl.m += t;
           float xa[VPL];
 #pragma unroll
           for (int c = 0; c < VPL; c++) xa[c] = x[t][c];
-          store_head_lanes<VPL>(g, sl, false, it - r.n_head, xa, lane);
+          store_head_lanes<VPL>(g, sl, is_v, is_v ? it - r.n_head - g.n_kv : it - r.n_head, xa, lane);
         }
       } else {
         uint8_t* head = sl0.base + sv.off + (it - r.n_head - g.n_kv) * sv.head + sl0.tile * sv.tile;
@@ -680,6 +678,26 @@ __global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, Rop
       }
     }
   }
+}
+
+// Workgroups x < n_quads take an aligned run of 4 f16 / bf16 tokens each (quads[x] = its first
+// row), the others one of the remaining rows (rest[x - n_quads], or row x - n_quads without a
+// list), in one launch. blockIdx.y picks the workgroup's share of the heads, items y*ipw .. y*ipw+ipw-1, so a
+// short call still spreads over the chip instead of leaving each workgroup a long chain of round
+// trips.
+template <int VPL>
+__global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, RopeGeom r, const int32_t* quads,
+                                                                 uint32_t n_quads, const int32_t* rest,
+                                                                 const int32_t* row_seq, const int32_t* row_pos,
+                                                                 const float* q, const float* k, const float* v,
+                                                                 float* q_out, uint32_t ipw) {
+  __shared__ float2 cs[4][ROPE_MAX_DIM / 2];
+  const uint32_t it0 = blockIdx.y * ipw, n_items = min(r.n_head + 2 * g.n_kv, it0 + ipw);
+  if (blockIdx.x < n_quads)
+    rope_tokens<VPL, 4>(g, r, cs, (uint32_t)quads[blockIdx.x], it0, n_items, row_seq, row_pos, q, k, v, q_out);
+  else
+    rope_tokens<VPL, 1>(g, r, cs, rest ? (uint32_t)rest[blockIdx.x - n_quads] : blockIdx.x - n_quads, it0, n_items,
+                        row_seq, row_pos, q, k, v, q_out);
 }
 
 struct SnapGeom {
@@ -1005,24 +1023,40 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
   const bool pairs_ok = half == 0 || !neox || (half % vpl == 0 && ((half / vpl) & (half / vpl - 1)) == 0);
   const bool reg = g.hd == g.hdv && g.hd % 64 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) && pairs_ok;
   if (reg) {
-    // aligned quads of consecutive f16 / bf16 rows (when the caller found any), then the other rows
-    if (n_quads > 0 && (g.kv_type == KV_F16 || g.kv_type == KV_BF16)) {
-      switch (vpl) {
-        case 1: hipLaunchKernelGGL(qk_rope_store_quad_kernel<1>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
-        case 2: hipLaunchKernelGGL(qk_rope_store_quad_kernel<2>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
-        case 4: hipLaunchKernelGGL(qk_rope_store_quad_kernel<4>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
-        default: hipLaunchKernelGGL(qk_rope_store_quad_kernel<8>, dim3(n_quads), dim3(256), 0, s, g, r, quads, row_seq, row_pos, q, k, v, q_out); break;
-      }
-    } else {
+    // aligned runs of 4 f16 / bf16 rows (when the caller found any) with the other rows, or a
+    // short call of any type (decode rows), go to the split kernel: one launch, each row's heads
+    // split over workgroups (8 items = one round of 2 heads per wave at the least) until the grid
+    // holds about 1024 workgroups, the 4 per CU its registers allow (measured on 256 .. 8192 rows:
+    // a target of 512 or 2048 is slower at 2048 and 4096 rows). Long calls without runs go to the
+    // row kernel, which keeps 16 heads per wave in flight.
+    const bool quad_ok = n_quads > 0 && (g.kv_type == KV_F16 || g.kv_type == KV_BF16);
+    if (!quad_ok) {
+      n_quads = 0;
       rest = nullptr;
       n_rest = n_rows;
     }
-    if (n_rest == 0) return hipGetLastError();
+    if (quad_ok || n_rows < 1024) {
+      const uint32_t n_wg = n_quads + n_rest, n_items = r.n_head + 2 * g.n_kv, max_split = (n_items + 7) / 8;
+      const uint32_t split = std::min(max_split, std::max(1u, (1024u + n_wg - 1) / n_wg));
+      const uint32_t ipw = ((n_items + split - 1) / split + 3) & ~3u;
+      const dim3 grid(n_wg, (n_items + ipw - 1) / ipw);
+#define LMH_QUAD(V)                                                                                            \
+  hipLaunchKernelGGL(qk_rope_store_quad_kernel<V>, grid, dim3(256), 0, s, g, r, quads, n_quads, rest, row_seq, \
+                     row_pos, q, k, v, q_out, ipw)
+      switch (vpl) {
+        case 1: LMH_QUAD(1); break;
+        case 2: LMH_QUAD(2); break;
+        case 4: LMH_QUAD(4); break;
+        default: LMH_QUAD(8); break;
+      }
+#undef LMH_QUAD
+      return hipGetLastError();
+    }
     switch (vpl) {
-      case 1: hipLaunchKernelGGL(qk_rope_store_reg_kernel<1>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
-      case 2: hipLaunchKernelGGL(qk_rope_store_reg_kernel<2>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
-      case 4: hipLaunchKernelGGL(qk_rope_store_reg_kernel<4>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
-      default: hipLaunchKernelGGL(qk_rope_store_reg_kernel<8>, dim3(n_rest), dim3(256), 0, s, g, r, rest, row_seq, row_pos, q, k, v, q_out); break;
+      case 1: hipLaunchKernelGGL(qk_rope_store_reg_kernel<1>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 2: hipLaunchKernelGGL(qk_rope_store_reg_kernel<2>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 4: hipLaunchKernelGGL(qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      default: hipLaunchKernelGGL(qk_rope_store_reg_kernel<8>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
     }
   } else {
     hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
