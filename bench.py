@@ -92,14 +92,16 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
     ms_step, _ = timed(False)
     ms_step_ev, kt = timed(timing_kernel)
     per_kind = {k: (ms / n if n else 0.0) for k, (ms, n) in kt.items()}
-    # the dominant kernel: prefill when the step has multi-token segments, else decode
-    main = "prefill" if per_kind["prefill"] > 0 else "decode"
+    # the dominant kernel: the one launch of a mixed step (prefill units and decode rows), else
+    # prefill when the step has multi-token segments, else decode
+    main = "mixed" if per_kind["mixed"] > 0 else "prefill" if per_kind["prefill"] > 0 else "decode"
     k_avg = per_kind[main]
     res = {
         "config": name, "kv_type": w.kv_type, "rows": w.n_rows, "ms_per_step": ms_step,
         "ms_per_step_with_kernel_events": ms_step_ev,
         "kernel": main, "kernel_ms": k_avg, "decode_ms": per_kind["decode"], "prefill_ms": per_kind["prefill"],
-        "merge_ms": per_kind["merge"], "bytes": w.algorithmic_bytes(), "flops": w.flops(),
+        "mixed_ms": per_kind["mixed"], "merge_ms": per_kind["merge"], "bytes": w.algorithmic_bytes(),
+        "flops": w.flops(),
     }
     res["GBps"] = res["bytes"] / (ms_step * 1e-3) / 1e9
     res["TFLOPs"] = res["flops"] / (ms_step * 1e-3) / 1e12
@@ -367,8 +369,8 @@ def time_window(steps: int, warmup_s: float):
         hc.set_timing(False)
         if events:
             kt = hc.kernel_times()
-            res["prefill_ms"] = kt["prefill"][0] / max(kt["prefill"][1], 1)
-            res["decode_ms"] = kt["decode"][0] / max(kt["decode"][1], 1)
+            for k in ("mixed", "prefill", "decode", "merge"):
+                res[f"{k}_ms"] = kt[k][0] / max(kt[k][1], 1)
         else:
             res["ms_per_step"] = el * 1e3 / steps
     import ctypes as C
@@ -379,8 +381,9 @@ def time_window(steps: int, warmup_s: float):
     res.update(window_blocks_live=live, window_pool_blocks=wi.pool_blocks, paged_blocks_same_contexts=paged_equiv,
                window_pool_bytes=wi.pool_blocks * wi.block_bytes, paged_bytes_same_contexts=paged_equiv * wi.block_bytes)
     res["GBps"] = res["bytes"] / (res["ms_per_step"] * 1e-3) / 1e9
-    log(f"[bench] window_c5w: {res['ms_per_step'] * 1e3:.1f} us/step (prefill {res['prefill_ms'] * 1e3:.1f} us, decode "
-        f"{res['decode_ms'] * 1e3:.1f} us); window blocks live {live} of {wi.pool_blocks}, paged equivalent {paged_equiv}")
+    log(f"[bench] window_c5w: {res['ms_per_step'] * 1e3:.1f} us/step (mixed prefill + decode kernel "
+        f"{res['mixed_ms'] * 1e3:.1f} us, merge {res['merge_ms'] * 1e3:.1f} us); window blocks live {live} of "
+        f"{wi.pool_blocks}, paged equivalent {paged_equiv}")
     del hc
     torch.cuda.empty_cache()
     return res

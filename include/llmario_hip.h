@@ -241,6 +241,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
 #define LMH_KERNEL_MERGE 2u
 #define LMH_KERNEL_ROPE_STORE 3u /* lmh_qk_rope_store's kernel */
 #define LMH_KERNEL_SNAPSHOT 4u   /* lmh_kv_write_seq / lmh_kv_read_seq kernels */
+#define LMH_KERNEL_MIXED 5u      /* lmh_attend's one launch for a call with both prefill units and decode rows */
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches);
 

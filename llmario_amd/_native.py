@@ -157,7 +157,7 @@ SIGNATURES = {
     "lmh_chain_hashes": (i32, [P, u64, u32, C.POINTER(SchedOptions), P, u64, C.POINTER(u64)]),
 }
 
-KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE, KERNEL_ROPE_STORE, KERNEL_SNAPSHOT = 0, 1, 2, 3, 4
+KERNEL_DECODE, KERNEL_PREFILL, KERNEL_MERGE, KERNEL_ROPE_STORE, KERNEL_SNAPSHOT, KERNEL_MIXED = 0, 1, 2, 3, 4, 5
 
 _lib = None
 

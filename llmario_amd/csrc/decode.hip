@@ -24,15 +24,12 @@
 // whose result is scaled by that chunk's per-key scale; V scales fold into P per 32-dim block.
 //
 // f32 pages (VALU): lane per key for Q.K, lane per dim for P.V, fp32 throughout.
-#include "device.h"
+#include "decode_tile.h"
 
 namespace lmh {
 namespace {
 
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-typedef __bf16 b8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
+using namespace dtile;
 
 constexpr int WAVES = 4;  // waves (work items) per workgroup
 
@@ -44,102 +41,6 @@ constexpr int WAVES = 4;  // waves (work items) per workgroup
 template <int HD>
 constexpr int waves_per_eu() {
   return HD >= 256 ? 1 : LMH_DECODE_WPE;
-}
-
-__device__ inline float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
-
-__device__ inline float xmax_groups(float x) {  // max over lanes l, l^16, l^32, l^48
-  x = fmaxf(x, __shfl_xor(x, 16));
-  return fmaxf(x, __shfl_xor(x, 32));
-}
-__device__ inline float xsum_groups(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
-}
-
-__device__ inline uint16_t bf16_rne(float x) {
-  uint32_t u = __float_as_uint(x);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
-
-// int8 x4 (packed in a uint32) -> f16 x4, exact.
-// Four int8 codes -> four f16, exactly: each byte biased to unsigned (q ^ 0x80 = q + 128) becomes
-// the low mantissa byte of f16 1024 (0x64xx = 1024 + u, exact for u < 256), then 1152 is
-// subtracted two lanes at a time (packed f16).
-__device__ inline h4 i8x4_to_h4(uint32_t w) {
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const uint32_t u = w ^ 0x80808080u;
-  const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // [b0, 0x64, b1, 0x64]
-  const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // [b2, 0x64, b3, 0x64]
-  const h2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
-  const h2 a = __builtin_bit_cast(h2, lo) - off, b = __builtin_bit_cast(h2, hi) - off;
-  return h4{a[0], a[1], b[0], b[1]};
-}
-
-// bf16 x4 (two uint32) -> f16 x4 (exact for normal f16 range).
-__device__ inline h4 bf4_to_h4(uint32_t a, uint32_t b) {
-  h4 r;
-  r[0] = (_Float16)__uint_as_float(a << 16);
-  r[1] = (_Float16)__uint_as_float(a & 0xffff0000u);
-  r[2] = (_Float16)__uint_as_float(b << 16);
-  r[3] = (_Float16)__uint_as_float(b & 0xffff0000u);
-  return r;
-}
-
-__device__ inline float h_to_f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-
-template <int KVT, int HD, int HDV>
-struct TileRegs {
-  // f16/bf16: K one uint4 per 32 dims, V one uint4 per 32 dims.
-  // q8_0: K codes one uint4 per 64 dims, V codes one uint4 per 64 dims, plus the lane's scales.
-  static constexpr int NK = (KVT == KV_Q8) ? HD / 64 : HD / 32;
-  static constexpr int NV = (KVT == KV_Q8) ? HDV / 64 : HDV / 32;
-  static constexpr int NKS = (KVT == KV_Q8) ? (4 * (HD / 32) * 2 + 15) / 16 : 0;   // scale uint4s
-  static constexpr int NVS = (KVT == KV_Q8) ? (4 * (HDV / 32) * 2 + 15) / 16 : 0;
-  uint4 k[NK];
-  uint4 v[NV];
-  uint4 ks[NKS > 0 ? NKS : 1];
-  uint4 vs[NVS > 0 ? NVS : 1];
-};
-
-// 16 bytes of a page. Ordinary (caching) loads: successive decode steps re-read the same pages,
-// and a step whose pages fit the last-level cache keeps them there (measured on c2, 297 MB of
-// K/V: 50.7 us per step with these loads against 52.4 us with non-temporal ones).
-__device__ inline uint4 load_stream(const uint8_t* p) { return *(const uint4*)p; }
-
-template <int KVT, int HD, int HDV>
-__device__ inline void load_tile(TileRegs<KVT, HD, HDV>& t, const uint8_t* kb, const uint8_t* vb,
-                                 const uint8_t* ksb, const uint8_t* vsb, uint32_t lane) {
-  using T = TileRegs<KVT, HD, HDV>;
-#pragma unroll
-  for (int c = 0; c < T::NK; c++) t.k[c] = load_stream(kb + c * 1024 + lane * 16);
-#pragma unroll
-  for (int c = 0; c < T::NV; c++) t.v[c] = load_stream(vb + c * 1024 + lane * 16);
-  if constexpr (KVT == KV_Q8) {
-    // scales [key m][chunk]: lane group g = lane/16 needs keys 4g..4g+3, all chunks (contiguous)
-    const uint32_t g = lane >> 4;
-#pragma unroll
-    for (int c = 0; c < T::NKS; c++) t.ks[c] = *(const uint4*)(ksb + g * (4 * (HD / 32) * 2) + c * 16);
-#pragma unroll
-    for (int c = 0; c < T::NVS; c++) t.vs[c] = *(const uint4*)(vsb + g * (4 * (HDV / 32) * 2) + c * 16);
-  }
-}
-
-// Scale (as f32) for key 4g+r, chunk c, from the lane's scale registers.
-template <int NCH>
-__device__ inline float scale_at(const uint4* s, int r, int c) {
-  const int idx = r * NCH + c;  // f16 index
-  const uint32_t w = ((const uint32_t*)s)[idx >> 1];
-  return h_to_f((uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
-}
-
-// The first workgroup of a decode launch copies the call's merge list from the staged (host-mapped)
-// work list into device memory, beside its own work: the merge kernel that follows then starts
-// from device memory instead of a round trip over the bus.
-__device__ inline void copy_merges(const MergeCopy& mc) {
-  if (blockIdx.x != 0) return;
-  for (uint32_t i = threadIdx.x; i < mc.n_words; i += blockDim.x) mc.dst[i] = mc.src[i];
 }
 
 // Split-K merge (forward.rs:772-806), one wave per (task, query head), lanes over dims:
@@ -216,201 +117,9 @@ template <int KVT, int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD>(), waves_per_eu<HD>())))
 void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q, float* out,
                         float* part, MergeCopy mc) {
-  constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
-  constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
-  using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
-  const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  copy_merges(mc);
-  if (wi >= n_items) return;
-  const DecodeItem it = items[wi];
-  const int seq = (int)it.seq;
-  const int32_t* tab = g.table + (size_t)seq * g.bps;
-  const uint32_t hq = lane & 15u, grp = lane >> 4;
-  const bool hv = hq < r.ng && it.h0 + hq < r.group;
-  const uint32_t head = it.kvh * r.group + it.h0 + hq;
-
-  // Q as the B operand of S^T = K Q^T: chunk c, lane (grp, hq) holds dims 32c + 8grp .. +8.
-  MT qh[NC], ql[NC];
-  {
-    const float* qp = q + ((size_t)it.row * r.n_head + (hv ? head : 0)) * HD;
-#pragma unroll
-    for (int c = 0; c < NC; c++) {
-      float4 a = hv ? *(const float4*)(qp + 32 * c + 8 * grp) : make_float4(0, 0, 0, 0);
-      float4 b = hv ? *(const float4*)(qp + 32 * c + 8 * grp + 4) : make_float4(0, 0, 0, 0);
-      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        if constexpr (KVT == KV_BF16) {
-          const uint16_t hb = bf16_rne(x[i]);
-          const float hf = __uint_as_float((uint32_t)hb << 16);
-          qh[c][i] = __builtin_bit_cast(__bf16, hb);
-          ql[c][i] = __builtin_bit_cast(__bf16, bf16_rne(x[i] - hf));
-        } else {
-          const _Float16 hh = (_Float16)x[i];
-          qh[c][i] = hh;
-          ql[c][i] = (_Float16)(x[i] - (float)hh);
-        }
-      }
-    }
-  }
-
-  float m = -INFINITY, lsum = 0.0f;
-  f4 O[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; j++) O[j] = f4{0.f, 0.f, 0.f, 0.f};
-
-  // The item's tiles t0..t1 (at most 64, the host caps chunks): lane i holds the block id of
-  // tile t0 + i, so the loop reads ids with readlane instead of a dependent memory load.
-  const uint32_t t0 = it.p0 >> 4, t1 = (it.p1 - 1) >> 4;
-  const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
-  int my_blk = 0;
-  if (t0 + lane <= t1) my_blk = tab[((t0 + lane) << 4) >> g.bt_shift];
-  auto ptrs = [&](uint32_t t, const uint8_t*& kb, const uint8_t*& vb, const uint8_t*& ksb, const uint8_t*& vsb) {
-    const uint32_t pos = t << 4;
-    const int blk = __builtin_amdgcn_readlane(my_blk, (int)(t - t0));
-    const uint32_t sub = (pos & bt_mask) >> 4;
-    const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
-    const uint8_t* kh = base + g.k_off + it.kvh * g.k_head;
-    const uint8_t* vh = base + g.v_off + it.kvh * g.v_head;
-    kb = kh + sub * g.k_tile;
-    vb = vh + sub * g.v_tile;
-    ksb = kh + g.k_scale + sub * g.k_tile_s;
-    vsb = vh + g.v_scale + sub * g.v_tile_s;
-  };
-  auto fetch = [&](TileRegs<KVT, HD, HDV>& buf, uint32_t t) {
-    const uint8_t *kb, *vb, *ksb, *vsb;
-    ptrs(t, kb, vb, ksb, vsb);
-    load_tile(buf, kb, vb, ksb, vsb, lane);
-  };
-
-  auto step = [&](const TileRegs<KVT, HD, HDV>& cur, uint32_t t) {
-    // ---- scores S^T for 16 keys x 16 heads
-    f4 s = f4{0.f, 0.f, 0.f, 0.f};
-    if constexpr (KVT == KV_Q8) {
-#pragma unroll
-      for (int c = 0; c < NC; c++) {
-        const uint32_t* w = (const uint32_t*)&cur.k[c >> 1];
-        const int o = (c & 1) * 2;
-        const h4 lo4 = i8x4_to_h4(w[o]), hi4 = i8x4_to_h4(w[o + 1]);
-        const h8 kc = h8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-        f4 sc = f4{0.f, 0.f, 0.f, 0.f};
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qh[c], sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, ql[c], sc, 0, 0, 0);
-#pragma unroll
-        for (int rr = 0; rr < 4; rr++) s[rr] += sc[rr] * scale_at<NC>(cur.ks, rr, c);
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < NC; c++) {
-        const MT kc = __builtin_bit_cast(MT, cur.k[c]);
-        if constexpr (KVT == KV_BF16) {
-          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, qh[c], s, 0, 0, 0);
-          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kc, ql[c], s, 0, 0, 0);
-        } else {
-          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, qh[c], s, 0, 0, 0);
-          s = __builtin_amdgcn_mfma_f32_16x16x32_f16(kc, ql[c], s, 0, 0, 0);
-        }
-      }
-    }
-    // ---- online softmax (log2 domain), keys outside [p0, p1) masked
-    const uint32_t kbase = (t << 4) + 4u * grp;
-    float sc[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-      const uint32_t key = kbase + rr;
-      sc[rr] = (key >= it.p0 && key < it.p1) ? s[rr] * r.scale_log2 : -INFINITY;
-    }
-    // Lazy reference max: m (per head) moves only when a score exceeds it by more than 8, so
-    // p = 2^(s - m) <= 2^8 and O is rescaled on few tiles; each lane checks its own 4 scores and
-    // only a triggered tile reduces the head's max across the lane groups.
-    const float lm = fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3]));
-    if (__ballot(lm > m + 8.0f)) {
-      const float tm = xmax_groups(lm);
-      const float mn = tm > m + 8.0f ? tm : m;
-      // no key of this head seen yet (m = -inf): O and lsum are still zero
-      const float alpha = mn == m ? 1.f : (m == -INFINITY ? 0.f : exp2_fast(m - mn));
-      lsum *= alpha;
-#pragma unroll
-      for (int j = 0; j < NJ; j++) O[j] *= alpha;
-      m = mn;
-    }
-    const float mref = m == -INFINITY ? 0.f : m;  // every score is -inf while m is
-    float p[4];
-#pragma unroll
-    for (int rr = 0; rr < 4; rr++) p[rr] = exp2_fast(sc[rr] - mref);
-    lsum += (p[0] + p[1]) + (p[2] + p[3]);
-    // ---- O^T += V^T P^T
-    if constexpr (KVT == KV_Q8) {
-      // P times the V scale of each (key, 32-dim block), in packed f16: the lane's scales sit as
-      // [key i][block b] halves, so keys (0, 1) and (2, 3) of block b pair up with one permute.
-      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-      constexpr int NCH = HDV / 32;
-      const uint32_t* vsw = (const uint32_t*)cur.vs;
-      const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]}, p23 = h2{(_Float16)p[2], (_Float16)p[3]};
-#pragma unroll
-      for (int b = 0; b < HDV / 32; b++) {
-        const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t s01 = __builtin_amdgcn_perm(vsw[(NCH + b) >> 1], vsw[b >> 1], sel);
-        const uint32_t s23 = __builtin_amdgcn_perm(vsw[(3 * NCH + b) >> 1], vsw[(2 * NCH + b) >> 1], sel);
-        const h2 q01 = p01 * __builtin_bit_cast(h2, s01), q23 = p23 * __builtin_bit_cast(h2, s23);
-        const h4 pb = h4{q01[0], q01[1], q23[0], q23[1]};
-#pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-          const int j = 2 * b + jj;
-          const uint32_t w = ((const uint32_t*)&cur.v[j >> 2])[j & 3];
-          O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(w), pb, O[j], 0, 0, 0);
-        }
-      }
-    } else {
-      const h4 pb = h4{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
-#pragma unroll
-      for (int j = 0; j < NJ; j++) {
-        const uint32_t* w = (const uint32_t*)&cur.v[j >> 1];
-        const int o = (j & 1) * 2;
-        h4 va;
-        if constexpr (KVT == KV_BF16) {
-          va = bf4_to_h4(w[o], w[o + 1]);
-        } else {
-          va = __builtin_bit_cast(h4, make_uint2(w[o], w[o + 1]));
-        }
-        O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, O[j], 0, 0, 0);
-      }
-    }
-  };
-
-  // Two-deep ping-pong: tile t+1 is in flight while tile t is computed.
-  TileRegs<KVT, HD, HDV> b0, b1;
-  fetch(b0, t0);
-  for (uint32_t t = t0; t <= t1; t += 2) {
-    if (t + 1 <= t1) fetch(b1, t + 1);
-    step(b0, t);
-    if (t + 1 > t1) break;
-    if (t + 2 <= t1) fetch(b0, t + 2);
-    step(b1, t + 1);
-  }
-  lsum = xsum_groups(lsum);
-
-  if (it.slot == NO_SLOT) {
-    if (!hv) return;
-    const float inv = 1.0f / lsum;
-    float* op = out + ((size_t)it.row * r.n_head + head) * HDV;
-#pragma unroll
-    for (int j = 0; j < NJ; j++) {
-      const f4 o = O[j] * inv;
-      *(float4*)(op + 16 * j + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
-    }
-    return;
-  }
-  if (hv) {
-    float* pp = part + ((size_t)it.slot * r.ng + hq) * (HDV + 4);
-#pragma unroll
-    for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][0], O[j][1], O[j][2], O[j][3]);
-    if (grp == 0) {
-      pp[HDV] = m;
-      pp[HDV + 1] = lsum;
-    }
-  }
+  copy_merges(mc, blockIdx.x == 0);
+  if (wi < n_items) decode_item<KVT, HD, HDV>(g, r, items, wi, q, out, part);
 }
 
 // ---- f32 pages: VALU path ----------------------------------------------------------------------
@@ -424,7 +133,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
   __shared__ float ps[WAVES][NG][64];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t wi = blockIdx.x * WAVES + w;
-  copy_merges(mc);
+  copy_merges(mc, blockIdx.x == 0);
   const bool active = wi < n_items;
   DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, 0, 0};
   const uint32_t ng = r.ng;

@@ -167,6 +167,12 @@ bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
                           uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s);
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group);
+// A call holding both prefill units and decode items, in one launch (any type and head size
+// prefill_supported accepts): pf_wg prefill workgroups, then the decode items eight per workgroup.
+hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
+                        uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
+                        uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
+                        hipStream_t s);
 uint32_t prefill_cols_per_unit();
 size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg);
 

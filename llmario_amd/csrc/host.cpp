@@ -179,8 +179,6 @@ struct lmh_kv {
   // ---- device
   int device = 0;
   uint32_t n_cu = 0;                        // compute units of the device
-  hipStream_t side = nullptr;               // decode work running beside a prefill kernel
-  hipEvent_t fork = nullptr, join = nullptr;
   std::vector<uint32_t> decode_capacity;    // per layer: decode items resident at once (0 = not yet asked)
   uint8_t* d_pool = nullptr;
   int32_t* d_table = nullptr;
@@ -198,8 +196,8 @@ struct lmh_kv {
   std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
   std::vector<uint32_t> ev_kind;
   size_t ev_used = 0;
-  double acc_ms[5] = {0, 0, 0, 0, 0};
-  uint64_t launches[5] = {0, 0, 0, 0, 0};
+  double acc_ms[6] = {0, 0, 0, 0, 0, 0};
+  uint64_t launches[6] = {0, 0, 0, 0, 0, 0};
   std::vector<PrefillItem> pitems;
   std::vector<uint8_t> payload;
   std::vector<lmh_sched*> scheds;           // schedulers bound to this handle
@@ -207,9 +205,6 @@ struct lmh_kv {
 
   ~lmh_kv() {
     if (d_pool || d_table || d_wpool) (void)hipDeviceSynchronize();
-    if (fork) (void)hipEventDestroy(fork);
-    if (join) (void)hipEventDestroy(join);
-    if (side) (void)hipStreamDestroy(side);
     if (d_pool) (void)hipFree(d_pool);
     if (d_table) (void)hipFree(d_table);
     if (d_wpool) (void)hipFree(d_wpool);
@@ -756,9 +751,6 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   if (e == hipSuccess) e = hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, o->device);
   kv->n_cu = (uint32_t)std::max(n_cu, 1);
   kv->decode_capacity.assign(kv->layers.size(), 0);
-  if (e == hipSuccess) e = hipStreamCreateWithFlags(&kv->side, hipStreamNonBlocking);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->fork, hipEventDisableTiming);
-  if (e == hipSuccess) e = hipEventCreateWithFlags(&kv->join, hipEventDisableTiming);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_pool, kv->pool_blocks * kv->block_bytes);
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
   if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wpool, kv->wpool_blocks * kv->wblock_bytes);
@@ -1436,29 +1428,6 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     if ((e = kv->merge_buf.ensure(merges_bytes)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
   }
   if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
-  // A mixed batch runs its decode items on a second stream, beside the prefill kernel (which
-  // holds one workgroup per CU it uses; the decode waves take the CUs it leaves free), and the
-  // caller's stream waits for both before the merge.
-  const bool overlap = !kv->pitems.empty() && !kv->items.empty();
-  hipStream_t ds = st;
-  if (overlap) {
-    if ((e = hipEventRecord(kv->fork, st)) != hipSuccess) return kv->hip_fail(e, "event");
-    if ((e = hipStreamWaitEvent(kv->side, kv->fork, 0)) != hipSuccess) return kv->hip_fail(e, "stream wait");
-    ds = kv->side;
-  }
-  if (!kv->pitems.empty()) {
-    PrefillGeom pg{};
-    pg.n_head = y.n_head;
-    pg.group = group;
-    pg.scale_log2 = scale * 1.4426950408889634f;
-    pg.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
-    if ((e = kv->time_begin(st, LMH_KERNEL_PREFILL)) != hipSuccess) return kv->hip_fail(e, "event");
-    e = launch_prefill(kv->geom(layer), pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg,
-                       max_pages, q, out, st);
-    if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
-    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
-  }
-  if (kv->items.empty()) return kv->release_rows(slot, st);
   const PageGeom g = kv->geom(layer);
   RowGeom r{};
   r.row_seq = rs;
@@ -1468,15 +1437,36 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   r.ng = ng;
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
-  if ((e = kv->time_begin(ds, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
+  PrefillGeom pg{};
+  pg.n_head = y.n_head;
+  pg.group = group;
+  pg.scale_log2 = r.scale_log2;
+  pg.window = r.window;
   const MergeCopy mc{(const uint32_t*)(ex + items_pad), (uint32_t*)kv->merge_buf.p,
                      kv->merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
-  e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, ds);
-  if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
-  if ((e = kv->time_end(ds)) != hipSuccess) return kv->hip_fail(e, "event");
+  // A mixed batch (prefill units and decode items) runs as one launch: the prefill workgroups
+  // first (one per CU they reach), then the decode items, a wave each, on the CUs left free.
+  const bool overlap = !kv->pitems.empty() && !kv->items.empty();
   if (overlap) {
-    if ((e = hipEventRecord(kv->join, ds)) != hipSuccess) return kv->hip_fail(e, "event");
-    if ((e = hipStreamWaitEvent(st, kv->join, 0)) != hipSuccess) return kv->hip_fail(e, "stream wait");
+    if ((e = kv->time_begin(st, LMH_KERNEL_MIXED)) != hipSuccess) return kv->hip_fail(e, "event");
+    e = launch_mixed(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, r,
+                     (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st);
+    if (e != hipSuccess) return kv->hip_fail(e, "mixed kernel");
+    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  }
+  if (!overlap && !kv->pitems.empty()) {
+    if ((e = kv->time_begin(st, LMH_KERNEL_PREFILL)) != hipSuccess) return kv->hip_fail(e, "event");
+    e = launch_prefill(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, q, out,
+                       st);
+    if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
+    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
+  }
+  if (kv->items.empty()) return kv->release_rows(slot, st);
+  if (!overlap) {
+    if ((e = kv->time_begin(st, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
+    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st);
+    if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
+    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   if (!kv->merges.empty()) {
     if ((e = kv->time_begin(st, LMH_KERNEL_MERGE)) != hipSuccess) return kv->hip_fail(e, "event");
@@ -1495,7 +1485,7 @@ int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
 }
 
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches) {
-  if (!kv || kernel > LMH_KERNEL_SNAPSHOT) return LMH_INVALID_ARGUMENT;
+  if (!kv || kernel > LMH_KERNEL_MIXED) return LMH_INVALID_ARGUMENT;
   hipError_t e = kv->collect_times();
   if (e != hipSuccess) return kv->hip_fail(e, "event timing");
   if (ms) *ms = kv->acc_ms[kernel];

@@ -21,7 +21,7 @@
 // column's reference max enters as the initial accumulator of Q.K, so the products are the
 // exponent arguments directly. The reference max moves lazily (only when a score exceeds it by
 // more than 8 in the log2 domain), so the O accumulators are almost never rescaled.
-#include "device.h"
+#include "decode_tile.h"
 
 namespace lmh {
 namespace {
@@ -75,10 +75,10 @@ __device__ inline uint32_t bf2_to_h2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
 }
 
+// Workgroup `wg` of a prefill launch: its list of units, items[wg * per_wg ..].
 template <int KVT, int HD>
-__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32_t per_wg, const float* q,
-                    float* out) {
+__device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items,
+                                           uint32_t per_wg, const float* q, float* out, uint32_t wg) {
   constexpr int NC = HD / 32;                 // Q.K chunks of 32 dims
   constexpr int NJ = HD / 16;                 // O^T blocks of 16 dims
   constexpr int TILE = 16 * HD * 2;           // bytes of one 16-token page tile (K or V)
@@ -90,7 +90,7 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
   // The workgroup's units (the host's balanced assignment, per_wg slots, an empty unit ends the
   // list): fetched once, so each unit starts without a memory round trip for its descriptor.
   {
-    const uint32_t* src = (const uint32_t*)(items + (size_t)blockIdx.x * per_wg);
+    const uint32_t* src = (const uint32_t*)(items + (size_t)wg * per_wg);
     for (uint32_t i = threadIdx.x; i < per_wg * (sizeof(PrefillItem) / 4); i += NT) ((uint32_t*)units)[i] = src[i];
   }
   __syncthreads();
@@ -486,10 +486,50 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
 }
 
 template <int KVT, int HD>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32_t per_wg, const float* q,
+                    float* out) {
+  prefill_wg<KVT, HD>(g, pg, items, per_wg, q, out, blockIdx.x);
+}
+
+// A mixed batch (prefill units and decode items) in one launch: workgroups 0 .. pf_wg-1 run the
+// prefill units as prefill_kernel does (one per CU it reaches), the others take PW decode items
+// each, a wave per item, on the CUs the prefill workgroups leave free and then on those they
+// release. The decode waves fit the same register budget (two waves per SIMD) and each
+// workgroup carries the prefill LDS allocation, so a CU holds one workgroup of either kind: the
+// same eight waves per CU the decode kernel runs at. One launch instead of a decode launch on a
+// second stream saves the two cross-stream waits and their idle gaps.
+template <int KVT, int HD>
+__global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_t per_wg, uint32_t pf_wg, RowGeom r,
+                  const DecodeItem* items, uint32_t n_items, const float* q, float* out, float* part, MergeCopy mc) {
+  if (blockIdx.x < pf_wg) {
+    prefill_wg<KVT, HD>(g, pg, pitems, per_wg, q, out, blockIdx.x);
+    return;
+  }
+  const uint32_t b = blockIdx.x - pf_wg;
+  dtile::copy_merges(mc, b == 0);
+  const uint32_t wi = b * PW + (threadIdx.x >> 6);
+  if (wi < n_items) dtile::decode_item<KVT, HD, HD>(g, r, items, wi, q, out, part);
+}
+
+template <int KVT, int HD>
 hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
                     uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s) {
   const size_t lds = prefill_lds_bytes(HD, max_pages, per_wg);
   hipLaunchKernelGGL((prefill_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+  return hipGetLastError();
+}
+
+template <int KVT, int HD>
+hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
+                          uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
+                          uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
+                          hipStream_t s) {
+  const size_t lds = prefill_lds_bytes(HD, max_pages, per_wg);
+  const uint32_t n_wg = pf_wg + (n_items + PW - 1) / PW;
+  hipLaunchKernelGGL((mixed_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r, items,
+                     n_items, q, out, part, mc);
   return hipGetLastError();
 }
 
@@ -504,6 +544,19 @@ size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg) {
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group) {
   return (kv_type == KV_F16 || kv_type == KV_BF16) && hd == hdv && (hd == 64 || hd == 128) && group >= 1 &&
          group <= PW * COLS;
+}
+
+hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
+                        uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
+                        uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
+                        hipStream_t s) {
+  if (pf_wg == 0 || per_wg == 0 || n_items == 0 || g.hd != g.hdv) return hipErrorInvalidValue;
+#define LMH_MIXED(T, D)                                                                                          \
+  if (g.kv_type == T && g.hd == D)                                                                               \
+    return launch_mixed_t<T, D>(g, pg, pitems, pf_wg, per_wg, max_pages, r, items, n_items, q, out, part, mc, s);
+  LMH_MIXED(KV_F16, 128) LMH_MIXED(KV_F16, 64) LMH_MIXED(KV_BF16, 128) LMH_MIXED(KV_BF16, 64)
+#undef LMH_MIXED
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,

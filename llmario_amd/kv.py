@@ -268,13 +268,14 @@ class HipKvCache:
         self._check(N.lib().lmh_kv_set_timing(self.h, 1 if on else 0))
 
     def kernel_time(self, kernel: str = "decode"):
-        """(milliseconds, launches) of one kernel kind ("decode" | "prefill" | "merge") since its
-        last read (needs set_timing(True) while the calls ran)."""
+        """(milliseconds, launches) of one kernel kind ("decode" | "prefill" | "merge" | "mixed" |
+        "rope_store" | "snapshot") since its last read (needs set_timing(True) while the calls
+        ran). "mixed" is the one launch of a call with both prefill units and decode rows."""
         kind = {"decode": N.KERNEL_DECODE, "prefill": N.KERNEL_PREFILL, "merge": N.KERNEL_MERGE,
-                "rope_store": N.KERNEL_ROPE_STORE, "snapshot": N.KERNEL_SNAPSHOT}[kernel]
+                "rope_store": N.KERNEL_ROPE_STORE, "snapshot": N.KERNEL_SNAPSHOT, "mixed": N.KERNEL_MIXED}[kernel]
         ms, n = C.c_double(), N.u64()
         self._check(N.lib().lmh_kv_kernel_time(self.h, kind, C.byref(ms), C.byref(n)))
         return ms.value, n.value
 
     def kernel_times(self) -> dict:
-        return {k: self.kernel_time(k) for k in ("decode", "prefill", "merge")}
+        return {k: self.kernel_time(k) for k in ("decode", "prefill", "merge", "mixed")}
