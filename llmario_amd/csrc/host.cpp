@@ -20,7 +20,6 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <deque>
 #include <map>
 #include <queue>
 #include <string>
@@ -65,6 +64,23 @@ uint32_t tile_bytes(uint32_t t, uint32_t dim) {
 }
 uint32_t tile_scale_bytes(uint32_t t, uint32_t dim) { return t == LMH_KV_Q8_0 ? 16 * (dim / 32) * 2 : 0; }
 
+struct DirtyRows {  // the rows [lo, hi) of a host-side table that differ from the device copy
+  uint64_t lo = ~0ull, hi = 0;
+  void mark(uint64_t r) {
+    lo = std::min(lo, r);
+    hi = std::max(hi, r + 1);
+  }
+  void all(uint64_t n) {
+    lo = 0;
+    hi = n;
+  }
+  bool any() const { return lo < hi; }
+  void clear() {
+    lo = ~0ull;
+    hi = 0;
+  }
+};
+
 struct Uploader {  // ring of pinned, device-mapped staging slots, reused once their event has passed
   static constexpr int N = 4;
   uint8_t* host[N] = {};
@@ -81,6 +97,17 @@ struct Uploader {  // ring of pinned, device-mapped staging slots, reused once t
       }
       if (host[i]) (void)hipHostFree(host[i]);
     }
+  }
+  // Every slot allocated up front with at least `bytes`, so calls on the hot path do not pay for a
+  // pinned allocation the first time a slot comes round.
+  hipError_t reserve(size_t bytes) {
+    for (int i = 0; i < N; i++) {
+      int idx;
+      uint8_t* p;
+      hipError_t e = acquire(bytes, idx, p);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
   }
   // A host buffer of at least `bytes` whose previous copy has finished.
   hipError_t acquire(size_t bytes, int& idx, uint8_t*& ptr) {
@@ -173,7 +200,7 @@ struct lmh_kv {
   uint8_t* d_wpool = nullptr;
   int32_t* d_wtable = nullptr;
   std::vector<int32_t> h_wtable;
-  bool wtable_dirty = false;
+  DirtyRows wtable_rows;
   // ---- sequences
   std::vector<Seq> seqs;
   // ---- device
@@ -183,7 +210,7 @@ struct lmh_kv {
   uint8_t* d_pool = nullptr;
   int32_t* d_table = nullptr;
   std::vector<int32_t> h_table;
-  bool table_dirty = true;
+  DirtyRows table_rows;
   std::vector<PageOp> pending;
   Uploader up;
   DevBuf part_buf, ops_buf, merge_buf;
@@ -246,7 +273,7 @@ struct lmh_kv {
     int32_t* row = h_table.data() + s * bps;
     const auto& bl = seqs[s].blocks;
     for (uint64_t i = 0; i < bps; i++) row[i] = i < bl.size() ? (int32_t)bl[i] : -1;
-    table_dirty = true;
+    table_rows.mark(s);
   }
 
   // ---- window pool (metal/src/kv.rs:304-372) ---------------------------------------------
@@ -256,7 +283,7 @@ struct lmh_kv {
     int32_t* row = h_wtable.data() + s * bps;
     const auto& wb = seqs[s].wblocks;
     for (uint64_t i = 0; i < bps; i++) row[i] = i < wb.size() ? wb[i] : -1;
-    wtable_dirty = true;
+    wtable_rows.mark(s);
   }
   // Window blocks reserve_window(s, len, new_len) releases and takes (whole calls are checked
   // before any change, so a short window pool fails like a short paged pool: nothing changes).
@@ -322,19 +349,19 @@ struct lmh_kv {
     const uint64_t missing = want > seqs[s].blocks.size() ? want - seqs[s].blocks.size() : 0;
     const uint64_t wanted = blocks_needed(s, new_len);
     const bool cow = wanted > missing;
-    if (pool.free_q.size() < wanted) {
+    if (pool.free_blocks() < wanted) {
       if (needed) *needed = wanted;
-      if (free_blocks) *free_blocks = pool.free_q.size();
+      if (free_blocks) *free_blocks = pool.free_blocks();
       return fail(LMH_KV_FULL, "KV cache full: " + std::to_string(wanted) + " more blocks needed, " +
-                                   std::to_string(pool.free_q.size()) + " free");
+                                   std::to_string(pool.free_blocks()) + " free");
     }
     uint64_t w_take = 0, w_give = 0;
     if (with_window) window_delta(s, len, new_len, w_take, w_give);
-    if (w_take > wpool.free_q.size() + w_give) {
+    if (w_take > wpool.free_blocks() + w_give) {
       if (needed) *needed = w_take;
-      if (free_blocks) *free_blocks = wpool.free_q.size() + w_give;
+      if (free_blocks) *free_blocks = wpool.free_blocks() + w_give;
       return fail(LMH_KV_FULL, "window pool full: " + std::to_string(w_take) + " window blocks needed, " +
-                                   std::to_string(wpool.free_q.size() + w_give) + " free");
+                                   std::to_string(wpool.free_blocks() + w_give) + " free");
     }
     if (with_window) reserve_window(s, len, new_len);
     if (len % bt != 0 && len < new_len) {
@@ -426,25 +453,21 @@ struct lmh_kv {
       }
     }
     pending.clear();
-    if (table_dirty) {
+    // the block-table rows changed since the last upload (one copy spanning them)
+    auto upload = [&](DirtyRows& d, const std::vector<int32_t>& h_tab, int32_t* d_tab) -> int32_t {
+      if (!d.any()) return LMH_OK;
       int idx;
       uint8_t* h;
-      const size_t bytes = h_table.size() * 4;
+      const size_t off = d.lo * bps, bytes = (d.hi - d.lo) * bps * 4;
       if ((e = up.acquire(bytes, idx, h)) != hipSuccess) return hip_fail(e, "staging");
-      std::memcpy(h, h_table.data(), bytes);
-      if ((e = up.send(idx, d_table, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
-      table_dirty = false;
-    }
-    if (wtable_dirty) {
-      int idx;
-      uint8_t* h;
-      const size_t bytes = h_wtable.size() * 4;
-      if ((e = up.acquire(bytes, idx, h)) != hipSuccess) return hip_fail(e, "staging");
-      std::memcpy(h, h_wtable.data(), bytes);
-      if ((e = up.send(idx, d_wtable, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
-      wtable_dirty = false;
-    }
-    return LMH_OK;
+      std::memcpy(h, h_tab.data() + off, bytes);
+      if ((e = up.send(idx, d_tab + off, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
+      d.clear();
+      return LMH_OK;
+    };
+    int32_t rc = upload(table_rows, h_table, d_table);
+    if (rc == LMH_OK && window) rc = upload(wtable_rows, h_wtable, d_wtable);
+    return rc;
   }
 
   PageGeom geom(uint32_t l) const {
@@ -736,6 +759,7 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   kv->backed.assign(kv->pool_blocks, 0);
   kv->seqs.assign(kv->n_seqs, Seq{});
   kv->h_table.assign(kv->n_seqs * kv->bps, -1);
+  kv->table_rows.all(kv->n_seqs);
   if (kv->window) {
     // metal/src/kv.rs:130-133: a sequence's live window blocks are the window behind its first new
     // token plus one call's tokens, and a partial block at each end
@@ -743,7 +767,7 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
     kv->wpool_blocks = kv->n_seqs * std::min<uint64_t>((kv->window + n_batch + bt - 1) / bt + 1, kv->bps);
     kv->wpool.init(kv->wpool_blocks, bt);
     kv->h_wtable.assign(kv->n_seqs * kv->bps, -1);
-    kv->wtable_dirty = true;
+    kv->wtable_rows.all(kv->n_seqs);
   }
   kv->device = o->device;
   hipError_t e = hipSetDevice(o->device);
@@ -755,6 +779,7 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
   if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wpool, kv->wpool_blocks * kv->wblock_bytes);
   if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wtable, kv->h_wtable.size() * 4);
+  if (e == hipSuccess) e = kv->up.reserve(std::max<size_t>(64 << 10, kv->bps * 4 * 16));
   if (e != hipSuccess) {
     g_create_error = std::string("device allocation failed: ") + hipGetErrorString(e);
     delete kv;
@@ -821,7 +846,7 @@ int32_t lmh_kv_set_seq_len(lmh_kv* kv, uint64_t seq, uint64_t len) {
   if (kv->window) {  // the window blocks the next query can see: [first_live(len), ceil(len / bt))
     uint64_t take, give;
     kv->window_delta(seq, len, len, take, give);
-    if (take > kv->wpool.free_q.size() + give) return kv->fail(LMH_KV_FULL, "window pool full");
+    if (take > kv->wpool.free_blocks() + give) return kv->fail(LMH_KV_FULL, "window pool full");
     kv->reserve_window(seq, len, len);
   }
   kv->seqs[seq].len = len;
@@ -830,7 +855,7 @@ int32_t lmh_kv_set_seq_len(lmh_kv* kv, uint64_t seq, uint64_t len) {
 
 int32_t lmh_kv_free_blocks(const lmh_kv* kv, uint64_t* n) {
   if (!kv || !n) return LMH_INVALID_ARGUMENT;
-  *n = kv->pool.free_q.size();
+  *n = kv->pool.free_blocks();
   return LMH_OK;
 }
 
@@ -946,18 +971,18 @@ int32_t lmh_kv_read_seq(lmh_kv* kv, uint64_t seq, uint64_t len, const void* src,
   const uint64_t nb = (len + kv->bt - 1) / kv->bt;
   uint64_t own = 0;
   for (uint32_t b : kv->seqs[seq].blocks) own += kv->pool.meta[b].refs == 1 ? 1 : 0;
-  if (nb > kv->pool.free_q.size() + own) {
+  if (nb > kv->pool.free_blocks() + own) {
     if (needed) *needed = nb;
-    if (free_blocks) *free_blocks = kv->pool.free_q.size() + own;
+    if (free_blocks) *free_blocks = kv->pool.free_blocks() + own;
     return kv->fail(LMH_KV_FULL, "KV cache full: snapshot needs " + std::to_string(nb) + " blocks");
   }
   uint64_t first, end;
   window_span(kv, len, first, end);
   uint64_t wown = 0;
   for (int32_t b : kv->seqs[seq].wblocks) wown += b >= 0 ? 1 : 0;
-  if (end - first > kv->wpool.free_q.size() + wown) {
+  if (end - first > kv->wpool.free_blocks() + wown) {
     if (needed) *needed = end - first;
-    if (free_blocks) *free_blocks = kv->wpool.free_q.size() + wown;
+    if (free_blocks) *free_blocks = kv->wpool.free_blocks() + wown;
     return kv->fail(LMH_KV_FULL, "window pool full: snapshot needs " + std::to_string(end - first) + " window blocks");
   }
   kv->clear(seq);
@@ -986,7 +1011,7 @@ int32_t lmh_kv_window_info(const lmh_kv* kv, lmh_window_info* out) {
   out->window = kv->window;
   out->block_bytes = kv->wblock_bytes;
   out->pool_blocks = kv->wpool_blocks;
-  out->free_blocks = kv->wpool.free_q.size();
+  out->free_blocks = kv->wpool.free_blocks();
   return LMH_OK;
 }
 
@@ -1016,14 +1041,10 @@ int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, ui
       return kv->fail(LMH_INVALID_ARGUMENT, "block id out of range or repeated");
     want[blocks[i]] = 1;
   }
-  uint64_t found = 0;
-  for (uint32_t b : kv->pool.free_q) found += want[b];
-  if (found != n) return kv->fail(LMH_INVALID_ARGUMENT, "a requested block is not free");
-  std::deque<uint32_t> rest;
-  for (uint32_t b : kv->pool.free_q)
-    if (!want[b]) rest.push_back(b);
-  kv->pool.free_q.swap(rest);
+  for (uint64_t i = 0; i < n; i++)
+    if (!kv->pool.is_free(blocks[i])) return kv->fail(LMH_INVALID_ARGUMENT, "a requested block is not free");
   for (uint64_t i = 0; i < n; i++) {
+    kv->pool.unlink_free(blocks[i]);
     BlockMeta& m = kv->pool.meta[blocks[i]];
     if (m.has_hash) {
       kv->pool.by_hash.erase(m.hash);
@@ -1082,14 +1103,14 @@ int32_t lmh_batch_prepare(lmh_kv* kv, const lmh_seq_tokens* batch, uint64_t n, l
   }
   uint64_t need = 0;
   for (uint64_t i = 0; i < n; i++) need += kv->blocks_needed(batch[i].seq, kv->seqs[batch[i].seq].len + batch[i].n_tokens);
-  if (need > kv->pool.free_q.size()) {
+  if (need > kv->pool.free_blocks()) {
     if (needed) *needed = need;
-    if (free_blocks) *free_blocks = kv->pool.free_q.size();
+    if (free_blocks) *free_blocks = kv->pool.free_blocks();
     return kv->fail(LMH_KV_FULL, "KV cache full: " + std::to_string(need) + " more blocks needed, " +
-                                     std::to_string(kv->pool.free_q.size()) + " free");
+                                     std::to_string(kv->pool.free_blocks()) + " free");
   }
   if (kv->window) {  // the window pool, entry by entry in batch order (each releases before it takes)
-    uint64_t free = kv->wpool.free_q.size(), w_need = 0;
+    uint64_t free = kv->wpool.free_blocks(), w_need = 0;
     bool short_ = false;
     for (uint64_t i = 0; i < n; i++) {
       uint64_t take, give;
@@ -1102,7 +1123,7 @@ int32_t lmh_batch_prepare(lmh_kv* kv, const lmh_seq_tokens* batch, uint64_t n, l
     }
     if (short_) {
       if (needed) *needed = w_need;
-      if (free_blocks) *free_blocks = kv->wpool.free_q.size();
+      if (free_blocks) *free_blocks = kv->wpool.free_blocks();
       return kv->fail(LMH_KV_FULL, "window pool full: " + std::to_string(w_need) + " window blocks needed");
     }
   }

@@ -14,7 +14,6 @@
 #include <algorithm>
 #include <array>
 #include <cstring>
-#include <deque>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -36,11 +35,18 @@ struct BlockMeta {
   uint32_t refs = 0;
   bool has_hash = false;
   Hash hash{};
+  uint32_t prev = 0xffffffffu, next = 0xffffffffu;  // free-queue links (held while refs == 0)
 };
 
+// The block pool of kv/src/lib.rs:75-186. The LRU free queue is a list threaded through the
+// blocks' metadata (a block is on it exactly while it has no references), so taking a cached block
+// back out of the middle (reclaim) is O(1) where a queue scan would cost O(free blocks); the free
+// and cached-free counts are kept as the queue changes.
 struct BlockPool {
+  static constexpr uint32_t NIL = 0xffffffffu;
   std::vector<BlockMeta> meta;
-  std::deque<uint32_t> free_q;
+  uint32_t head = NIL, tail = NIL;
+  uint64_t n_free = 0, n_cached_free = 0;
   std::unordered_map<Hash, uint32_t, HashKey> by_hash;
   uint64_t hits = 0, misses = 0, evictions = 0;
   uint32_t block_tokens = 16;
@@ -48,18 +54,42 @@ struct BlockPool {
   void init(uint64_t n_blocks, uint32_t bt) {
     block_tokens = bt;
     meta.assign(n_blocks, BlockMeta{});
-    free_q.clear();
+    head = tail = NIL;
+    n_free = n_cached_free = 0;
     by_hash.clear();
     hits = misses = evictions = 0;
-    for (uint64_t i = 0; i < n_blocks; i++) free_q.push_back((uint32_t)i);
+    for (uint64_t i = 0; i < n_blocks; i++) push_free((uint32_t)i);
   }
-  uint64_t free_blocks() const { return free_q.size(); }
+  uint64_t free_blocks() const { return n_free; }
+  uint64_t cached_free_blocks() const { return n_cached_free; }
+  bool is_free(uint32_t b) const { return meta[b].refs == 0; }
+  // append to the back of the free queue / unlink from anywhere in it
+  void push_free(uint32_t b) {
+    BlockMeta& m = meta[b];
+    m.prev = tail;
+    m.next = NIL;
+    if (tail != NIL) meta[tail].next = b;
+    else head = b;
+    tail = b;
+    n_free++;
+    if (m.has_hash) n_cached_free++;
+  }
+  void unlink_free(uint32_t b) {
+    BlockMeta& m = meta[b];
+    if (m.prev != NIL) meta[m.prev].next = m.next;
+    else head = m.next;
+    if (m.next != NIL) meta[m.next].prev = m.prev;
+    else tail = m.prev;
+    m.prev = m.next = NIL;
+    n_free--;
+    if (m.has_hash) n_cached_free--;
+  }
   // lib.rs:93-109: n blocks LRU-first, evicting cached content; false (nothing taken) if short
   bool alloc(uint64_t n, std::vector<uint32_t>& out) {
-    if (free_q.size() < n) return false;
+    if (n_free < n) return false;
     for (uint64_t i = 0; i < n; i++) {
-      const uint32_t b = free_q.front();
-      free_q.pop_front();
+      const uint32_t b = head;
+      unlink_free(b);
       BlockMeta& m = meta[b];
       if (m.has_hash) {
         by_hash.erase(m.hash);
@@ -75,7 +105,7 @@ struct BlockPool {
   void release(uint32_t b) {
     BlockMeta& m = meta[b];
     if (m.refs == 0) return;
-    if (--m.refs == 0) free_q.push_back(b);
+    if (--m.refs == 0) push_free(b);
   }
   // lib.rs:113-118 (a call that would change nothing returns early)
   void set_hash(uint32_t b, const Hash& h) {
@@ -85,6 +115,7 @@ struct BlockPool {
       if (it != by_hash.end() && it->second == b) return;
     }
     if (m.has_hash) by_hash.erase(m.hash);
+    else if (m.refs == 0) n_cached_free++;
     m.hash = h;
     m.has_hash = true;
     by_hash[h] = b;
@@ -96,21 +127,15 @@ struct BlockPool {
     auto it = by_hash.find(m.hash);
     if (it != by_hash.end() && it->second == b) by_hash.erase(it);
     m.has_hash = false;
+    if (m.refs == 0) n_cached_free--;
   }
   // lib.rs:132-143: a free cached block leaves the free queue, an in-use one gains a reference
   bool reclaim(const Hash& h, uint32_t& b) {
     auto it = by_hash.find(h);
     if (it == by_hash.end()) return false;
     b = it->second;
-    BlockMeta& m = meta[b];
-    if (m.refs == 0) {
-      for (auto q = free_q.begin(); q != free_q.end(); ++q)
-        if (*q == b) {
-          free_q.erase(q);
-          break;
-        }
-    }
-    m.refs++;
+    if (meta[b].refs == 0) unlink_free(b);
+    meta[b].refs++;
     hits++;
     return true;
   }

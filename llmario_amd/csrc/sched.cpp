@@ -414,10 +414,8 @@ int32_t lmh_sched_get_stats(const lmh_sched* s, lmh_sched_stats* o) {
   o->queued = s->queue.size();
   o->retractions = s->retractions;
   o->n_blocks = p.meta.size();
-  o->free = p.free_q.size();
-  uint64_t cf = 0;
-  for (uint32_t b : p.free_q) cf += p.meta[b].has_hash ? 1 : 0;
-  o->cached_free = cf;
+  o->free = p.free_blocks();
+  o->cached_free = p.cached_free_blocks();
   o->hits = p.hits;
   o->misses = p.misses;
   o->evictions = p.evictions;
