@@ -39,6 +39,17 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def read_ceiling(nbytes: int, iters: int = 50) -> float:
+    """GB/s of a plain streaming read of `nbytes` on cuda:0 (the library's benchmark hook)."""
+    from llmario_amd import _native as N
+
+    gbs = ctypes.c_double()
+    rc = N.lib().lmh_bench_read_ceiling(0, nbytes, iters, ctypes.byref(gbs))
+    if rc != N.OK:
+        raise RuntimeError(f"lmh_bench_read_ceiling failed ({rc})")
+    return gbs.value
+
+
 def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, warmup_s: float = 0.0):
     """Time `steps` calls of one configuration after at least `warmup` untimed calls and at least
     `warmup_s` seconds of them (matrix-core work runs at a lower clock for the first tens of
@@ -515,6 +526,13 @@ def main():
             "frac": round(head["hbm_frac"], 4), "traffic": traffic,
             "kernel": "decode_mfma_kernel<f16,128,128>", "kernel_us": round(head["kernel_ms"] * 1e3, 2),
             "algorithmic_bytes": head["bytes"]}
+    # the device's practical streaming-read rate over the same number of bytes (a plain read
+    # kernel, lmh_bench_read_ceiling), beside the published peak the roofline uses
+    ceil_gbs = read_ceiling(int(head["bytes"]))
+    roof["read_ceiling_GBps"] = round(ceil_gbs, 1)
+    roof["frac_of_read_ceiling"] = round(head["kernel_GBps"] / ceil_gbs, 4)
+    log(f"[bench] streaming-read ceiling over {int(head['bytes'])} bytes: {ceil_gbs:.0f} GB/s; decode kernel at "
+        f"{roof['frac_of_read_ceiling']:.1%} of it")
     cpu = None
     if not args.no_cpu_baseline:
         th = physical_cores()

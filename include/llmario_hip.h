@@ -245,6 +245,12 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable);
 int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* launches);
 
+/* Benchmark hook (no counterpart in the reference; for benchmark drivers that report how far the
+ * attention kernels are from what the device can stream): allocates `bytes` (rounded down to 16)
+ * on `device`, reads them `iters` times with a plain streaming-read kernel, and returns the mean
+ * read rate in GB/s (HIP events around the launches). Synchronous; frees what it allocated. */
+int32_t lmh_bench_read_ceiling(int32_t device, uint64_t bytes, uint32_t iters, double* gbps);
+
 /* ---- request scheduler: the host side of the batch hand-off ----
  * Scheduler (crates/engine/sched/src/lib.rs:75-282) over the block pool, with Sequence
  * (kv/src/lib.rs:262-335) for admission. Each step takes every decoding slot's next token, then

@@ -138,6 +138,7 @@ SIGNATURES = {
     "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
     "lmh_kv_set_timing": (i32, [P, i32]),
     "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
+    "lmh_bench_read_ceiling": (i32, [i32, u64, u32, C.POINTER(C.c_double)]),
     "lmh_sched_create": (i32, [C.POINTER(SchedOptions), P, C.POINTER(P)]),
     "lmh_sched_destroy": (None, [P]),
     "lmh_sched_last_error": (C.c_char_p, [P]),

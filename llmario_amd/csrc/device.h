@@ -146,6 +146,8 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
                            uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s);
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s);
+// benchmark hook: one streaming read of `bytes` (a multiple of 16) at p
+hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.
 // The merge list of the call (src: staged, host-mapped; dst: device memory), copied by the decode
 // launch for the merge kernel that follows it (n_words = 0: nothing to copy).

@@ -1499,6 +1499,34 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   return kv->release_rows(slot, st);
 }
 
+int32_t lmh_bench_read_ceiling(int32_t device, uint64_t bytes, uint32_t iters, double* gbps) {
+  bytes &= ~15ull;
+  if (!gbps || bytes == 0 || iters == 0) return LMH_INVALID_ARGUMENT;
+  if (hipSetDevice(device) != hipSuccess) return LMH_DEVICE_ERROR;
+  uint8_t* p = nullptr;
+  uint32_t* sink = nullptr;
+  hipEvent_t a = nullptr, b = nullptr;
+  hipError_t e = hipMalloc((void**)&p, bytes);
+  if (e == hipSuccess) e = hipMalloc((void**)&sink, 16);
+  if (e == hipSuccess) e = hipMemset(p, 1, bytes);
+  if (e == hipSuccess) e = hipEventCreate(&a);
+  if (e == hipSuccess) e = hipEventCreate(&b);
+  for (uint32_t i = 0; e == hipSuccess && i < 3; i++) e = launch_read_ceiling(p, bytes, sink, nullptr);
+  if (e == hipSuccess) e = hipEventRecord(a, nullptr);
+  for (uint32_t i = 0; e == hipSuccess && i < iters; i++) e = launch_read_ceiling(p, bytes, sink, nullptr);
+  if (e == hipSuccess) e = hipEventRecord(b, nullptr);
+  if (e == hipSuccess) e = hipEventSynchronize(b);
+  float ms = 0.f;
+  if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+  if (a) (void)hipEventDestroy(a);
+  if (b) (void)hipEventDestroy(b);
+  if (sink) (void)hipFree(sink);
+  if (p) (void)hipFree(p);
+  if (e != hipSuccess) return e == hipErrorOutOfMemory ? LMH_OUT_OF_MEMORY : LMH_DEVICE_ERROR;
+  *gbps = (double)bytes * iters / (ms * 1e-3) / 1e9;
+  return LMH_OK;
+}
+
 int32_t lmh_kv_set_timing(lmh_kv* kv, int32_t enable) {
   if (!kv) return LMH_INVALID_ARGUMENT;
   kv->timing = enable != 0;

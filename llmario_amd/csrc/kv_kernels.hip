@@ -1109,6 +1109,22 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
   return hipGetLastError();
 }
 
+// Benchmark hook: every 16-byte word of a buffer read once (grid-stride, folded so the loads are
+// kept), the plain streaming read the decode kernel's bandwidth is compared with.
+__global__ __launch_bounds__(256) void read_ceiling_kernel(const uint4* __restrict__ p, uint64_t n, uint32_t* sink) {
+  uint32_t acc = 0;
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x) {
+    const uint4 v = p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;  // practically never: the loads are not dead code
+}
+
+hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s) {
+  hipLaunchKernelGGL(read_ceiling_kernel, dim3(4096), dim3(256), 0, s, (const uint4*)p, bytes / 16, sink);
+  return hipGetLastError();
+}
+
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s) {
   if (n == 0) return hipSuccess;
