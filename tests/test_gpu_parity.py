@@ -163,6 +163,11 @@ SMALL = [
     ("bf16", Layer(16, 1, 64, 64), [500], [45], 0, 64),
     ("f16", Layer(40, 8, 128, 128), [600, 20], [130, 1], 37, 16),
     ("bf16", Layer(32, 8, 128, 128), [1000], [260], 300, 16),
+    # prefill segments and decode rows in one call (one launch of the mixed kernel), each
+    # type / head size the prefill path takes
+    ("f16", Layer(16, 4, 64, 64), [700, 64], [20, 1], 0, 16),
+    ("bf16", Layer(32, 8, 128, 128), [1500, 10], [1, 40], 0, 16),
+    ("bf16", Layer(8, 2, 64, 64), [90, 3000, 0], [1, 1, 70], 500, 32),
 ]
 
 
