@@ -233,9 +233,11 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
-/* Timing hook for benchmarks: when enabled, lmh_attend, lmh_qk_rope_store and the snapshot calls bracket each kernel they launch with HIP
- * events on `stream`; lmh_kv_kernel_time returns the accumulated milliseconds and launch count of
- * one kernel kind since its last read, and resets them (it waits for the recorded events). */
+/* Timing hook for benchmarks: when enabled, lmh_attend times each kernel it launches with a HIP
+ * event pair that the kernel's own dispatch records (hipExtLaunchKernel: the kernel alone), and
+ * lmh_qk_rope_store and the snapshot calls bracket their kernels with HIP events on `stream`;
+ * lmh_kv_kernel_time returns the accumulated milliseconds and launch count of one kernel kind
+ * since its last read, and resets them (it waits for the recorded events). */
 #define LMH_KERNEL_DECODE 0u
 #define LMH_KERNEL_PREFILL 1u
 #define LMH_KERNEL_MERGE 2u
@@ -247,8 +249,9 @@ int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* la
 
 /* Benchmark hook (no counterpart in the reference; for benchmark drivers that report how far the
  * attention kernels are from what the device can stream): allocates `bytes` (rounded down to 16)
- * on `device`, reads them `iters` times with a plain streaming-read kernel, and returns the mean
- * read rate in GB/s (HIP events around the launches). Synchronous; frees what it allocated. */
+ * on `device`, reads them `iters` times with a plain streaming-read kernel, and returns the read
+ * rate in GB/s over the launches' summed durations (events recorded by each dispatch, as
+ * lmh_attend's kernels are timed). Synchronous; frees what it allocated. */
 int32_t lmh_bench_read_ceiling(int32_t device, uint64_t bytes, uint32_t iters, double* gbps);
 
 /* ---- request scheduler: the host side of the batch hand-off ----

@@ -287,22 +287,22 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
 
 template <int KVT, int HD, int HDV>
 hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                      const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s) {
+                      const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
   const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
   if constexpr (KVT == KV_F32) {
-    hipLaunchKernelGGL((decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
+    LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
   } else {
-    hipLaunchKernelGGL((decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
+    LMH_LAUNCH(ev, (decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
   }
   return hipGetLastError();
 }
 
 template <int KVT>
 hipError_t dispatch_hd(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s) {
-  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, mc, s);
-  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, mc, s);
-  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, mc, s);
+                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
+  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, mc, s, ev);
+  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, mc, s, ev);
+  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, mc, s, ev);
   return hipErrorInvalidValue;
 }
 
@@ -343,26 +343,27 @@ bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
 }
 
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s) {
+                         const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,
+                         const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
   switch (g.kv_type) {
-    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, mc, s);
-    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, mc, s);
-    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, mc, s);
-    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, mc, s);
+    case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, mc, s, ev);
+    case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, mc, s, ev);
+    case KV_Q8: return dispatch_hd<KV_Q8>(g, r, items, n_items, q, out, part, mc, s, ev);
+    case KV_F32: return dispatch_hd<KV_F32>(g, r, items, n_items, q, out, part, mc, s, ev);
   }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, hipStream_t s) {
+                        float* out, hipStream_t s, const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
   const uint32_t waves = n_items * r.ng;
   const dim3 grid((waves + 3) / 4), block(256);
   switch (hdv) {
-    case 64: hipLaunchKernelGGL(merge_kernel<64>, grid, block, 0, s, r, items, n_items, part, out); break;
-    case 128: hipLaunchKernelGGL(merge_kernel<128>, grid, block, 0, s, r, items, n_items, part, out); break;
-    case 256: hipLaunchKernelGGL(merge_kernel<256>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 64: LMH_LAUNCH(ev, merge_kernel<64>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 128: LMH_LAUNCH(ev, merge_kernel<128>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 256: LMH_LAUNCH(ev, merge_kernel<256>, grid, block, 0, s, r, items, n_items, part, out); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

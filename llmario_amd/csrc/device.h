@@ -23,6 +23,7 @@
 // (q8_0: 34 bytes per 32 values; f16/bf16: 2 bytes; f32: 4 bytes per value).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -125,6 +126,20 @@ struct RopeGeom {
 constexpr uint32_t ROPE_Q_NORM = 1, ROPE_K_NORM = 2, ROPE_V_NORM = 4, ROPE_APPLY = 8, ROPE_NEOX = 16;
 constexpr uint32_t ROPE_MAX_DIM = 512;  // largest hd / hdv the fused kernel stages per wave
 
+// Benchmark timing: a launch may carry a start / stop event pair that its own dispatch records
+// (hipExtLaunchKernel), so the measured interval is the kernel alone, without event packets queued
+// around it. Null events: an ordinary launch.
+struct LaunchEv {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+#define LMH_LAUNCH(ev, kernel, grid, block, lds, stream, ...)                                             \
+  do {                                                                                                    \
+    if ((ev).start)                                                                                       \
+      hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, (ev).start, (ev).stop, 0u, __VA_ARGS__);     \
+    else                                                                                                  \
+      hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                  \
+  } while (0)
+
 // Launch wrappers (defined in the .hip files). Return hipSuccess or the launch error.
 hipError_t launch_store_f32(const PageGeom& g, const int32_t* row_seq, const int32_t* row_pos, uint32_t n_rows,
                             const float* k, const float* v, hipStream_t s);
@@ -147,7 +162,7 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s);
 // benchmark hook: one streaming read of `bytes` (a multiple of 16) at p
-hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s);
+hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s, const LaunchEv& ev);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.
 // The merge list of the call (src: staged, host-mapped; dst: device memory), copied by the decode
 // launch for the merge kernel that follows it (n_words = 0: nothing to copy).
@@ -157,9 +172,10 @@ struct MergeCopy {
   uint32_t n_words;
 };
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
-                         const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s);
+                         const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,
+                         const LaunchEv& ev = {});
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, hipStream_t s);
+                        float* out, hipStream_t s, const LaunchEv& ev = {});
 // Decode work items (waves) one CU holds at once for a layer's decode kernel (occupancy query).
 uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
@@ -167,14 +183,15 @@ bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 // Prefill (multi-token segments on matrix cores): n_wg workgroups, workgroup b runs the units
 // items[b * per_wg ..] up to the first with n_tok == 0. `max_pages` bounds the key pages of any unit.
 hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
-                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s);
+                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s,
+                          const LaunchEv& ev = {});
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group);
 // A call holding both prefill units and decode items, in one launch (any type and head size
 // prefill_supported accepts): pf_wg prefill workgroups, then the decode items eight per workgroup.
 hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
                         uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
                         uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
-                        hipStream_t s);
+                        hipStream_t s, const LaunchEv& ev = {});
 uint32_t prefill_cols_per_unit();
 size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg);
 

@@ -577,6 +577,25 @@ struct lmh_kv {
     ev_kind[ev_used] = kind;
     return hipEventRecord(evs[ev_used].first, st);
   }
+  // The same pair for a launch that records it itself (LaunchEv: start and stop are stamped by the
+  // kernel's dispatch), so the interval is the kernel alone. Empty when timing is off.
+  hipError_t time_launch(uint32_t kind, LaunchEv& ev) {
+    ev = LaunchEv{};
+    if (!timing) return hipSuccess;
+    if (ev_used == evs.size()) {
+      hipEvent_t a, b;
+      hipError_t e = hipEventCreate(&a);
+      if (e == hipSuccess) e = hipEventCreate(&b);
+      if (e != hipSuccess) return e;
+      evs.push_back({a, b});
+      ev_kind.push_back(0);
+    }
+    ev_kind[ev_used] = kind;
+    ev.start = evs[ev_used].first;
+    ev.stop = evs[ev_used].second;
+    ev_used++;
+    return hipSuccess;
+  }
   hipError_t time_end(hipStream_t st) {
     if (!timing) return hipSuccess;
     hipError_t e = hipEventRecord(evs[ev_used].second, st);
@@ -1468,33 +1487,31 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   // A mixed batch (prefill units and decode items) runs as one launch: the prefill workgroups
   // first (one per CU they reach), then the decode items, a wave each, on the CUs left free.
   const bool overlap = !kv->pitems.empty() && !kv->items.empty();
+  LaunchEv ev;
   if (overlap) {
-    if ((e = kv->time_begin(st, LMH_KERNEL_MIXED)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = kv->time_launch(LMH_KERNEL_MIXED, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_mixed(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, r,
-                     (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st);
+                     (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "mixed kernel");
-    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   if (!overlap && !kv->pitems.empty()) {
-    if ((e = kv->time_begin(st, LMH_KERNEL_PREFILL)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = kv->time_launch(LMH_KERNEL_PREFILL, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_prefill(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, q, out,
-                       st);
+                       st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
-    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   if (kv->items.empty()) return kv->release_rows(slot, st);
   if (!overlap) {
-    if ((e = kv->time_begin(st, LMH_KERNEL_DECODE)) != hipSuccess) return kv->hip_fail(e, "event");
-    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st);
+    if ((e = kv->time_launch(LMH_KERNEL_DECODE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
+    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st,
+                      ev);
     if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
-    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   if (!kv->merges.empty()) {
-    if ((e = kv->time_begin(st, LMH_KERNEL_MERGE)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = kv->time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_merge(r, y.hdv, (const MergeItem*)kv->merge_buf.p, (uint32_t)kv->merges.size(),
-                     (const float*)kv->part_buf.p, out, st);
+                     (const float*)kv->part_buf.p, out, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
-    if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   }
   return kv->release_rows(slot, st);
 }
@@ -1505,25 +1522,28 @@ int32_t lmh_bench_read_ceiling(int32_t device, uint64_t bytes, uint32_t iters, d
   if (hipSetDevice(device) != hipSuccess) return LMH_DEVICE_ERROR;
   uint8_t* p = nullptr;
   uint32_t* sink = nullptr;
-  hipEvent_t a = nullptr, b = nullptr;
+  LaunchEv ev;
   hipError_t e = hipMalloc((void**)&p, bytes);
   if (e == hipSuccess) e = hipMalloc((void**)&sink, 16);
   if (e == hipSuccess) e = hipMemset(p, 1, bytes);
-  if (e == hipSuccess) e = hipEventCreate(&a);
-  if (e == hipSuccess) e = hipEventCreate(&b);
-  for (uint32_t i = 0; e == hipSuccess && i < 3; i++) e = launch_read_ceiling(p, bytes, sink, nullptr);
-  if (e == hipSuccess) e = hipEventRecord(a, nullptr);
-  for (uint32_t i = 0; e == hipSuccess && i < iters; i++) e = launch_read_ceiling(p, bytes, sink, nullptr);
-  if (e == hipSuccess) e = hipEventRecord(b, nullptr);
-  if (e == hipSuccess) e = hipEventSynchronize(b);
-  float ms = 0.f;
-  if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
-  if (a) (void)hipEventDestroy(a);
-  if (b) (void)hipEventDestroy(b);
+  if (e == hipSuccess) e = hipEventCreate(&ev.start);
+  if (e == hipSuccess) e = hipEventCreate(&ev.stop);
+  for (uint32_t i = 0; e == hipSuccess && i < 3; i++) e = launch_read_ceiling(p, bytes, sink, nullptr, LaunchEv{});
+  // each launch timed by events its own dispatch records, as the attention kernels are timed
+  double total_ms = 0.0;
+  for (uint32_t i = 0; e == hipSuccess && i < iters; i++) {
+    e = launch_read_ceiling(p, bytes, sink, nullptr, ev);
+    if (e == hipSuccess) e = hipEventSynchronize(ev.stop);
+    float ms = 0.f;
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, ev.start, ev.stop);
+    total_ms += ms;
+  }
+  if (ev.start) (void)hipEventDestroy(ev.start);
+  if (ev.stop) (void)hipEventDestroy(ev.stop);
   if (sink) (void)hipFree(sink);
   if (p) (void)hipFree(p);
   if (e != hipSuccess) return e == hipErrorOutOfMemory ? LMH_OUT_OF_MEMORY : LMH_DEVICE_ERROR;
-  *gbps = (double)bytes * iters / (ms * 1e-3) / 1e9;
+  *gbps = (double)bytes * iters / (total_ms * 1e-3) / 1e9;
   return LMH_OK;
 }
 

@@ -1120,8 +1120,8 @@ __global__ __launch_bounds__(256) void read_ceiling_kernel(const uint4* __restri
   if (acc == 0x9e3779b9u) sink[0] = acc;  // practically never: the loads are not dead code
 }
 
-hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s) {
-  hipLaunchKernelGGL(read_ceiling_kernel, dim3(4096), dim3(256), 0, s, (const uint4*)p, bytes / 16, sink);
+hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s, const LaunchEv& ev) {
+  LMH_LAUNCH(ev, read_ceiling_kernel, dim3(4096), dim3(256), 0, s, (const uint4*)p, bytes / 16, sink);
   return hipGetLastError();
 }
 

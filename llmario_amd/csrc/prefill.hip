@@ -515,9 +515,9 @@ void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_
 
 template <int KVT, int HD>
 hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
-                    uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s) {
-  const size_t lds = prefill_lds_bytes(HD, max_pages, per_wg);
-  hipLaunchKernelGGL((prefill_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+                    uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s, const LaunchEv& ev) {
+  const uint32_t lds = (uint32_t)prefill_lds_bytes(HD, max_pages, per_wg);
+  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
   return hipGetLastError();
 }
 
@@ -525,11 +525,11 @@ template <int KVT, int HD>
 hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
                           uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
                           uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
-                          hipStream_t s) {
-  const size_t lds = prefill_lds_bytes(HD, max_pages, per_wg);
+                          hipStream_t s, const LaunchEv& ev) {
+  const uint32_t lds = (uint32_t)prefill_lds_bytes(HD, max_pages, per_wg);
   const uint32_t n_wg = pf_wg + (n_items + PW - 1) / PW;
-  hipLaunchKernelGGL((mixed_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r, items,
-                     n_items, q, out, part, mc);
+  LMH_LAUNCH(ev, (mixed_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r, items,
+             n_items, q, out, part, mc);
   return hipGetLastError();
 }
 
@@ -549,25 +549,26 @@ bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t gro
 hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
                         uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
                         uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
-                        hipStream_t s) {
+                        hipStream_t s, const LaunchEv& ev) {
   if (pf_wg == 0 || per_wg == 0 || n_items == 0 || g.hd != g.hdv) return hipErrorInvalidValue;
 #define LMH_MIXED(T, D)                                                                                          \
   if (g.kv_type == T && g.hd == D)                                                                               \
-    return launch_mixed_t<T, D>(g, pg, pitems, pf_wg, per_wg, max_pages, r, items, n_items, q, out, part, mc, s);
+    return launch_mixed_t<T, D>(g, pg, pitems, pf_wg, per_wg, max_pages, r, items, n_items, q, out, part, mc, s, ev);
   LMH_MIXED(KV_F16, 128) LMH_MIXED(KV_F16, 64) LMH_MIXED(KV_BF16, 128) LMH_MIXED(KV_BF16, 64)
 #undef LMH_MIXED
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
-                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s) {
+                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s,
+                          const LaunchEv& ev) {
   if (n_wg == 0 || per_wg == 0) return hipSuccess;
   if (g.kv_type == KV_BF16) {
-    if (g.hd == 128) return launch_t<KV_BF16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
-    if (g.hd == 64) return launch_t<KV_BF16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
+    if (g.hd == 128) return launch_t<KV_BF16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+    if (g.hd == 64) return launch_t<KV_BF16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
   } else if (g.kv_type == KV_F16) {
-    if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
-    if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s);
+    if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+    if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
   }
   return hipErrorInvalidValue;
 }
