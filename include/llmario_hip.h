@@ -233,9 +233,9 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
-/* Timing hook for benchmarks: when enabled, lmh_attend times each kernel it launches with a HIP
- * event pair that the kernel's own dispatch records (hipExtLaunchKernel: the kernel alone), and
- * lmh_qk_rope_store and the snapshot calls bracket their kernels with HIP events on `stream`;
+/* Timing hook for benchmarks: when enabled, lmh_attend and lmh_qk_rope_store time each kernel
+ * they launch with a HIP event pair that the kernel's own dispatch records (hipExtLaunchKernel: the
+ * kernel alone), and the snapshot calls bracket their kernels with HIP events on `stream`;
  * lmh_kv_kernel_time returns the accumulated milliseconds and launch count of one kernel kind
  * since its last read, and resets them (it waits for the recorded events). */
 #define LMH_KERNEL_DECODE 0u

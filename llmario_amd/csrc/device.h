@@ -154,7 +154,7 @@ hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, cons
 hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int32_t* row_seq, const int32_t* row_pos,
                                 uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
                                 const int32_t* quads, uint32_t n_quads, const int32_t* rest, uint32_t n_rest,
-                                hipStream_t s);
+                                hipStream_t s, const LaunchEv& ev = {});
 // One layer's share of a sequence's snapshot (write: pages -> reference block format; read: the
 // reverse), positions 0 .. n_pos-1.
 hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t n_pos, uint32_t bt, uint64_t bb,

@@ -1320,11 +1320,11 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
              (p->flags & LMH_ROPE_Q_NORM) ? p->q_norm : nullptr, (p->flags & LMH_ROPE_K_NORM) ? p->k_norm : nullptr,
              apply ? p->freq_div : nullptr, (const float*)ex};
   hipError_t e;
-  if ((e = kv->time_begin(st, LMH_KERNEL_ROPE_STORE)) != hipSuccess) return kv->hip_fail(e, "event");
+  LaunchEv ev;
+  if ((e = kv->time_launch(LMH_KERNEL_ROPE_STORE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
   e = launch_qk_rope_store(kv->geom(layer), r, rs, rp, (uint32_t)n_rows, q_in, k_in, v_in, q_out, d_lists, n_quads,
-                           d_lists + n_quads, (uint32_t)(lists.size() - n_quads), st);
+                           d_lists + n_quads, (uint32_t)(lists.size() - n_quads), st, ev);
   if (e != hipSuccess) return kv->hip_fail(e, "kernel launch");
-  if ((e = kv->time_end(st)) != hipSuccess) return kv->hip_fail(e, "event");
   return kv->release_rows(slot, st);
 }
 

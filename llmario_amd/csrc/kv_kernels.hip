@@ -1014,7 +1014,7 @@ hipError_t launch_gather_encoded(const PageGeom& g, const int32_t* row_seq, cons
 hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int32_t* row_seq, const int32_t* row_pos,
                                 uint32_t n_rows, const float* q, const float* k, const float* v, float* q_out,
                                 const int32_t* quads, uint32_t n_quads, const int32_t* rest, uint32_t n_rest,
-                                hipStream_t s) {
+                                hipStream_t s, const LaunchEv& ev) {
   if (n_rows == 0) return hipSuccess;
   // register path: hd == hdv = 64*VPL; Normal pairs are always in-lane (VPL >= 2) or one lane
   // apart; Neox partners are half_rot/VPL lanes apart, which must be a whole power of two
@@ -1041,8 +1041,8 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
       const uint32_t ipw = ((n_items + split - 1) / split + 3) & ~3u;
       const dim3 grid(n_wg, (n_items + ipw - 1) / ipw);
 #define LMH_QUAD(V)                                                                                            \
-  hipLaunchKernelGGL(qk_rope_store_quad_kernel<V>, grid, dim3(256), 0, s, g, r, quads, n_quads, rest, row_seq, \
-                     row_pos, q, k, v, q_out, ipw)
+  LMH_LAUNCH(ev, qk_rope_store_quad_kernel<V>, grid, dim3(256), 0, s, g, r, quads, n_quads, rest, row_seq, row_pos, \
+             q, k, v, q_out, ipw)
       switch (vpl) {
         case 1: LMH_QUAD(1); break;
         case 2: LMH_QUAD(2); break;
@@ -1053,13 +1053,13 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
       return hipGetLastError();
     }
     switch (vpl) {
-      case 1: hipLaunchKernelGGL(qk_rope_store_reg_kernel<1>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      case 2: hipLaunchKernelGGL(qk_rope_store_reg_kernel<2>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      case 4: hipLaunchKernelGGL(qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      default: hipLaunchKernelGGL(qk_rope_store_reg_kernel<8>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 1: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<1>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 2: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<2>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      case 4: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      default: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<8>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
     }
   } else {
-    hipLaunchKernelGGL(qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
+    LMH_LAUNCH(ev, qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);
   }
   return hipGetLastError();
 }
