@@ -54,3 +54,12 @@ def test_create_rejects_bad_options_without_touching_the_device():
     o.kv_type = N.KV_Q8_0
     layer[0] = N.LayerDesc(8, 8, 48, 48)
     assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.INVALID_ARGUMENT  # kv.rs:103-109
+
+
+def test_read_ceiling_hook_rejects_bad_arguments_without_touching_the_device():
+    g = ctypes.c_double()
+    lib = N.lib()
+    assert lib.lmh_bench_read_ceiling(0, 0, 10, ctypes.byref(g)) == N.INVALID_ARGUMENT        # no bytes
+    assert lib.lmh_bench_read_ceiling(0, 15, 10, ctypes.byref(g)) == N.INVALID_ARGUMENT       # under 16 bytes
+    assert lib.lmh_bench_read_ceiling(0, 1 << 20, 0, ctypes.byref(g)) == N.INVALID_ARGUMENT   # no launches
+    assert lib.lmh_bench_read_ceiling(0, 1 << 20, 10, None) == N.INVALID_ARGUMENT             # no result slot
