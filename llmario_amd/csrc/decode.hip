@@ -46,7 +46,9 @@ constexpr int waves_per_eu() {
 // Split-K merge (forward.rs:772-806), one wave per (task, query head), lanes over dims:
 // m* = max m_s, out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m in the log2 domain.
 // A separate launch: the kernel boundary makes every split's partials visible across XCDs.
-template <int HDV>
+// GROUPS: some item has more than 16 splits (rows past the first 16 are loaded in groups of 16;
+// without it the kernel keeps the lighter code that a call with at most 16 splits per item runs).
+template <int HDV, bool GROUPS>
 __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* items, uint32_t n_items,
                                                     const float* part, float* out) {
   constexpr int ND = (HDV + 63) / 64;
@@ -66,7 +68,7 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
   float M = -INFINITY, L = 0.f;
   // Up to 64 splits per round: lane s holds split s's (m, l); every lane then folds all of the
   // round's partial rows into its NP dims. The first 16 rows are loaded together with (m, l), so
-  // a merge of up to 16 splits costs one memory round trip.
+  // a merge of up to 16 splits costs one memory round trip; later rows follow in groups of 16.
   for (uint32_t s0 = 0; s0 < mi.n_split; s0 += 64) {
     const uint32_t s = s0 + lane;
     const uint32_t n = (mi.n_split - s0) < 64u ? (mi.n_split - s0) : 64u;
@@ -94,17 +96,40 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
 #pragma unroll
     for (int i = 0; i < NP; i++) acc[i] *= rescale;
     M = Mn;
+    if constexpr (!GROUPS) {
 #pragma unroll
-    for (int k = 0; k < 16; k++) {
-      const float ck = (uint32_t)k < n ? __shfl(c, k) : 0.f;
+      for (int k = 0; k < 16; k++) {
+        const float ck = (uint32_t)k < n ? __shfl(c, k) : 0.f;
 #pragma unroll
-      for (int i = 0; i < NP; i++) acc[i] += ck * pre[k][i];
+        for (int i = 0; i < NP; i++) acc[i] += ck * pre[k][i];
+      }
+      continue;
     }
-    for (uint32_t k = 16; k < n; k++) {
-      const float ck = __shfl(c, (int)k);
-      const float* pp = base + (s0 + k) * stride + lane * NP;
+    // rows in groups of 16, each group's loads issued together and one group ahead of its sums
+    // (a split count of 17..64 costs one round trip per group, not one per row)
+    for (uint32_t k0 = 0; k0 < n; k0 += 16) {
+      float nxt[16][NP];
+      if (k0 + 16 < n) {
 #pragma unroll
-      for (int i = 0; i < NP; i++) acc[i] += ck * pp[i];
+        for (int k = 0; k < 16; k++) {
+          const uint32_t row = k0 + 16 + k < n ? k0 + 16 + k : k0 + 16;
+          const float* pp = base + (s0 + row) * stride + lane * NP;
+#pragma unroll
+          for (int i = 0; i < NP; i++) nxt[k][i] = pp[i];
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        const float ck = k0 + k < n ? __shfl(c, (int)(k0 + k)) : 0.f;
+#pragma unroll
+        for (int i = 0; i < NP; i++) acc[i] += ck * pre[k][i];
+      }
+      if (k0 + 16 < n) {
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+#pragma unroll
+          for (int i = 0; i < NP; i++) pre[k][i] = nxt[k][i];
+      }
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
@@ -356,14 +381,23 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
 }
 
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, hipStream_t s, const LaunchEv& ev) {
+                        float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
   const uint32_t waves = n_items * r.ng;
   const dim3 grid((waves + 3) / 4), block(256);
   switch (hdv) {
-    case 64: LMH_LAUNCH(ev, merge_kernel<64>, grid, block, 0, s, r, items, n_items, part, out); break;
-    case 128: LMH_LAUNCH(ev, merge_kernel<128>, grid, block, 0, s, r, items, n_items, part, out); break;
-    case 256: LMH_LAUNCH(ev, merge_kernel<256>, grid, block, 0, s, r, items, n_items, part, out); break;
+    case 64:
+      if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<64, true>), grid, block, 0, s, r, items, n_items, part, out);
+      else LMH_LAUNCH(ev, (merge_kernel<64, false>), grid, block, 0, s, r, items, n_items, part, out);
+      break;
+    case 128:
+      if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<128, true>), grid, block, 0, s, r, items, n_items, part, out);
+      else LMH_LAUNCH(ev, (merge_kernel<128, false>), grid, block, 0, s, r, items, n_items, part, out);
+      break;
+    case 256:
+      if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<256, true>), grid, block, 0, s, r, items, n_items, part, out);
+      else LMH_LAUNCH(ev, (merge_kernel<256, false>), grid, block, 0, s, r, items, n_items, part, out);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

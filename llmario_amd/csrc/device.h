@@ -174,8 +174,9 @@ struct MergeCopy {
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
                          const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,
                          const LaunchEv& ev = {});
+// max_split: the largest n_split of the items (over 16: rows loaded in groups of 16)
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, hipStream_t s, const LaunchEv& ev = {});
+                        float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev = {});
 // Decode work items (waves) one CU holds at once for a layer's decode kernel (occupancy query).
 uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);

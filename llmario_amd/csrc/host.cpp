@@ -1509,8 +1509,10 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   }
   if (!kv->merges.empty()) {
     if ((e = kv->time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
+    uint32_t max_split = 0;
+    for (const MergeItem& m : kv->merges) max_split = std::max(max_split, m.n_split);
     e = launch_merge(r, y.hdv, (const MergeItem*)kv->merge_buf.p, (uint32_t)kv->merges.size(),
-                     (const float*)kv->part_buf.p, out, st, ev);
+                     (const float*)kv->part_buf.p, out, max_split, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
   }
   return kv->release_rows(slot, st);
