@@ -161,6 +161,8 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
                            uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s);
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s);
+// n words from src (host-mapped staging memory) to dst (device memory), as a kernel on s
+hipError_t launch_copy_words(uint32_t* dst, const uint32_t* src, uint64_t n, hipStream_t s);
 // benchmark hook: one streaming read of `bytes` (a multiple of 16) at p
 hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink, hipStream_t s, const LaunchEv& ev);
 // Returns hipErrorInvalidValue for a (type, hd, hdv) with no kernel instance.

@@ -141,8 +141,11 @@ struct Uploader {  // ring of pinned, device-mapped staging slots, reused once t
     used[idx] = e == hipSuccess;
     return e;
   }
+  // The slot's first `bytes` (a multiple of 4) to device memory, copied by a kernel on `s` that
+  // reads the mapped slot (a host-to-device copy would run on the copy engine, and the stream's
+  // next kernel would wait for its completion signal).
   hipError_t send(int idx, void* dst, size_t bytes, hipStream_t s) {
-    hipError_t e = hipMemcpyAsync(dst, host[idx], bytes, hipMemcpyHostToDevice, s);
+    hipError_t e = launch_copy_words((uint32_t*)dst, (const uint32_t*)dev[idx], bytes / 4, s);
     if (e != hipSuccess) return e;
     return mark(idx, s);
   }
@@ -213,7 +216,7 @@ struct lmh_kv {
   DirtyRows table_rows;
   std::vector<PageOp> pending;
   Uploader up;
-  DevBuf part_buf, ops_buf, merge_buf;
+  DevBuf part_buf, merge_buf;
   // ---- per-call host scratch
   std::vector<int32_t> row_seq, row_pos;
   std::vector<DecodeItem> items;
@@ -439,11 +442,11 @@ struct lmh_kv {
         uint8_t* h;
         if ((e = up.acquire(zb.size() * 4, idx, h)) != hipSuccess) return hip_fail(e, "staging");
         std::memcpy(h, zb.data(), zb.size() * 4);
-        if ((e = ops_buf.ensure(zb.size() * 4)) != hipSuccess) return hip_fail(e, "hipMalloc");
-        if ((e = up.send(idx, ops_buf.p, zb.size() * 4, st)) != hipSuccess) return hip_fail(e, "upload");
-        if ((e = launch_zero_blocks(w ? d_wpool : d_pool, w ? wblock_bytes : block_bytes, (const int32_t*)ops_buf.p,
+        // the zero kernel reads the block ids from the mapped staging slot
+        if ((e = launch_zero_blocks(w ? d_wpool : d_pool, w ? wblock_bytes : block_bytes, (const int32_t*)up.dev[idx],
                                     (uint32_t)zb.size(), st)) != hipSuccess)
           return hip_fail(e, "zero kernel");
+        if ((e = up.mark(idx, st)) != hipSuccess) return hip_fail(e, "event");
         i = j;
       } else {
         e = hipMemcpyAsync(d_pool + (size_t)pending[i].dst * block_bytes,

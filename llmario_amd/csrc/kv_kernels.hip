@@ -1125,6 +1125,22 @@ hipError_t launch_read_ceiling(const uint8_t* p, uint64_t bytes, uint32_t* sink,
   return hipGetLastError();
 }
 
+// Words from host-mapped staging memory into device memory (block-table rows): a kernel on the
+// caller's stream, where a host-to-device copy would go to the copy engine and make the stream's
+// next kernel wait for its completion signal.
+__global__ __launch_bounds__(256) void copy_words_kernel(uint32_t* __restrict__ dst, const uint32_t* __restrict__ src,
+                                                         uint64_t n) {
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    dst[i] = src[i];
+}
+
+hipError_t launch_copy_words(uint32_t* dst, const uint32_t* src, uint64_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  const uint64_t wg = (n + 255) / 256;
+  hipLaunchKernelGGL(copy_words_kernel, dim3((uint32_t)(wg < 1024 ? wg : 1024)), dim3(256), 0, s, dst, src, n);
+  return hipGetLastError();
+}
+
 hipError_t launch_zero_blocks(uint8_t* pool, uint64_t block_bytes, const int32_t* blocks, uint32_t n,
                               hipStream_t s) {
   if (n == 0) return hipSuccess;
