@@ -65,6 +65,8 @@ class Step:  # sched/src/lib.rs:48-55
     decodes: list = field(default_factory=list)
     prefills: list = field(default_factory=list)  # (slot, start, end)
     tokens: int = 0
+    # the C struct next_step filled, reused by prepare / complete while the lists are unchanged
+    _packed: object = field(default=None, repr=False, compare=False)
 
 
 @dataclass(frozen=True)
@@ -183,11 +185,22 @@ class Scheduler:
     def next_step(self) -> Step:
         st = self._step_struct()
         self._check(N.lib().lmh_sched_next_step(self.h, C.byref(st)), "next_step")
-        return Step([self._dec[i] for i in range(st.n_decodes)],
-                    [(self._pre[i].slot, self._pre[i].start, self._pre[i].end) for i in range(st.n_prefills)],
+        nd, np_ = st.n_decodes, st.n_prefills
+        step = Step(self._dec[:nd], [(self._pre[i].slot, self._pre[i].start, self._pre[i].end) for i in range(np_)],
                     st.tokens)
+        dec = (C.c_uint32 * max(nd, 1))()
+        pre = (N.PrefillRange * max(np_, 1))()
+        C.memmove(dec, self._dec, nd * C.sizeof(C.c_uint32))
+        C.memmove(pre, self._pre, np_ * C.sizeof(N.PrefillRange))
+        packed = N.Step(decodes=dec, n_decodes=nd, prefills=pre, n_prefills=np_, tokens=st.tokens)
+        step._packed = (packed, (dec, pre), (tuple(step.decodes), tuple(step.prefills), step.tokens))
+        return step
 
     def _pack(self, step: Step):
+        if step._packed is not None:
+            packed, keep, sig = step._packed
+            if sig == (tuple(step.decodes), tuple(step.prefills), step.tokens):
+                return packed, keep
         dec = (C.c_uint32 * max(len(step.decodes), 1))(*step.decodes)
         pre = (N.PrefillRange * max(len(step.prefills), 1))(*[N.PrefillRange(s, 0, a, b) for s, a, b in step.prefills])
         return N.Step(decodes=dec, n_decodes=len(step.decodes), prefills=pre, n_prefills=len(step.prefills),
