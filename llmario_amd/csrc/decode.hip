@@ -148,11 +148,13 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
 }
 
 // ---- f32 pages: VALU path ----------------------------------------------------------------------
-template <int HD, int HDV>
+// NG: query heads per item (the launch's ng when the group is 1, 2, 4 or 8; 16 otherwise, with a
+// run-time guard for a last head block shorter than 16), so the per-head loops carry no guards
+// for the common group sizes.
+template <int HD, int HDV, int NG>
 __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
                                                                 uint32_t n_items, const float* q, float* out,
                                                                 float* part, MergeCopy mc) {
-  constexpr int NG = 16;
   constexpr int ND = HDV / 64 > 0 ? HDV / 64 : 1;  // dims per lane in P.V
   __shared__ float qs[WAVES][NG][HD];
   __shared__ float ps[WAVES][NG][64];
@@ -162,7 +164,8 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
   const bool active = wi < n_items;
   DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, 0, 0};
   const uint32_t ng = r.ng;
-  const uint32_t nh = (it.h0 + ng <= r.group) ? ng : r.group - it.h0;
+  // heads of this item; NG < 16 only when it equals the group size, so every item has NG heads
+  const uint32_t nh = NG < 16 ? (uint32_t)NG : (it.h0 + ng <= r.group) ? ng : r.group - it.h0;
   if (active) {
     for (uint32_t e = lane; e < nh * HD; e += 64) {
       const uint32_t h = e / HD, d = e % HD;
@@ -315,7 +318,13 @@ hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* ite
                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
   const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
   if constexpr (KVT == KV_F32) {
-    LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
+    switch (r.group) {
+      case 1: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 1>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
+      case 2: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 2>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
+      case 4: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 4>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
+      case 8: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 8>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
+      default: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 16>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
+    }
   } else {
     LMH_LAUNCH(ev, (decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
   }
@@ -339,7 +348,7 @@ uint32_t resident_t() {
   int blocks = 0;
   hipError_t e;
   if constexpr (KVT == KV_F32)
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HD>, 64 * WAVES, 0);
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HD, 16>, 64 * WAVES, 0);
   else
     e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_mfma_kernel<KVT, HD, HD>, 64 * WAVES, 0);
   return (e == hipSuccess && blocks > 0) ? (uint32_t)blocks * WAVES : WAVES;
