@@ -3,16 +3,22 @@
 Headline (the driver's JSON line): BASELINE.json's metric on configs[1], GQA paged decode
 (32 sequences x 1 token, 32 Q / 8 KV heads, hd 128, f16 KV, contexts U[512, 4096], 16-token
 pages): decode KV-read GB/s. One step = one `lmh_attend` call over the whole batch (host
-hand-off + kernels), inputs already resident in HBM. `value` = algorithmic bytes per step /
-wall time per step, from a timed run without per-kernel events; `roofline` = the decode kernel's
-algorithmic bytes / its average duration from HIP events recorded around every launch on the
-launch stream during a second timed run of the same steps.
+hand-off + kernels), inputs already resident in HBM. The cache holds 5 layers of that geometry
+(1.5 GB of K/V) and step i attends layer i % 5, as an engine's layer loop does, so every step
+reads its pages from HBM rather than from the last-level cache. `value` = algorithmic bytes per
+step / wall time per step, from a timed run without per-kernel events; `roofline` = the decode
+kernel's algorithmic bytes / its average duration from HIP events recorded by each launch's
+dispatch during a second timed run of the same steps. The one-layer variant (every step re-reads
+the same 297 MB) is reported beside it as `c2_warm`.
 
-Also reported (extra keys): every other configuration's throughput and roofline fraction, the
+Also reported (extra keys, each in isolation: a failing leg is recorded under `errors` and the
+headline line still prints): every other configuration's throughput and its launch roofline
+(max(bytes / HBM peak, FLOPs / MFMA peak) against the kernel time, with the decode and prefill
+parts of a mixed launch), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
 of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), c5w
-with its layer in the sliding-window pool (`window_c5w`), and the CPU baseline
-(the C++ restatement of the reference's CPU attention, oracle/, on host cores).
+with its layer in the sliding-window pool (`window_c5w`), and the CPU baseline (the C++
+restatement of the reference's CPU attention, oracle/, on the host's cores and on one thread).
 """
 
 from __future__ import annotations
@@ -33,6 +39,7 @@ HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 FP32_PEAK_TFLOPS = 157.3
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
+COLD_LAYERS = 5   # c2_cold: 5 x 297 MB of K/V in rotation
 
 
 def log(*a):
@@ -50,10 +57,15 @@ def read_ceiling(nbytes: int, iters: int = 50) -> float:
     return gbs.value
 
 
-def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, warmup_s: float = 0.0):
+def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, warmup_s: float = 0.0,
+                n_layers: int = 1, tuning: dict | None = None, label: str | None = None):
     """Time `steps` calls of one configuration after at least `warmup` untimed calls and at least
     `warmup_s` seconds of them (matrix-core work runs at a lower clock for the first tens of
-    milliseconds of load, so the compute-bound configurations are warmed by time)."""
+    milliseconds of load, so the compute-bound configurations are warmed by time).
+    n_layers > 1: the cache holds that many layers of the configuration (same rows in each) and
+    step i attends layer i % n_layers, so each step reads K/V last touched n_layers - 1 steps
+    earlier (an engine's layer loop): with n_layers x the K/V bytes well above the device's
+    last-level cache, every step's pages come from HBM. tuning: lmh_kv_set_tuning options."""
     import torch
 
     from llmario_amd import harness
@@ -63,22 +75,25 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
     w = config(name)
     t_load = time.perf_counter()
     gen = Generator(w)
-    hc = harness.load(w, gen)
+    hc = harness.load(w, gen, n_layers=n_layers)
+    if tuning:
+        hc.set_tuning(**tuning)
     L = w.layer
     q = torch.from_numpy(gen.q()).cuda()
     out = torch.empty((w.n_rows, L.n_head, L.hdv), device="cuda")
     segs = Segments(w.segments())
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
+    label = label or name
     t_w = time.perf_counter()
     n_w = 0
     while n_w < warmup or time.perf_counter() - t_w < warmup_s:
-        hc.attend(0, segs, q, out, w.scale, w.window, sp)
+        hc.attend(n_w % n_layers, segs, q, out, w.scale, w.window, sp)
         n_w += 1
         if n_w % 16 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
-    log(f"[bench] {name}: loaded in {t_w - t_load:.1f}s; warmup {n_w} calls in {time.perf_counter() - t_w:.3f}s")
+    log(f"[bench] {label}: loaded in {t_w - t_load:.1f}s; warmup {n_w} calls in {time.perf_counter() - t_w:.3f}s")
 
     def timed(kernel_events: bool):
         """`steps` back-to-back calls between two synchronisations; the step time is the larger of
@@ -89,8 +104,8 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         ev0.record(stream)
-        for _ in range(steps):
-            hc.attend(0, segs, q, out, w.scale, w.window, sp)
+        for i in range(steps):
+            hc.attend(i % n_layers, segs, q, out, w.scale, w.window, sp)
         ev1.record(stream)
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
@@ -108,7 +123,8 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
     main = "mixed" if per_kind["mixed"] > 0 else "prefill" if per_kind["prefill"] > 0 else "decode"
     k_avg = per_kind[main]
     res = {
-        "config": name, "kv_type": w.kv_type, "rows": w.n_rows, "ms_per_step": ms_step,
+        "config": label, "kv_type": w.kv_type, "rows": w.n_rows, "layers_in_rotation": n_layers,
+        "tuning": hc.tuning(), "ms_per_step": ms_step,
         "ms_per_step_with_kernel_events": ms_step_ev,
         "kernel": main, "kernel_ms": k_avg, "decode_ms": per_kind["decode"], "prefill_ms": per_kind["prefill"],
         "mixed_ms": per_kind["mixed"], "merge_ms": per_kind["merge"], "bytes": w.algorithmic_bytes(),
@@ -118,12 +134,28 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
     res["TFLOPs"] = res["flops"] / (ms_step * 1e-3) / 1e12
     res["kernel_GBps"] = res["bytes"] / (k_avg * 1e-3) / 1e9
     res["kernel_TFLOPs"] = res["flops"] / (k_avg * 1e-3) / 1e12
+    # the kernel against its own roofline: t_roof = max(bytes / HBM peak, FLOPs / MFMA peak) for
+    # the whole launch; a mixed launch also reports each part's share of that bound
+    parts = w.parts()
+    t_b = res["bytes"] / (HBM_PEAK_GBS * 1e9)
+    t_f = res["flops"] / (MFMA_BF16_PEAK_TFLOPS * 1e12)
+    t_roof = max(t_b, t_f)
+    res["roofline"] = {
+        "bound": "hbm" if t_b >= t_f else "mfma", "t_roof_us": t_roof * 1e6, "kernel_us": k_avg * 1e3,
+        "frac": t_roof / (k_avg * 1e-3),
+        "decode_part": {"bytes": parts["decode_bytes"], "flops": parts["decode_flops"],
+                        "t_hbm_us": parts["decode_bytes"] / (HBM_PEAK_GBS * 1e9) * 1e6},
+        "prefill_part": {"bytes": parts["prefill_bytes"], "flops": parts["prefill_flops"],
+                         "t_mfma_us": parts["prefill_flops"] / (MFMA_BF16_PEAK_TFLOPS * 1e12) * 1e6},
+    }
     res["hbm_frac"] = res["kernel_GBps"] / HBM_PEAK_GBS
     res["mfma_frac"] = res["kernel_TFLOPs"] / MFMA_BF16_PEAK_TFLOPS
     del hc
     torch.cuda.empty_cache()
-    log(f"[bench] {name}: {ms_step * 1e3:.1f} us/step, kernel {k_avg * 1e3:.1f} us, "
-        f"{res['kernel_GBps']:.0f} GB/s ({res['hbm_frac']:.1%} HBM), {res['kernel_TFLOPs']:.1f} TFLOP/s")
+    log(f"[bench] {label}: {ms_step * 1e3:.1f} us/step, kernel {k_avg * 1e3:.1f} us, "
+        f"{res['kernel_GBps']:.0f} GB/s ({res['hbm_frac']:.1%} HBM), {res['kernel_TFLOPs']:.1f} TFLOP/s "
+        f"({res['mfma_frac']:.1%} MFMA); launch roofline {res['roofline']['bound']} "
+        f"{res['roofline']['t_roof_us']:.1f} us = {res['roofline']['frac']:.1%}")
     return res
 
 
@@ -245,20 +277,26 @@ def time_sched(steps: int, warmup_s: float):
     import torch
 
     from llmario_amd.kv import HipKvCache, Layer
-    from llmario_amd.sched import CacheKey, Decoding, Priority, Request, Scheduler
+    from llmario_amd.sched import Admitted, CacheKey, Decoding, Priority, Request, Scheduler
 
     rng = np.random.default_rng(5)
     ctx = [int(c) for c in rng.integers(1024, 8192, size=16, endpoint=True)]
     L = Layer(40, 8, 128, 128)
-    max_ctx = 8192 + 1024
+    max_ctx = 8192 + 2048
     hc = HipKvCache([L], max_ctx=max_ctx, n_seqs=18, kv_type="f16", block_tokens=16)
     budget = 16 + 2 * 512
     sch = Scheduler.bound(hc, budget, 18, CacheKey(bytes([5]), "f16", "theta=1e6"))
     vocab = 150000
-    long_ids = set()
-    for c in ctx:  # long-running decodes: the prompt, then generation up to the context limit
-        a = sch.admit(Request(rng.integers(0, vocab, size=c, dtype=np.uint32), max_ctx - c, Priority.Interactive))
-        long_ids.add(a.slot)
+    # long-running decodes: each generates up to `long_new` tokens after its prompt; one that
+    # reaches that count is finished and its request admitted again (its prompt blocks are
+    # published, so the new admission reuses them and decodes on at the same context), so the loop
+    # can run any number of steps without a sequence reaching max_ctx
+    long_new = 1024
+    long_prompt = {}
+    for c in ctx:
+        prompt = rng.integers(0, vocab, size=c, dtype=np.uint32)
+        a = sch.admit(Request(prompt, long_new, Priority.Interactive))
+        long_prompt[a.slot] = prompt
     arrivals = [rng.integers(0, vocab, size=4608, dtype=np.uint32) for _ in range(64)]
 
     def feed(n):
@@ -274,7 +312,7 @@ def time_sched(steps: int, warmup_s: float):
     out = torch.empty((budget, L.n_head, L.hdv), device="cuda")
     stream = torch.cuda.current_stream()
     scale = L.hd ** -0.5
-    acc = {"host": 0.0, "launch": 0.0, "rows": 0, "decodes": 0, "steps": 0, "fed": 0}
+    acc = {"host": 0.0, "launch": 0.0, "rows": 0, "decodes": 0, "steps": 0, "fed": 0, "renewed": 0}
 
     def one_step():
         t0 = time.perf_counter()
@@ -288,9 +326,18 @@ def time_sched(steps: int, warmup_s: float):
         sch.complete(st)
         for (sid, _, end) in st.prefills:
             sch.publish_prompt(sid, end)
-        for sid in st.decodes:  # a prompt request ends after its one generated token
-            if sid not in long_ids:
+        for sid in st.decodes:
+            if sid not in long_prompt:   # a prompt request ends after its one generated token
                 sch.finish(sid)
+                continue
+            sl = sch.slot(sid)
+            if sl.generated >= long_new:   # renew a long decode before it outgrows its reservation
+                prompt = long_prompt.pop(sid)
+                sch.finish(sid)
+                a = sch.admit(Request(prompt, long_new, Priority.Interactive))
+                assert isinstance(a, Admitted), "a renewed long request was not admitted"
+                long_prompt[a.slot] = prompt
+                acc["renewed"] += 1
         if sch.queued() < 2:
             feed(4)
         sch.drain_queue()
@@ -302,14 +349,20 @@ def time_sched(steps: int, warmup_s: float):
 
     feed(4)
     t_w = time.perf_counter()
-    while sum(1 for i in long_ids if sch.slot(i).state == Decoding()) < 16 or time.perf_counter() - t_w < warmup_s:
+    # warm-up: until every long request decodes, then at least warmup_s seconds (at most 2000 steps)
+    n_dec_steps = 0
+    while True:
+        decoding = sum(1 for i in long_prompt if sch.slot(i).state == Decoding())
+        if decoding == 16:
+            n_dec_steps += 1
+            if time.perf_counter() - t_w >= warmup_s or n_dec_steps >= 2000:
+                break
         one_step()
         if acc["steps"] % 16 == 0:
             torch.cuda.synchronize()
     torch.cuda.synchronize()
     log(f"[bench] sched_c5: {acc['steps']} warm-up steps in {time.perf_counter() - t_w:.2f}s")
-    acc.update(host=0.0, launch=0.0, rows=0, decodes=0, steps=0)
-    assert all(sch.slot(i) is not None for i in long_ids), "a long decode request was retracted"
+    acc.update(host=0.0, launch=0.0, rows=0, decodes=0, steps=0, renewed=0)
     t0 = time.perf_counter()
     for _ in range(steps):
         one_step()
@@ -319,7 +372,7 @@ def time_sched(steps: int, warmup_s: float):
            "host_us_per_step": acc["host"] * 1e6 / steps, "launch_us_per_step": acc["launch"] * 1e6 / steps,
            "rows_per_step": acc["rows"] / steps,
            "decode_rows_per_step": acc["decodes"] / steps, "rows_per_s": acc["rows"] / el,
-           "pool": sch.pool_stats()}
+           "long_requests_renewed": acc["renewed"], "pool": sch.pool_stats()}
     log(f"[bench] sched_c5: {res['ms_per_step'] * 1e3:.1f} us/step, scheduler host {res['host_us_per_step']:.1f} us/step, "
         f"producer + attend calls {res['launch_us_per_step']:.1f} us/step, "
         f"{res['rows_per_step']:.0f} rows/step ({res['decode_rows_per_step']:.1f} decode), {res['rows_per_s']:.0f} rows/s")
@@ -400,30 +453,40 @@ def time_window(steps: int, warmup_s: float):
     return res
 
 
-def physical_cores() -> int:
+def host_cpu() -> dict:
+    """The host's CPU model, its physical cores (no SMT siblings) among the CPUs this process may
+    run on, and the threads the baseline uses: every such physical core, capped at the per-GPU
+    CPU share the job is given (OMP_NUM_THREADS: a GPU box gives one GPU's job 16 CPUs, whatever
+    the machine has)."""
+    model, cores = "unknown", set()
+    allowed = os.sched_getaffinity(0) if hasattr(os, "sched_getaffinity") else set(range(os.cpu_count() or 1))
     try:
-        cores = set()
-        phys = core = None
+        cpu = phys = None
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("physical id"):
-                    phys = line.split(":")[1].strip()
-                elif line.startswith("core id"):
-                    core = line.split(":")[1].strip()
-                    cores.add((phys, core))
-        n = len(cores) or os.cpu_count() or 1
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "processor":
+                    cpu = int(v)
+                elif k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id" and cpu in allowed:
+                    cores.add((phys, v))
     except OSError:
-        n = os.cpu_count() or 1
-    try:
-        n = min(n, len(os.sched_getaffinity(0)))
-    except AttributeError:
         pass
-    return max(1, min(n, 16))
+    n_phys = len(cores) or len(allowed)
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(n_phys, share) if share > 0 else n_phys
+    return {"model": model, "physical_cores_allowed": n_phys, "cpus_allowed": len(allowed),
+            "cpu_share": share or None, "threads": max(1, threads)}
 
 
 def cpu_baseline(name: str, seconds: float, threads: int):
     """The restated reference CPU path (oracle/, a C++ port of attend/attend_split over a
-    reference-layout page store) on this host's cores, same inputs, pages pre-touched."""
+    reference-layout page store, the same (row, KV head) tasks, split rule and static chunking)
+    on this host's cores, same inputs, pages pre-touched. Times whole steps for about `seconds`."""
     import oracle as O
     from llmario_amd.workloads import Generator, config
 
@@ -442,12 +505,25 @@ def cpu_baseline(name: str, seconds: float, threads: int):
         oc.attend(0, segs, q, w.scale, w.window, threads)
         n += 1
         el = time.perf_counter() - t0
-        if el >= seconds or n >= 1000:
+        if el >= seconds or n >= 2000:
             break
     per = el / n
-    return {"value": w.algorithmic_bytes() / per / 1e9, "unit": "GB/s", "cores": threads, "kind": "port",
+    return {"value": w.algorithmic_bytes() / per / 1e9, "unit": "GB/s", "threads": threads,
+            "ms_per_step": per * 1e3, "steps": n,
             "sample": f"{name} full step ({w.n_rows} decode rows, {sum(w.totals)} cached positions), "
-                      f"{n} steps in {el:.1f}s, {per * 1e3:.2f} ms/step"}
+                      f"{n} steps in {el:.1f}s"}
+
+
+def run_leg(name, fn, errors):
+    """One extra measurement; its failure is recorded under its name and does not stop the run."""
+    try:
+        return fn()
+    except Exception as e:  # noqa: BLE001 - a side leg must never cost the headline line
+        import traceback
+        log(f"[bench] {name} failed: {e!r}")
+        traceback.print_exc(file=sys.stderr)
+        errors[name] = f"{type(e).__name__}: {e}"
+        return None
 
 
 def main():
@@ -455,9 +531,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5,window_c5w",
+    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5,window_c5w",
                     help="other configs to report ('' = none)")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="CPU baseline budget (c2 on all threads and on 1, c1 on both)")
+    ap.add_argument("--layers", type=int, default=0,
+                    help="with --profile-config: layers in rotation (0 = 1, or COLD_LAYERS for c2_cold)")
     ap.add_argument("--extra-warmup-s", type=float, default=0.2,
                     help="minimum warm-up time of each extra configuration (clock ramp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -500,23 +579,38 @@ def main():
         print(json.dumps(time_window(args.steps, args.extra_warmup_s)), flush=True)
         return
     if args.profile_config:
-        res = time_config(args.profile_config, args.steps, args.warmup, warmup_s=args.extra_warmup_s)
+        name, tuning, layers = args.profile_config, None, args.layers or 1
+        if name == "c2_cold":
+            name, layers = "c2", args.layers or COLD_LAYERS
+        elif name == "c3_p_f16":
+            name, tuning = "c3", {"prefill_p_f16": True}
+        res = time_config(name, args.steps, args.warmup, warmup_s=args.extra_warmup_s, n_layers=layers,
+                          tuning=tuning, label=args.profile_config)
         print(json.dumps(res), flush=True)
         return
 
-    head = time_config("c2", args.steps, args.warmup)
+    # Headline: c2 with the cache of COLD_LAYERS layers in rotation (1.5 GB of K/V, six times the
+    # device's last-level cache), so each step's pages come from HBM as in an engine's layer loop;
+    # the same config with one layer (every step re-reads the same 297 MB) is reported beside it.
+    errors = {}
+    head = time_config("c2", args.steps, args.warmup, n_layers=COLD_LAYERS, label="c2_cold")
     extra = {}
+    extra["c2_warm"] = run_leg("c2_warm", lambda: time_config("c2", args.steps, args.warmup, label="c2_warm"), errors)
+    short = max(5, min(args.steps, 20))
+    legs = {
+        "rope_c3": lambda: time_rope_store(short, args.extra_warmup_s),
+        "snapshot_c4": lambda: time_snapshot(short, args.extra_warmup_s),
+        "sched_c5": lambda: time_sched(max(5, min(args.steps, 40)), args.extra_warmup_s),
+        "window_c5w": lambda: time_window(short, args.extra_warmup_s),
+        # the prefill with P rounded to f16 (Metal's prefill precision), beside c3's default
+        "c3_p_f16": lambda: time_config("c3", short, 3, warmup_s=args.extra_warmup_s,
+                                        tuning={"prefill_p_f16": True}, label="c3_p_f16"),
+    }
     for name in [x for x in args.extra.split(",") if x]:
-        if name == "rope_c3":
-            extra[name] = time_rope_store(max(5, min(args.steps, 20)), args.extra_warmup_s)
-        elif name == "snapshot_c4":
-            extra[name] = time_snapshot(max(5, min(args.steps, 20)), args.extra_warmup_s)
-        elif name == "sched_c5":
-            extra[name] = time_sched(max(5, min(args.steps, 40)), args.extra_warmup_s)
-        elif name == "window_c5w":
-            extra[name] = time_window(max(5, min(args.steps, 20)), args.extra_warmup_s)
-        else:
-            extra[name] = time_config(name, max(5, min(args.steps, 20)), 3, warmup_s=args.extra_warmup_s)
+        fn = legs.get(name) or (lambda name=name: time_config(name, short, 3, warmup_s=args.extra_warmup_s))
+        r = run_leg(name, fn, errors)
+        if r is not None:
+            extra[name] = r
 
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
@@ -525,19 +619,38 @@ def main():
     roof = {"bound": "hbm", "achieved": round(head["kernel_GBps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(head["hbm_frac"], 4), "traffic": traffic,
             "kernel": "decode_mfma_kernel<f16,128,128>", "kernel_us": round(head["kernel_ms"] * 1e3, 2),
-            "algorithmic_bytes": head["bytes"]}
+            "algorithmic_bytes": head["bytes"],
+            "workload": f"c2, {COLD_LAYERS} layers in rotation (cold: K/V from HBM each step)"}
     # the device's practical streaming-read rate over the same number of bytes (a plain read
     # kernel, lmh_bench_read_ceiling), beside the published peak the roofline uses
-    ceil_gbs = read_ceiling(int(head["bytes"]))
-    roof["read_ceiling_GBps"] = round(ceil_gbs, 1)
-    roof["frac_of_read_ceiling"] = round(head["kernel_GBps"] / ceil_gbs, 4)
-    log(f"[bench] streaming-read ceiling over {int(head['bytes'])} bytes: {ceil_gbs:.0f} GB/s; decode kernel at "
-        f"{roof['frac_of_read_ceiling']:.1%} of it")
+    ceil_gbs = run_leg("read_ceiling", lambda: read_ceiling(int(head["bytes"])), errors)
+    if ceil_gbs:
+        roof["read_ceiling_GBps"] = round(ceil_gbs, 1)
+        roof["frac_of_read_ceiling"] = round(head["kernel_GBps"] / ceil_gbs, 4)
+        log(f"[bench] streaming-read ceiling over {int(head['bytes'])} bytes: {ceil_gbs:.0f} GB/s; decode kernel at "
+            f"{roof['frac_of_read_ceiling']:.1%} of it")
     cpu = None
     if not args.no_cpu_baseline:
-        th = physical_cores()
-        log(f"[bench] cpu baseline: c2 on {th} threads")
-        cpu = cpu_baseline("c2", args.cpu_seconds, th)
+        def baseline():
+            hc = host_cpu()
+            log(f"[bench] cpu baseline: {hc['model']}, {hc['physical_cores_allowed']} physical cores allowed, "
+                f"{hc['threads']} threads")
+            t = args.cpu_seconds
+            c2_all = cpu_baseline("c2", t * 0.45, hc["threads"])
+            c2_one = cpu_baseline("c2", t * 0.35, 1)
+            c1_all = cpu_baseline("c1", t * 0.1, hc["threads"])
+            c1_one = cpu_baseline("c1", t * 0.1, 1)
+            return {"value": round(c2_all["value"], 2), "unit": "GB/s", "cores": hc["threads"], "kind": "port",
+                    "sample": c2_all["sample"] + f" on {hc['threads']} threads (restated reference CPU path)",
+                    "cpu_model": hc["model"], "physical_cores_allowed": hc["physical_cores_allowed"],
+                    "cpu_share": hc["cpu_share"],
+                    "c2_1_thread": {"value": round(c2_one["value"], 3), "ms_per_step": round(c2_one["ms_per_step"], 3),
+                                    "sample": c2_one["sample"]},
+                    "c1": {"threads": hc["threads"], "value": round(c1_all["value"], 3),
+                           "ms_per_step": round(c1_all["ms_per_step"], 4), "sample": c1_all["sample"]},
+                    "c1_1_thread": {"value": round(c1_one["value"], 3), "ms_per_step": round(c1_one["ms_per_step"], 4),
+                                    "sample": c1_one["sample"]}}
+        cpu = run_leg("cpu_baseline", baseline, errors)
     line = {
         "metric": "decode KV-read GB/s (GQA paged decode, configs[1])",
         "value": round(head["GBps"], 1),
@@ -552,14 +665,23 @@ def main():
         "dtype": "f16",
         "data": "synthetic (seeded N(0,1) K/V/Q rounded to f16, seeded permuted block tables)",
         "config": {"workload": "c2: GQA paged decode, 32 seqs x 1 token, 32 Q / 8 KV heads, hd 128, "
-                               "ctx U[512,4096], page 16, f16 KV",
+                               f"ctx U[512,4096], page 16, f16 KV; cache of {COLD_LAYERS} such layers, one "
+                               "attended per step in rotation",
                    "parallelism": "single GPU"},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
-                    for k, v in {"c2": head, **extra}.items()},
+        "configs": {k: _round_floats(v) for k, v in {"c2_cold": head, **extra}.items() if v is not None},
+        "errors": errors or None,
     }
     print(json.dumps(line), flush=True)
+
+
+def _round_floats(v):
+    if isinstance(v, float):
+        return round(v, 4)
+    if isinstance(v, dict):
+        return {k: _round_floats(x) for k, x in v.items()}
+    return v
 
 
 if __name__ == "__main__":

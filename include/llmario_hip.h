@@ -233,6 +233,29 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
+/* Handle options of lmh_attend's planning and precision (no counterpart in the reference, whose
+ * CPU path has no such choices; its thread-count split rule is forward.rs:613-633). Set once or
+ * between calls; a zero field selects the default.
+ *   prefill_p_f16: 1 = the prefill products take P rounded to f16, the precision of Metal's
+ *     attn_prefill (attn_prefill.metal: half P); 0 (default) = P as f16 hi + lo parts (~22 bits,
+ *     the CPU path's f32 weights to within the 2e-3 bound even on rows whose output cancels).
+ *   prefill_min_rows: segments of at least this many rows go to the matrix-core prefill kernel
+ *     (default 16; 1 .. 2^32).
+ *   decode_target_items: split-K target of decode work items (default: the items the device holds
+ *     at once, from the occupancy query).
+ *   decode_min_tiles: smallest split-K chunk in 16-key tiles (default 8; 2 for f32 pages; 1 .. 64).
+ * Out-of-range values fail with LMH_INVALID_ARGUMENT and change nothing. */
+typedef struct lmh_attend_tuning {
+  uint32_t abi_version;        /* LMH_ABI_VERSION */
+  uint32_t prefill_p_f16;
+  uint64_t prefill_min_rows;
+  uint64_t decode_target_items;
+  uint64_t decode_min_tiles;
+} lmh_attend_tuning;
+int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t);
+/* The options in force (defaults resolved; decode_target_items 0 = the occupancy default). */
+int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t);
+
 /* Timing hook for benchmarks: when enabled, lmh_attend and lmh_qk_rope_store time each kernel
  * they launch with a HIP event pair that the kernel's own dispatch records (hipExtLaunchKernel: the
  * kernel alone), and the snapshot calls bracket their kernels with HIP events on `stream`;

@@ -58,6 +58,11 @@ class RopeParams(C.Structure):
                 ("attn_factor", C.c_float), ("q_norm", P), ("k_norm", P), ("freq_div", P)]
 
 
+class AttendTuning(C.Structure):
+    _fields_ = [("abi_version", u32), ("prefill_p_f16", u32), ("prefill_min_rows", u64),
+                ("decode_target_items", u64), ("decode_min_tiles", u64)]
+
+
 PRIORITY_BATCH, PRIORITY_API, PRIORITY_INTERACTIVE = 0, 1, 2
 
 
@@ -136,6 +141,8 @@ SIGNATURES = {
     "lmh_kv_gather_encoded": (i32, [P, u32, P, u64, P, P, P]),
     "lmh_qk_rope_store": (i32, [P, u32, P, u64, P, P, P, P, C.POINTER(RopeParams), P]),
     "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
+    "lmh_kv_set_tuning": (i32, [P, C.POINTER(AttendTuning)]),
+    "lmh_kv_get_tuning": (i32, [P, C.POINTER(AttendTuning)]),
     "lmh_kv_set_timing": (i32, [P, i32]),
     "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
     "lmh_bench_read_ceiling": (i32, [i32, u64, u32, C.POINTER(C.c_double)]),

@@ -123,6 +123,7 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
                                             const float* q, float* out, float* part) {
   constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
   constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
+  constexpr int PUP = KVT == KV_Q8 ? 0 : 7;  // weights scaled by 2^PUP (see the softmax step)
   using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
   const uint32_t lane = threadIdx.x & 63u;
   const DecodeItem it = items[wi];
@@ -237,35 +238,46 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
       for (int j = 0; j < NJ; j++) O[j] *= alpha;
       m = mn;
     }
-    const float mref = m == -INFINITY ? 0.f : m;  // every score is -inf while m is
+    // Weights p = 2^(s - m + PUP): the reference max shifted by PUP (the partial's m is written
+    // as m - PUP), so every weight is <= 2^(8 + PUP) and the f16 lo parts below stay normal for
+    // all weights above 2^(-PUP - 2) of the largest. q8_0 weights are multiplied by V scales
+    // first and keep PUP = 0 (their range is the scales').
+    const float mref = (m == -INFINITY ? 0.f : m) - (float)PUP;  // every score is -inf while m is
     float p[4];
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) p[rr] = exp2_fast(sc[rr] - mref);
     lsum += (p[0] + p[1]) + (p[2] + p[3]);
-    // ---- O^T += V^T P^T
+    // ---- O^T += V^T P^T, P carried past f16 as hi + lo halves (two products on the same V
+    // operand): the weights keep ~22 bits, as the f32 weights of the CPU path (forward.rs:645-666)
     if constexpr (KVT == KV_Q8) {
-      // P times the V scale of each (key, 32-dim block), in packed f16: the lane's scales sit as
-      // [key i][block b] halves, so keys (0, 1) and (2, 3) of block b pair up with one permute.
-      typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+      // P times the V scale of each (key, 32-dim block), in f32, then split: the lane's scales
+      // sit as [key i][block b] halves.
       constexpr int NCH = HDV / 32;
-      const uint32_t* vsw = (const uint32_t*)cur.vs;
-      const h2 p01 = h2{(_Float16)p[0], (_Float16)p[1]}, p23 = h2{(_Float16)p[2], (_Float16)p[3]};
 #pragma unroll
       for (int b = 0; b < HDV / 32; b++) {
-        const uint32_t sel = (b & 1) ? 0x07060302u : 0x05040100u;
-        const uint32_t s01 = __builtin_amdgcn_perm(vsw[(NCH + b) >> 1], vsw[b >> 1], sel);
-        const uint32_t s23 = __builtin_amdgcn_perm(vsw[(3 * NCH + b) >> 1], vsw[(2 * NCH + b) >> 1], sel);
-        const h2 q01 = p01 * __builtin_bit_cast(h2, s01), q23 = p23 * __builtin_bit_cast(h2, s23);
-        const h4 pb = h4{q01[0], q01[1], q23[0], q23[1]};
+        h4 ph, pl;
+#pragma unroll
+        for (int rr = 0; rr < 4; rr++) {
+          const float x = p[rr] * scale_at<NCH>(cur.vs, rr, b);
+          ph[rr] = (_Float16)x;
+          pl[rr] = (_Float16)(x - (float)ph[rr]);
+        }
 #pragma unroll
         for (int jj = 0; jj < 2; jj++) {
           const int j = 2 * b + jj;
           const uint32_t w = ((const uint32_t*)&cur.v[j >> 2])[j & 3];
-          O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(i8x4_to_h4(w), pb, O[j], 0, 0, 0);
+          const h4 va = i8x4_to_h4(w);
+          O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, O[j], 0, 0, 0);
+          O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, O[j], 0, 0, 0);
         }
       }
     } else {
-      const h4 pb = h4{(_Float16)p[0], (_Float16)p[1], (_Float16)p[2], (_Float16)p[3]};
+      h4 ph, pl;
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) {
+        ph[rr] = (_Float16)p[rr];
+        pl[rr] = (_Float16)(p[rr] - (float)ph[rr]);
+      }
 #pragma unroll
       for (int j = 0; j < NJ; j++) {
         const uint32_t* w = (const uint32_t*)&cur.v[j >> 1];
@@ -276,7 +288,8 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
         } else {
           va = __builtin_bit_cast(h4, make_uint2(w[o], w[o + 1]));
         }
-        O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pb, O[j], 0, 0, 0);
+        O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, ph, O[j], 0, 0, 0);
+        O[j] = __builtin_amdgcn_mfma_f32_16x16x16f16(va, pl, O[j], 0, 0, 0);
       }
     }
   };
@@ -309,7 +322,7 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
 #pragma unroll
     for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][0], O[j][1], O[j][2], O[j][3]);
     if (grp == 0) {
-      pp[HDV] = m;
+      pp[HDV] = m - (float)PUP;  // the reference the weights were taken against
       pp[HDV + 1] = lsum;
     }
   }

@@ -231,6 +231,9 @@ struct lmh_kv {
   std::vector<PrefillItem> pitems;
   std::vector<uint8_t> payload;
   std::vector<lmh_sched*> scheds;           // schedulers bound to this handle
+  // ---- lmh_attend planning / precision options (lmh_kv_set_tuning)
+  bool prefill_p_f16 = false;
+  uint64_t prefill_min_rows = 16, decode_target_items = 0, decode_min_tiles = 0;  // 0: defaults
   std::string err;
 
   ~lmh_kv() {
@@ -621,12 +624,6 @@ struct lmh_kv {
 };
 
 namespace {
-
-uint64_t env_u64(const char* name, uint64_t dflt) {
-  const char* v = std::getenv(name);
-  if (!v || !*v) return dflt;
-  return std::strtoull(v, nullptr, 10);
-}
 
 // FNV-1a (kv.rs:944-960 StableHasher)
 struct Fnv {
@@ -1354,7 +1351,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
   // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over one
   // workgroup per CU.
-  const uint64_t pf_min = env_u64("LMH_PREFILL_MIN_ROWS", 16);
+  const uint64_t pf_min = kv->prefill_min_rows;
   const bool pf_ok = scale > 0.f && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
   std::vector<uint8_t> decode_row(n_rows, 1);
   kv->pitems.clear();
@@ -1382,7 +1379,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
       for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
     }
     assign_prefill_units(kv->pitems, window, kv->n_cu, pf_wg, pf_per_wg);
-    if (prefill_lds_bytes(y.hd, max_pages, pf_per_wg) > 160 * 1024) {
+    if (prefill_lds_bytes(y.hd, max_pages, pf_per_wg) + prefill_static_lds_bytes() > 160 * 1024) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
       kv->pitems.clear();
       std::fill(decode_row.begin(), decode_row.end(), 1);
@@ -1405,12 +1402,13 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   // none waits for a slot to free up (a second, mostly empty round would double the kernel time).
   if (kv->decode_capacity[layer] == 0)
     kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd) * kv->n_cu;
-  const uint64_t target = std::max<uint64_t>(env_u64("LMH_DECODE_TARGET_ITEMS", kv->decode_capacity[layer]), 1);
+  const uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items
+                                                                     : kv->decode_capacity[layer], 1);
   // Smallest chunk: 8 tiles for the matrix-core kernels (enough work per wave to stream at full
   // rate); 2 tiles for f32 rows, whose VALU kernel walks keys with dependent loads (latency-bound:
   // more, shorter items hide it better).
   const uint64_t min_chunk =
-      std::max<uint64_t>(env_u64("LMH_DECODE_MIN_TILES", kv->kv_type == LMH_KV_F32 ? 2 : 8), 1);
+      kv->decode_min_tiles ? kv->decode_min_tiles : (kv->kv_type == LMH_KV_F32 ? 2 : 8);
   // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane);
   // grown until the rows' rounded-up split counts fit the target
   auto n_items_for = [&](uint64_t c) {
@@ -1485,6 +1483,7 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   pg.group = group;
   pg.scale_log2 = r.scale_log2;
   pg.window = r.window;
+  pg.p_f16 = kv->prefill_p_f16 ? 1u : 0u;
   const MergeCopy mc{(const uint32_t*)(ex + items_pad), (uint32_t*)kv->merge_buf.p,
                      kv->merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
   // A mixed batch (prefill units and decode items) runs as one launch: the prefill workgroups
@@ -1519,6 +1518,30 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
   }
   return kv->release_rows(slot, st);
+}
+
+int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {
+  if (!kv) return LMH_INVALID_ARGUMENT;
+  if (!t || t->abi_version != LMH_ABI_VERSION) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: null or ABI version");
+  if (t->prefill_p_f16 > 1) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_p_f16 must be 0 or 1");
+  if (t->prefill_min_rows > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_min_rows out of range");
+  if (t->decode_min_tiles > 64) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: decode_min_tiles must be <= 64");
+  if (t->decode_target_items > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: decode_target_items out of range");
+  kv->prefill_p_f16 = t->prefill_p_f16 != 0;
+  kv->prefill_min_rows = t->prefill_min_rows ? t->prefill_min_rows : 16;
+  kv->decode_target_items = t->decode_target_items;
+  kv->decode_min_tiles = t->decode_min_tiles;
+  return LMH_OK;
+}
+
+int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t) {
+  if (!kv || !t) return LMH_INVALID_ARGUMENT;
+  t->abi_version = LMH_ABI_VERSION;
+  t->prefill_p_f16 = kv->prefill_p_f16 ? 1u : 0u;
+  t->prefill_min_rows = kv->prefill_min_rows;
+  t->decode_target_items = kv->decode_target_items;
+  t->decode_min_tiles = kv->decode_min_tiles ? kv->decode_min_tiles : (kv->kv_type == LMH_KV_F32 ? 2 : 8);
+  return LMH_OK;
 }
 
 int32_t lmh_bench_read_ceiling(int32_t device, uint64_t bytes, uint32_t iters, double* gbps) {

@@ -75,8 +75,10 @@ __device__ inline uint32_t bf2_to_h2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
 }
 
-// Workgroup `wg` of a prefill launch: its list of units, items[wg * per_wg ..].
-template <int KVT, int HD>
+// Workgroup `wg` of a prefill launch: its list of units, items[wg * per_wg ..]. PLO: P carried
+// past f16 as hi + lo halves (two P.V products on the same V operand); without it P is rounded
+// to f16, the precision of the Metal sibling's prefill.
+template <int KVT, int HD, bool PLO>
 __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items,
                                            uint32_t per_wg, const float* q, float* out, uint32_t wg) {
   constexpr int NC = HD / 32;                 // Q.K chunks of 32 dims
@@ -94,7 +96,10 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     for (uint32_t i = threadIdx.x; i < per_wg * (sizeof(PrefillItem) / 4); i += NT) ((uint32_t*)units)[i] = src[i];
   }
   __syncthreads();
-  for (uint32_t unit = 0; unit < per_wg; unit++) {
+  // Steps over (unit, pass): one pass per unit, or two when its Q has lo parts (below).
+  uint32_t unit = 0, pass = 0;
+  bool lo_any = false;
+  while (unit < per_wg) {
   const PrefillItem it = units[unit];
   if (it.n_tok == 0) break;
   const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -169,11 +174,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     }
   };
   // After this thread's rows of tile ti have landed, bf16 only: K and V are widened to f16 in
-  // place (so both products run in f16 and Q keeps 11 bits), and the thread's two V chunks A
-  // (tile 2h) and B (tile 2h+1), each [4 keys of dim d | 4 keys of dim d+16], are rewritten as
-  // A' = [A keys of d | B keys of d] and B' = [A keys of d+16 | B keys of d+16], so one 16-byte
-  // read is a whole 32-key operand of the P.V product. f16 tiles are used as loaded (the extra
-  // LDS pass would cost more than the operand assembly it saves).
+  // place (so both products run in f16 and Q keeps 11 bits per part), and the thread's two V
+  // chunks A (tile 2h) and B (tile 2h+1), each [4 keys of dim d | 4 keys of dim d+16], are
+  // rewritten as A' = [A keys of d | B keys of d] and B' = [A keys of d+16 | B keys of d+16], so
+  // one 16-byte read is a whole 32-key operand of the P.V product. f16 tiles are used as loaded
+  // (the extra LDS pass would cost more than the operand assembly it saves).
   auto settle = [&](uint32_t ti) {
     uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
     if constexpr (KVT == KV_BF16) {
@@ -208,65 +213,118 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // publishes tile 0 also publishes the list.
   issue(0);
   if (n_tiles > 1) issue(1);
-  // ---- this lane's columns (one per 16-column block); their Q rows are loaded here and
-  // converted after the block-id list is written, so both round trips overlap
-  uint32_t cpos[NCB], clo[NCB];
-  bool cval[NCB];
-  float4 qraw[NCB][NC][2];
-#pragma unroll
-  for (int cb = 0; cb < NCB; cb++) {
-    const uint32_t c = w * COLS + cb * 16 + hq;
+  // Q of column c (pair (token c / G, head c % G)) in dims 32ch + 8grp .. +8 as f16. Q stays
+  // unscaled: a Q held in f16 or bf16 values (activations already rounded to the cache's 16-bit
+  // type) is then exact in f16, and the products are exact against exactly represented K; the
+  // scale multiplies the accumulator in the exponent. A Q with bits below f16 splits into
+  // hi + lo f16 parts (~22 bits) whose products sum in one accumulator: when any lane of the
+  // workgroup has a nonzero lo part, the unit runs in two passes of 16 columns per wave, the
+  // second column block's registers holding the first's lo part (same registers, same products
+  // per pass, twice the passes).
+  auto load_q = [&](uint32_t c, float4 (&raw)[NC][2]) {
     const uint32_t t = c / G, hh = c % G;
-    cval[cb] = t < it.n_tok;
-    cpos[cb] = it.pos0 + (cval[cb] ? t : 0);
-    clo[cb] = (pg.window > 0 && cpos[cb] + 1 > pg.window) ? cpos[cb] + 1 - pg.window : 0;
-    const float* qp = q + ((size_t)(it.row0 + (cval[cb] ? t : 0)) * pg.n_head + it.kvh * G + hh) * HD;
+    const bool valid = t < it.n_tok;
+    const float* qp = q + ((size_t)(it.row0 + (valid ? t : 0)) * pg.n_head + it.kvh * G + hh) * HD;
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
-      qraw[cb][ch][0] = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp) : make_float4(0, 0, 0, 0);
-      qraw[cb][ch][1] = cval[cb] ? *(const float4*)(qp + 32 * ch + 8 * grp + 4) : make_float4(0, 0, 0, 0);
+      raw[ch][0] = valid ? *(const float4*)(qp + 32 * ch + 8 * grp) : make_float4(0, 0, 0, 0);
+      raw[ch][1] = valid ? *(const float4*)(qp + 32 * ch + 8 * grp + 4) : make_float4(0, 0, 0, 0);
     }
-  }
-  // ---- block ids of every key page this unit reads
-  {
-    const int32_t* tab = g.table + (size_t)it.seq * g.bps;
-    for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
-  }
-  // ---- Q fragments: q * scale * log2(e) in f16
-  h8 qf[NCB][NC];
-#pragma unroll
-  for (int cb = 0; cb < NCB; cb++) {
+  };
+  // f16 hi and lo parts of the raw rows; returns whether any lo part of this lane is nonzero
+  auto split_q = [&](const float4 (&raw)[NC][2], h8 (&hi)[NC], h8 (&lo)[NC]) {
+    bool nz = false;
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
-      const float4 a = qraw[cb][ch][0], b = qraw[cb][ch][1];
+      const float4 a = raw[ch][0], b = raw[ch][1];
       const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-      for (int i = 0; i < 8; i++) qf[cb][ch][i] = (_Float16)(x[i] * pg.scale_log2);
+      for (int i = 0; i < 8; i++) {
+        const _Float16 h = (_Float16)x[i];
+        const _Float16 l = (_Float16)(x[i] - (float)h);
+        hi[ch][i] = h;
+        lo[ch][i] = l;
+        nz |= l != (_Float16)0.0f;
+      }
     }
+    return nz;
+  };
+  h8 qf[2][NC];
+  if (pass == 0) {
+    bool lo_need = false;
+    {
+      float4 raw[2][NC][2];
+      load_q(w * COLS + hq, raw[0]);
+      load_q(w * COLS + 16 + hq, raw[1]);
+      // ---- block ids of every key page this unit reads
+      const int32_t* tab = g.table + (size_t)it.seq * g.bps;
+      for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
+      h8 lo_unused[NC];   // the lo parts are only tested here
+      lo_need |= split_q(raw[0], qf[0], lo_unused);
+      lo_need |= split_q(raw[1], qf[1], lo_unused);
+    }
+    // workgroup-wide OR of the lo flags: one word per wave (written by its first lane) behind a
+    // barrier (which also publishes the block-id list)
+    __shared__ uint32_t lo_flags[PW];
+    {
+      const bool wave_lo = __ballot(lo_need) != 0;
+      if (lane == 0) lo_flags[w] = wave_lo ? 1u : 0u;
+    }
+    __syncthreads();
+    uint32_t lo_or = 0;
+#pragma unroll
+    for (int i = 0; i < PW; i++) lo_or |= lo_flags[i];
+    lo_any = lo_or != 0;
+  }
+  if (lo_any) {   // column block `pass` of each wave: its Q as hi (qf[0]) + lo (qf[1])
+    float4 raw[NC][2];
+    load_q(w * COLS + pass * 16 + hq, raw);
+    split_q(raw, qf[0], qf[1]);
   }
 
-  // Online-softmax state per column. Q carries the scale (q * scale * log2 e), so a product is a
-  // score in the log2 domain, and the reference max m rides in as the products' initial
-  // accumulator: nmv = {-m, -m, -m, -m}, making every score s - m directly (m = 0 while the column
-  // has seen no key). thr: the relative score above which m must move (8, or -inf while no key is
-  // visible). l: row sum; O^T.
+  // One pass over the unit's key tiles for this wave's column blocks: LO = false, both blocks
+  // (columns 32w .. 32w+31) with Q in f16; LO = true, block `pb` (columns 32w + 16pb ..) with
+  // its Q as hi (qf[0]) + lo (qf[1]).
+  auto run = [&](auto lo_tag, uint32_t pb) {
+  constexpr bool LO = decltype(lo_tag)::value;
+  constexpr int NX = LO ? 1 : NCB;            // column blocks of the pass
+  const float c2 = pg.scale_log2;             // scale * log2(e): raw score -> log2 domain
+  uint32_t cpos[NCB], clo[NCB];
+  bool cval[NCB];
+#pragma unroll
+  for (int x = 0; x < NX; x++) {
+    const uint32_t c = w * COLS + (LO ? pb : x) * 16 + hq;
+    const uint32_t t = c / G;
+    cval[x] = t < it.n_tok;
+    cpos[x] = it.pos0 + (cval[x] ? t : 0);
+    clo[x] = (pg.window > 0 && cpos[x] + 1 > pg.window) ? cpos[x] + 1 - pg.window : 0;
+  }
+
+  // Online-softmax state per column. The accumulator of Q.K starts at nm = -m (m: the column's
+  // reference max in raw score units, 0 while it has seen no key), so a product is s - m and the
+  // weight is p = 2^(c2 (s - m) + PUP): weights are scaled by 2^PUP so that every weight (<=
+  // 2^(12 + PUP), below) keeps a normal f16 lo part down to 2^(-PUP - 2) of the largest. thr: the
+  // relative score (log2 domain) above which m must move (8, or -inf while no key is visible).
+  // l: row sum; O^T.
+  constexpr float PUP = 3.0f;
   float nm[NCB], thr[NCB], l[NCB];
   f4 nmv[NCB];
   f4 O[NJ][NCB];
 #pragma unroll
-  for (int cb = 0; cb < NCB; cb++) {
-    nm[cb] = 0.f;
-    nmv[cb] = f4{0.f, 0.f, 0.f, 0.f};
-    thr[cb] = -INFINITY;
-    l[cb] = 0.f;
+  for (int x = 0; x < NX; x++) {
+    nm[x] = 0.f;
+    nmv[x] = f4{0.f, 0.f, 0.f, 0.f};
+    thr[x] = -INFINITY;
+    l[x] = 0.f;
 #pragma unroll
-    for (int j = 0; j < NJ; j++) O[j][cb] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; j++) O[j][x] = f4{0.f, 0.f, 0.f, 0.f};
   }
-  // this wave's lowest/highest column positions (mask-free tiles)
-  const bool wave_active = w * COLS / G < it.n_tok;
+  // this wave's lowest/highest column positions in the pass (mask-free tiles)
+  const uint32_t c_first = w * COLS + (LO ? pb * 16 : 0), c_span = LO ? 16 : COLS;
+  const bool wave_active = c_first / G < it.n_tok;
   uint32_t wpos_min, wpos_max;
   {
-    const uint32_t t0 = w * COLS / G, tl = (w * COLS + COLS - 1) / G;
+    const uint32_t t0 = c_first / G, tl = (c_first + c_span - 1) / G;
     const uint32_t t1 = tl < it.n_tok ? tl : it.n_tok - 1;
     wpos_min = it.pos0 + (t0 < it.n_tok ? t0 : t1);
     wpos_max = it.pos0 + t1;
@@ -299,102 +357,121 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       }
     }
   };
-  // S^T for the 32 keys of a half (two 16-key page tiles) x this wave's 32 columns
+  // S^T for the 32 keys of a half (two 16-key page tiles) x the pass's columns (LO: the hi and
+  // lo products of one column block, summed)
   auto qk = [&](f4 (&S)[2][NCB], const KOps& ko) {
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
         const h8 a = __builtin_bit_cast(h8, ko.a[ch][kk]);
+        if constexpr (LO) {
+          S[kk][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][ch], ch == 0 ? nmv[0] : S[kk][0], 0, 0, 0);
+          S[kk][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ch], ch == 0 ? f4{0.f, 0.f, 0.f, 0.f} : S[kk][1],
+                                                            0, 0, 0);
+        } else {
 #pragma unroll
-        for (int cb = 0; cb < NCB; cb++) {
-          const f4 acc = ch == 0 ? nmv[cb] : S[kk][cb];
-          S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], acc, 0, 0, 0);
+          for (int cb = 0; cb < NCB; cb++) {
+            const f4 acc = ch == 0 ? nmv[cb] : S[kk][cb];
+            S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], acc, 0, 0, 0);
+          }
         }
       }
+    }
+    if constexpr (LO) {
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++) S[kk][0] += S[kk][1];
     }
   };
   // keys outside a column's [lo, pos] get -inf (keys past the range are past every position)
   auto mask = [&](f4 (&S)[2][NCB], uint32_t kbase) {
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) {
+    for (int x = 0; x < NX; x++) {
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const uint32_t key = kbase + kk * 16 + grp * 4 + r;
-          S[kk][cb][r] = (key > cpos[cb] || key < clo[cb]) ? -INFINITY : S[kk][cb][r];
+          S[kk][x][r] = (key > cpos[x] || key < clo[x]) ? -INFINITY : S[kk][x][r];
         }
       }
     }
   };
   // Lazy reference max: m moves (rescaling O and l) only when the weights of a half grow too
-  // large. Each lane sums its own 8 weights p = 2^(s - m) per column (the row-sum terms, needed
-  // anyway); a sum above 2^12 (some relative score above 9: every score <= 8 gives a sum <= 2^11)
+  // large. Each lane sums its own 8 weights per column (the row-sum terms, needed anyway); a sum
+  // above 2^(12 + PUP) (some relative score above 9: every score <= 8 gives a sum <= 2^(11 + PUP))
   // or a column with no visible key yet sends the wave to the rare path, where the column max is
   // reduced over the lane groups and m moves to it if it exceeds m + 8 (or is the first finite
-  // score). So every weight converted to f16 is <= 2^12, and O is almost never rescaled. The
-  // scores of the next half, already computed against the old m, are shifted with it.
+  // score). So every weight converted to f16 is <= 2^(12 + PUP), and O is almost never rescaled.
+  // The scores of the next half, already computed against the old m, are shifted with it.
   auto expo = [&](const f4 (&S)[2][NCB], float (&pw)[NCB][8], float (&ps)[NCB]) {
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) {
+    for (int x = 0; x < NX; x++) {
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) pw[cb][kk * 4 + r] = exp2_fast(S[kk][cb][r]);
+        for (int r = 0; r < 4; r++) pw[x][kk * 4 + r] = exp2_fast(fmaf(S[kk][x][r], c2, PUP));
       }
-      ps[cb] = ((pw[cb][0] + pw[cb][1]) + (pw[cb][2] + pw[cb][3])) +
-               ((pw[cb][4] + pw[cb][5]) + (pw[cb][6] + pw[cb][7]));
+      ps[x] = ((pw[x][0] + pw[x][1]) + (pw[x][2] + pw[x][3])) + ((pw[x][4] + pw[x][5]) + (pw[x][6] + pw[x][7]));
     }
   };
   auto rebase = [&](f4 (&S)[2][NCB], f4 (&Sn)[2][NCB]) {
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) {
-      const float lm = fmaxf(fmaxf(fmaxf(S[0][cb][0], S[0][cb][1]), fmaxf(S[0][cb][2], S[0][cb][3])),
-                             fmaxf(fmaxf(S[1][cb][0], S[1][cb][1]), fmaxf(S[1][cb][2], S[1][cb][3])));
-      const float tmax = max_over_groups(lm);
-      const bool mv = tmax > thr[cb];
-      // no key seen yet (thr = -inf): O and l are zero, and tmax may be any finite value
-      const float alpha = !mv ? 1.f : (thr[cb] == -INFINITY ? 0.f : exp2_fast(-tmax));
+    for (int x = 0; x < NX; x++) {
+      const float lm = fmaxf(fmaxf(fmaxf(S[0][x][0], S[0][x][1]), fmaxf(S[0][x][2], S[0][x][3])),
+                             fmaxf(fmaxf(S[1][x][0], S[1][x][1]), fmaxf(S[1][x][2], S[1][x][3])));
+      const float tmax = max_over_groups(lm);   // raw units, relative to m
+      const bool mv = tmax * c2 > thr[x];
       const float sh = mv ? tmax : 0.f;
-      l[cb] *= alpha;
+      const float nm_new = nm[x] - sh;
+      // no key seen yet (thr = -inf): O and l are zero, and tmax may be any finite value
+      const float alpha = !mv ? 1.f : (thr[x] == -INFINITY ? 0.f : exp2_fast((nm_new - nm[x]) * c2));
+      l[x] *= alpha;
 #pragma unroll
-      for (int j = 0; j < NJ; j++) O[j][cb] *= alpha;
+      for (int j = 0; j < NJ; j++) O[j][x] *= alpha;
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
-        S[kk][cb] -= sh;
-        Sn[kk][cb] -= sh;
+        S[kk][x] -= sh;
+        Sn[kk][x] -= sh;
       }
-      nm[cb] -= sh;
-      nmv[cb] = f4{nm[cb], nm[cb], nm[cb], nm[cb]};
-      thr[cb] = mv ? 8.0f : thr[cb];
+      nm[x] = nm_new;
+      nmv[x] = f4{nm_new, nm_new, nm_new, nm_new};
+      thr[x] = mv ? 8.0f : thr[x];
     }
   };
-  // P = 2^(s - m) rounded to f16, row sums in f32 (Sn: the next half's scores, see rebase)
-  auto softmax = [&](f4 (&S)[2][NCB], h8 (&P)[NCB], f4 (&Sn)[2][NCB]) {
+  // P = 2^(c2 (s - m) + PUP) as f16 hi (+ lo) parts, row sums in f32 (Sn: the next half's scores,
+  // see rebase)
+  auto softmax = [&](f4 (&S)[2][NCB], h8 (&Ph)[NCB], h8 (&Pl)[NCB], f4 (&Sn)[2][NCB]) {
     float pw[NCB][8], ps[NCB];
     expo(S, pw, ps);
     bool need = false;
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) need |= !(ps[cb] <= 4096.f) || thr[cb] == -INFINITY;
+    for (int x = 0; x < NX; x++) need |= !(ps[x] <= 4096.f * 8.f) || thr[x] == -INFINITY;
     if (__ballot(need)) {
       rebase(S, Sn);
       expo(S, pw, ps);
     }
 #pragma unroll
-    for (int cb = 0; cb < NCB; cb++) {
-      l[cb] += ps[cb];
-      P[cb] = h8{(_Float16)pw[cb][0], (_Float16)pw[cb][1], (_Float16)pw[cb][2], (_Float16)pw[cb][3],
-                 (_Float16)pw[cb][4], (_Float16)pw[cb][5], (_Float16)pw[cb][6], (_Float16)pw[cb][7]};
+    for (int x = 0; x < NX; x++) {
+      l[x] += ps[x];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const _Float16 h = (_Float16)pw[x][i];
+        Ph[x][i] = h;
+        if constexpr (PLO) Pl[x][i] = (_Float16)(pw[x][i] - (float)h);
+      }
     }
   };
   // O^T += V^T P^T over a half, 32 keys per MFMA
-  auto pv = [&](const h8 (&P)[NCB], const VOps& vo) {
+  auto pv = [&](const h8 (&Ph)[NCB], const h8 (&Pl)[NCB], const VOps& vo) {
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
       const h8 va = __builtin_bit_cast(h8, vo.a[j]);
 #pragma unroll
-      for (int cb = 0; cb < NCB; cb++) O[j][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, P[cb], O[j][cb], 0, 0, 0);
+      for (int x = 0; x < NX; x++) {
+        O[j][x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, Ph[x], O[j][x], 0, 0, 0);
+        if constexpr (PLO) O[j][x] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, Pl[x], O[j][x], 0, 0, 0);
+      }
     }
   };
 
@@ -422,7 +499,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   };
   auto sync = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
   f4 S0[2][NCB], S1[2][NCB];
-  h8 P[NCB];
+  h8 Ph[NCB], Pl[NCB];
   KOps ko;
   VOps vo;
   wait_tile(0);
@@ -445,8 +522,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       wait_tile(ti + 1);
       settle(ti + 1);
       qk(S1, ko);
-      softmax(S0, P, S1);
-      pv(P, vo);
+      softmax(S0, Ph, Pl, S1);
+      pv(Ph, Pl, vo);
       if (need_mask) mask(S1, key0 + 32);
     } else {
       wait_tile(ti + 1);
@@ -460,36 +537,46 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       // next iteration reads S0
       load_k(ko, kv_lds + ((ti + 1) % NSTAGE) * 8 * TILE, 0);
       qk(S0, ko);
-      softmax(S1, P, S0);
-      pv(P, vo);
+      softmax(S1, Ph, Pl, S0);
+      pv(Ph, Pl, vo);
     }
   }
 
   // ---- epilogue: per column, out = O / l (l summed over the lane groups)
 #pragma unroll
-  for (int cb = 0; cb < NCB; cb++) {
-    const float lt = sum_over_groups(l[cb]);
-    if (!cval[cb]) continue;
-    const uint32_t col = w * COLS + cb * 16 + hq;
+  for (int x = 0; x < NX; x++) {
+    const float lt = sum_over_groups(l[x]);
+    if (!cval[x]) continue;
+    const uint32_t col = w * COLS + (LO ? pb : x) * 16 + hq;
     const uint32_t t = col / G, hh = col % G;
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     float* op = out + ((size_t)(it.row0 + t) * pg.n_head + it.kvh * G + hh) * HD;
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
-      const f4 o = O[j][cb] * inv;
+      const f4 o = O[j][x] * inv;
       *(float4*)(op + 16 * j + 4 * grp) = make_float4(o[0], o[1], o[2], o[3]);
     }
   }
-  // every wave is done with the stages and block ids before the next unit refills them
+  // every wave is done with the stages and block ids before the next pass or unit refills them
   __syncthreads();
+  };
+
+  if (!lo_any) {
+    run(std::false_type{}, 0);
+    unit++;
+  } else {
+    run(std::true_type{}, pass);
+    pass ^= 1u;
+    if (pass == 0) unit++;
+  }
   }
 }
 
-template <int KVT, int HD>
+template <int KVT, int HD, bool PLO>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32_t per_wg, const float* q,
                     float* out) {
-  prefill_wg<KVT, HD>(g, pg, items, per_wg, q, out, blockIdx.x);
+  prefill_wg<KVT, HD, PLO>(g, pg, items, per_wg, q, out, blockIdx.x);
 }
 
 // A mixed batch (prefill units and decode items) in one launch: workgroups 0 .. pf_wg-1 run the
@@ -499,12 +586,12 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
 // workgroup carries the prefill LDS allocation, so a CU holds one workgroup of either kind: the
 // same eight waves per CU the decode kernel runs at. One launch instead of a decode launch on a
 // second stream saves the two cross-stream waits and their idle gaps.
-template <int KVT, int HD>
+template <int KVT, int HD, bool PLO>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_t per_wg, uint32_t pf_wg, RowGeom r,
                   const DecodeItem* items, uint32_t n_items, const float* q, float* out, float* part, MergeCopy mc) {
   if (blockIdx.x < pf_wg) {
-    prefill_wg<KVT, HD>(g, pg, pitems, per_wg, q, out, blockIdx.x);
+    prefill_wg<KVT, HD, PLO>(g, pg, pitems, per_wg, q, out, blockIdx.x);
     return;
   }
   const uint32_t b = blockIdx.x - pf_wg;
@@ -517,7 +604,10 @@ template <int KVT, int HD>
 hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
                     uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s, const LaunchEv& ev) {
   const uint32_t lds = (uint32_t)prefill_lds_bytes(HD, max_pages, per_wg);
-  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+  if (pg.p_f16)
+    LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+  else
+    LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
   return hipGetLastError();
 }
 
@@ -528,14 +618,20 @@ hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const Prefil
                           hipStream_t s, const LaunchEv& ev) {
   const uint32_t lds = (uint32_t)prefill_lds_bytes(HD, max_pages, per_wg);
   const uint32_t n_wg = pf_wg + (n_items + PW - 1) / PW;
-  LMH_LAUNCH(ev, (mixed_kernel<KVT, HD>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r, items,
-             n_items, q, out, part, mc);
+  if (pg.p_f16)
+    LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
+               items, n_items, q, out, part, mc);
+  else
+    LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
+               items, n_items, q, out, part, mc);
   return hipGetLastError();
 }
 
 }  // namespace
 
 uint32_t prefill_cols_per_unit() { return PW * COLS; }
+
+size_t prefill_static_lds_bytes() { return 64; }  // lo_flags[PW], rounded up
 
 size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg) {
   return NSTAGE * 8 * (16 * (size_t)hd * 2) + (size_t)per_wg * sizeof(PrefillItem) + (size_t)max_pages * 4;

@@ -16,13 +16,17 @@ from .kv import HipKvCache
 from .workloads import Generator, Workload
 
 
-def load(w: Workload, gen: Generator | None = None, device: int = 0, on_rows=None) -> HipKvCache:
-    """Build and fill the cache. ``on_rows(s, table, k, v)`` sees each sequence's host rows."""
+def load(w: Workload, gen: Generator | None = None, device: int = 0, on_rows=None, n_layers: int = 1) -> HipKvCache:
+    """Build and fill the cache. ``on_rows(s, table, k, v)`` sees each sequence's host rows.
+    With ``n_layers`` > 1 the cache holds that many layers of the workload's geometry (each block
+    carries every layer, as the reference's block does), all filled with the same rows: a step
+    that attends one layer at a time in rotation then reads K/V last touched n_layers - 1 steps
+    earlier, as an engine's layer loop does (forward.rs:329-367)."""
     import torch
 
     gen = gen or Generator(w)
     L = w.layer
-    cache = HipKvCache([L], max_ctx=w.max_ctx(), n_seqs=w.n_seqs, kv_type=w.kv_type,
+    cache = HipKvCache([L] * n_layers, max_ctx=w.max_ctx(), n_seqs=w.n_seqs, kv_type=w.kv_type,
                        block_tokens=w.block_tokens, pool_tokens=w.pool_tokens(), device=device)
     dev = torch.device("cuda", device)
     for s in range(w.n_seqs):
@@ -31,10 +35,11 @@ def load(w: Workload, gen: Generator | None = None, device: int = 0, on_rows=Non
         seg = [(s, 0, k.shape[0], 0)]
         kd = torch.from_numpy(np.ascontiguousarray(k)).to(dev)
         vd = torch.from_numpy(np.ascontiguousarray(v)).to(dev)
-        if k.dtype == np.uint8:
-            cache.store_encoded(0, seg, kd, vd)
-        else:
-            cache.store(0, seg, kd, vd)
+        for layer in range(n_layers):
+            if k.dtype == np.uint8:
+                cache.store_encoded(layer, seg, kd, vd)
+            else:
+                cache.store(layer, seg, kd, vd)
         torch.cuda.synchronize(dev)
         del kd, vd
         cache.set_len(s, w.prior[s])

@@ -264,6 +264,26 @@ class HipKvCache:
                                        C.c_void_p(out.data_ptr()), float(scale), int(window or 0),
                                        _stream_ptr(stream)))
 
+    def set_tuning(self, *, prefill_p_f16: bool | None = None, prefill_min_rows: int | None = None,
+                   decode_target_items: int | None = None, decode_min_tiles: int | None = None):
+        """lmh_kv_set_tuning: change the given options, keep the others (0 = the default)."""
+        t = N.AttendTuning()
+        self._check(N.lib().lmh_kv_get_tuning(self.h, C.byref(t)))
+        if prefill_p_f16 is not None:
+            t.prefill_p_f16 = 1 if prefill_p_f16 else 0
+        if prefill_min_rows is not None:
+            t.prefill_min_rows = int(prefill_min_rows)
+        if decode_target_items is not None:
+            t.decode_target_items = int(decode_target_items)
+        if decode_min_tiles is not None:
+            t.decode_min_tiles = int(decode_min_tiles)
+        self._check(N.lib().lmh_kv_set_tuning(self.h, C.byref(t)))
+
+    def tuning(self) -> dict:
+        t = N.AttendTuning()
+        self._check(N.lib().lmh_kv_get_tuning(self.h, C.byref(t)))
+        return {f: getattr(t, f) for f, _ in N.AttendTuning._fields_ if f != "abi_version"}
+
     def set_timing(self, on: bool):
         self._check(N.lib().lmh_kv_set_timing(self.h, 1 if on else 0))
 

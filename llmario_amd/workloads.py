@@ -93,6 +93,27 @@ class Workload:
         L = self.layer
         return 2.0 * (L.hd + L.hdv) * self.visible_pairs() * L.n_head
 
+    def parts(self) -> dict:
+        """The step's work split by kind: decode rows (single-row segments: their visible K/V bytes
+        per KV head plus their Q / O bytes, and FLOPs) and multi-row segments (prefill: their keys'
+        K/V once per KV head plus Q / O bytes, and FLOPs). Table reads are left out (a few KB)."""
+        L = self.layer
+        out = {"decode_bytes": 0.0, "decode_flops": 0.0, "prefill_bytes": 0.0, "prefill_flops": 0.0}
+        for p, n in zip(self.prior, self.new):
+            kind = "decode" if n == 1 else "prefill"
+            last = p + n - 1
+            lo = max(0, p + 1 - self.window) if self.window else 0
+            keys = last + 1 - lo
+            pairs = 0
+            for i in range(n):
+                pos = p + i
+                plo = max(0, pos + 1 - self.window) if self.window else 0
+                pairs += pos + 1 - plo
+            out[kind + "_bytes"] += keys * L.n_kv * (L.hd + L.hdv) * self.kv_elem_bytes() + \
+                n * L.n_head * (L.hd + L.hdv) * 4
+            out[kind + "_flops"] += 2.0 * (L.hd + L.hdv) * pairs * L.n_head
+        return out
+
 
 def config(name: str) -> Workload:
     """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096)."""

@@ -173,12 +173,11 @@ SMALL = [
 
 @pytest.mark.parametrize("kv,layer,prior,new,window,bt", SMALL)
 @pytest.mark.parametrize("split", ["auto", "forced"])
-def test_attend_small(cuda, monkeypatch, kv, layer, prior, new, window, bt, split):
-    if split == "forced":
-        monkeypatch.setenv("LMH_DECODE_MIN_TILES", "1")
-        monkeypatch.setenv("LMH_DECODE_TARGET_ITEMS", "100000")
+def test_attend_small(cuda, kv, layer, prior, new, window, bt, split):
     w = small("t", kv, layer, prior, new, window=window, seed=31, block_tokens=bt)
     hc, oc, q = pair(w)
+    if split == "forced":
+        hc.set_tuning(decode_min_tiles=1, decode_target_items=100000)
     got = run_gpu(hc, w, q)
     ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
     assert np.isfinite(got).all()
@@ -218,17 +217,16 @@ def test_attend_config_sampled_rows(cuda, name):
 
 @pytest.mark.parametrize("name", golden_names())
 @pytest.mark.parametrize("split", ["auto", "forced"])
-def test_golden_fixture(cuda, monkeypatch, name, split):
+def test_golden_fixture(cuda, name, split):
     """The fixture's encoded rows stored through the C ABI come back byte for byte, and attention
     over them matches the fixture's expected outputs (oracle and float64) within tolerance."""
     import torch
-    if split == "forced":
-        monkeypatch.setenv("LMH_DECODE_MIN_TILES", "1")
-        monkeypatch.setenv("LMH_DECODE_TARGET_ITEMS", "100000")
     f = load_golden(name)
     L = Layer(*f.layer)
     hc = HipKvCache([L], max_ctx=f.max_ctx, n_seqs=len(f.prior), kv_type=f.kv_type,
                     block_tokens=f.block_tokens, pool_tokens=f.pool_tokens)
+    if split == "forced":
+        hc.set_tuning(decode_min_tiles=1, decode_target_items=100000)
     for s in range(len(f.prior)):
         hc.adopt_blocks(s, f.tables[s])
         n = f.k_rows[s].shape[0]

@@ -9,11 +9,9 @@ K/V of a position is a closed-form function of (token, position), so blocks recl
 hash hold exactly what a recomputation would write; a wrong reuse shows up in the dense check.
 
 Error scale: these K/V are bounded (|v| <= 1) and the softmax is flat, so many outputs cancel to a
-few hundredths while the V rows are of order one. The kernels round P (and the prefill kernel
-q * scale * log2 e) to f16, an error relative to the terms w_i v_i, not to their sum, so each
-(row, head) is measured against ||sum_i w_i |v_i| ||_inf, the scale those roundings act on (equal
-to ||out||_inf when nothing cancels): ||got - ref||_inf / that <= 2e-3. The f32 oracle itself stays
-within 1e-4 of the dense form under the strict ||out||_inf normalization.
+few hundredths while the V rows are of order one; every (row, head) is still held to the strict
+per-row bound ||got - ref||_inf / ||ref||_inf <= 2e-3 (the kernels carry Q and P past f16 as hi + lo
+parts). The f32 oracle itself stays within 1e-4 of the dense form under the same normalization.
 """
 
 import numpy as np
@@ -41,26 +39,18 @@ def kv_rows(tokens, positions):
 
 
 def dense_attend(q_row, tokens, pos, scale):
-    """Attention of one row at `pos` over positions 0..=pos from the closed form (f16-rounded),
-    and per head the error scale ||sum_i w_i |v_i| ||_inf."""
+    """Attention of one row at `pos` over positions 0..=pos from the closed form (f16-rounded)."""
     k, v = kv_rows(tokens[:pos + 1], np.arange(pos + 1))
     k = k.astype(np.float16).astype(np.float64).reshape(pos + 1, NK, HD)
     v = v.astype(np.float16).astype(np.float64).reshape(pos + 1, NK, HD)
     out = np.zeros((NH, HD))
-    mag = np.zeros(NH)
     for h in range(NH):
         kh = h // (NH // NK)
         s = k[:, kh, :] @ q_row[h].astype(np.float64) * scale
         w = np.exp(s - s.max())
         w /= w.sum()
         out[h] = w @ v[:, kh, :]
-        mag[h] = (w @ np.abs(v[:, kh, :])).max()
-    return out, mag
-
-
-def scaled_err(got, ref, mag):
-    """max over heads of ||got - ref||_inf / mag (mag: the per-head error scale above)."""
-    return float((np.abs(np.asarray(got, np.float64) - ref).max(axis=-1) / mag).max())
+    return out
 
 
 @pytest.mark.parametrize("seed", [0, 1])
@@ -139,11 +129,11 @@ def test_scheduler_drives_the_hip_path_like_the_oracle(cuda, seed):
         got = out.cpu().numpy()
         ref = oc.attend(0, segs_o, qv, scale)
         for r in range(n):
-            dense, mag = dense_attend(qv[r], tokens[row_slot[r]], row_pos[r], scale)
+            dense = dense_attend(qv[r], tokens[row_slot[r]], row_pos[r], scale)
             assert row_rel_err(ref[r], dense) <= 1e-4, f"oracle, step {it} row {r}"
-            assert scaled_err(got[r], ref[r], mag) <= TOL["f16"], f"vs oracle, step {it} row {r}"
-            assert scaled_err(got[r], dense, mag) <= TOL["f16"], f"vs dense, step {it} row {r}"
-            stats["worst"] = max(stats["worst"], scaled_err(got[r], dense, mag))
+            assert row_rel_err(got[r], ref[r]) <= TOL["f16"], f"vs oracle, step {it} row {r}"
+            assert row_rel_err(got[r], dense) <= TOL["f16"], f"vs dense, step {it} row {r}"
+            stats["worst"] = max(stats["worst"], row_rel_err(got[r], ref[r]))
         hc.commit_batch(segs)
         oc.commit_batch(segs_o)
         hs.complete(st)
