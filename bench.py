@@ -582,8 +582,8 @@ def main():
         name, tuning, layers = args.profile_config, None, args.layers or 1
         if name == "c2_cold":
             name, layers = "c2", args.layers or COLD_LAYERS
-        elif name == "c3_p_f16":
-            name, tuning = "c3", {"prefill_p_f16": True}
+        elif name.endswith("_p_f16"):
+            name, tuning = name[:-len("_p_f16")], {"prefill_p_f16": True}
         res = time_config(name, args.steps, args.warmup, warmup_s=args.extra_warmup_s, n_layers=layers,
                           tuning=tuning, label=args.profile_config)
         print(json.dumps(res), flush=True)

@@ -233,6 +233,21 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
+/* lmh_attend for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation); no counterpart in the reference. Same arguments, results and
+ * errors as lmh_attend, and it allocates nothing: no device, pinned or event allocation. Split-K
+ * partials and the merge list live in a file-scope device array of 32 MiB per GPU, held until the
+ * process ends (its address is resolved once per device when a handle is created there): the
+ * split count is capped to what it holds, and a call that still needs more split-K scratch, or
+ * whose work list exceeds the staging capacity reserved at lmh_kv_create (1 MiB per slot: ~32 K
+ * decode items), fails with LMH_INVALID_ARGUMENT and a message naming both sizes. Nothing in the
+ * scratch must start at zero (every partial is written before it is read). Every call on one GPU
+ * shares its array, which keeps the last call's contents: calls that overlap on one GPU (other
+ * streams or other handles on the same device) race; issue them in order on one stream. The
+ * timing hook records nothing for these calls. */
+int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs,
+                           const float* q, float* out, float scale, uint64_t window, void* stream);
+
 /* Handle options of lmh_attend's planning and precision (no counterpart in the reference, whose
  * CPU path has no such choices; its thread-count split rule is forward.rs:613-633). Set once or
  * between calls; a zero field selects the default.

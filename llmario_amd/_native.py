@@ -141,6 +141,7 @@ SIGNATURES = {
     "lmh_kv_gather_encoded": (i32, [P, u32, P, u64, P, P, P]),
     "lmh_qk_rope_store": (i32, [P, u32, P, u64, P, P, P, P, C.POINTER(RopeParams), P]),
     "lmh_attend": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
+    "lmh_attend_noalloc": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
     "lmh_kv_set_tuning": (i32, [P, C.POINTER(AttendTuning)]),
     "lmh_kv_get_tuning": (i32, [P, C.POINTER(AttendTuning)]),
     "lmh_kv_set_timing": (i32, [P, i32]),

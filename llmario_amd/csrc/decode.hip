@@ -26,6 +26,9 @@
 // f32 pages (VALU): lane per key for Q.K, lane per dim for P.V, fp32 throughout.
 #include "decode_tile.h"
 
+#include <mutex>
+#include <unordered_map>
+
 namespace lmh {
 namespace {
 
@@ -360,6 +363,36 @@ uint32_t resident_hd(uint32_t hd) {
   return resident_t<KVT, 256>();
 }
 }  // namespace
+
+// ---- scratch of lmh_attend_noalloc --------------------------------------------------------------
+// Split-K partials and the merge list of calls that may not allocate: a file-scope device array,
+// one copy per GPU, held until the process ends. Host code never names `scratch` as an address
+// (in host code the name is a stand-in, not the device address): noalloc_scratch() resolves each
+// device's copy once with hipGetSymbolAddress, with that device current, and the launches take the
+// resolved pointer like any other buffer.
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+hipError_t noalloc_scratch(int device, uint8_t** out) {
+  static std::mutex mu;
+  static std::unordered_map<int, uint8_t*> addr;  // device ordinal -> address of its copy
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = addr.find(device);
+  if (it != addr.end()) {
+    *out = it->second;
+    return hipSuccess;
+  }
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return e;
+  if (cur != device) return hipErrorInvalidDevice;   // the caller makes `device` current first
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess) return e;
+  if (!p) return hipErrorInvalidSymbol;
+  addr[device] = (uint8_t*)p;
+  *out = (uint8_t*)p;
+  return hipSuccess;
+}
 
 uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd) {
   switch (kv_type) {

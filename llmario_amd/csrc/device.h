@@ -180,6 +180,10 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
 // max_split: the largest n_split of the items (over 16: rows loaded in groups of 16)
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
                         float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev = {});
+// The device scratch of lmh_attend_noalloc (split-K partials, then the merge list): its size, and
+// the address of `device`'s copy (call with that device current; resolved once per device).
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
+hipError_t noalloc_scratch(int device, uint8_t** out);
 // Decode work items (waves) one CU holds at once for a layer's decode kernel (occupancy query).
 uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd);
 bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);

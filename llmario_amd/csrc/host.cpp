@@ -107,10 +107,15 @@ struct Uploader {  // ring of pinned, device-mapped staging slots, reused once t
       hipError_t e = acquire(bytes, idx, p);
       if (e != hipSuccess) return e;
     }
+    reserved = bytes;
     return hipSuccess;
   }
-  // A host buffer of at least `bytes` whose previous copy has finished.
-  hipError_t acquire(size_t bytes, int& idx, uint8_t*& ptr) {
+  size_t reserved = 0;  // every slot holds at least this many bytes (set at creation)
+  // A host buffer of at least `bytes` whose previous copy has finished. may_grow = false: a slot
+  // too small is not reallocated (hipErrorOutOfMemory, nothing allocated): calls that may not
+  // allocate stay within the capacity reserved at creation.
+  hipError_t acquire(size_t bytes, int& idx, uint8_t*& ptr, bool may_grow = true) {
+    if (!may_grow && bytes > reserved) return hipErrorOutOfMemory;
     idx = next;
     next = (next + 1) % N;
     hipError_t e;
@@ -217,6 +222,7 @@ struct lmh_kv {
   std::vector<PageOp> pending;
   Uploader up;
   DevBuf part_buf, merge_buf;
+  uint8_t* scratch = nullptr;               // this device's copy of the no-allocation scratch
   // ---- per-call host scratch
   std::vector<int32_t> row_seq, row_pos;
   std::vector<DecodeItem> items;
@@ -437,10 +443,14 @@ struct lmh_kv {
     size_t i = 0;
     while (i < pending.size()) {
       if (pending[i].src < 0) {
+        // block ids in pieces no larger than a staging slot's reserved bytes, so flushing never
+        // grows the staging ring
         size_t j = i;
         std::vector<int32_t> zb;
         const int32_t w = pending[i].win;
-        while (j < pending.size() && pending[j].src < 0 && pending[j].win == w) zb.push_back(pending[j++].dst);
+        const size_t max_ids = std::max<size_t>(up.reserved / 4, 1);
+        while (j < pending.size() && pending[j].src < 0 && pending[j].win == w && zb.size() < max_ids)
+          zb.push_back(pending[j++].dst);
         int idx;
         uint8_t* h;
         if ((e = up.acquire(zb.size() * 4, idx, h)) != hipSuccess) return hip_fail(e, "staging");
@@ -460,14 +470,19 @@ struct lmh_kv {
     }
     pending.clear();
     // the block-table rows changed since the last upload (one copy spanning them)
+    // (in pieces of at most a staging slot's reserved bytes)
     auto upload = [&](DirtyRows& d, const std::vector<int32_t>& h_tab, int32_t* d_tab) -> int32_t {
       if (!d.any()) return LMH_OK;
-      int idx;
-      uint8_t* h;
       const size_t off = d.lo * bps, bytes = (d.hi - d.lo) * bps * 4;
-      if ((e = up.acquire(bytes, idx, h)) != hipSuccess) return hip_fail(e, "staging");
-      std::memcpy(h, h_tab.data() + off, bytes);
-      if ((e = up.send(idx, d_tab + off, bytes, st)) != hipSuccess) return hip_fail(e, "table upload");
+      const size_t piece = std::max<size_t>(up.reserved / 4 * 4, 4);
+      for (size_t done = 0; done < bytes; done += piece) {
+        const size_t n = std::min(piece, bytes - done);
+        int idx;
+        uint8_t* h;
+        if ((e = up.acquire(n, idx, h)) != hipSuccess) return hip_fail(e, "staging");
+        std::memcpy(h, (const uint8_t*)(h_tab.data() + off) + done, n);
+        if ((e = up.send(idx, (uint8_t*)(d_tab + off) + done, n, st)) != hipSuccess) return hip_fail(e, "table upload");
+      }
       d.clear();
       return LMH_OK;
     };
@@ -546,14 +561,19 @@ struct lmh_kv {
   // (a few dozen bytes per wave), so no copy has to run on the stream before them. The caller
   // enqueues every kernel that reads the slot, then calls release_rows(slot, stream).
   int32_t stage_rows(const void* extra, size_t extra_bytes, const void* extra2, size_t extra2_bytes,
-                     const int32_t*& d_rs, const int32_t*& d_rp, const uint8_t*& d_extra, int& slot) {
+                     const int32_t*& d_rs, const int32_t*& d_rp, const uint8_t*& d_extra, int& slot,
+                     bool may_grow = true) {
     const size_t nr = row_seq.size();
     const size_t rows_bytes = (nr * 8 + 255) / 256 * 256;
     const size_t extra_pad = (extra_bytes + 255) / 256 * 256;
     const size_t total = rows_bytes + extra_pad + extra2_bytes;
     hipError_t e;
     uint8_t* h;
-    if ((e = up.acquire(total, slot, h)) != hipSuccess) return hip_fail(e, "staging");
+    if (!may_grow && total > up.reserved)
+      return fail(LMH_INVALID_ARGUMENT, "the call's work list (" + std::to_string(total) +
+                                            " bytes) exceeds the staging capacity reserved at creation (" +
+                                            std::to_string(up.reserved) + " bytes)");
+    if ((e = up.acquire(total, slot, h, may_grow)) != hipSuccess) return hip_fail(e, "staging");
     std::memcpy(h, row_seq.data(), nr * 4);
     std::memcpy(h + nr * 4, row_pos.data(), nr * 4);
     if (extra_bytes) std::memcpy(h + rows_bytes, extra, extra_bytes);
@@ -798,7 +818,11 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   if (e == hipSuccess) e = hipMalloc((void**)&kv->d_table, std::max<uint64_t>(kv->h_table.size(), 1) * 4);
   if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wpool, kv->wpool_blocks * kv->wblock_bytes);
   if (e == hipSuccess && kv->window) e = hipMalloc((void**)&kv->d_wtable, kv->h_wtable.size() * 4);
-  if (e == hipSuccess) e = kv->up.reserve(std::max<size_t>(64 << 10, kv->bps * 4 * 16));
+  // staging slots sized for a call's work list (decode items, merges, prefill units: 1 MiB holds
+  // ~32 K decode items) and 16 block-table rows, so calls do not grow them
+  if (e == hipSuccess) e = kv->up.reserve(std::max<size_t>(1 << 20, kv->bps * 4 * 16));
+  // this device's copy of lmh_attend_noalloc's scratch (resolved once per device)
+  if (e == hipSuccess) e = noalloc_scratch(o->device, &kv->scratch);
   if (e != hipSuccess) {
     g_create_error = std::string("device allocation failed: ") + hipGetErrorString(e);
     delete kv;
@@ -1328,9 +1352,14 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
   return kv->release_rows(slot, st);
 }
 
-int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q, float* out,
-                   float scale, uint64_t window, void* stream) {
+// lmh_attend and lmh_attend_noalloc. noalloc: split-K partials and the merge list go to the
+// device's no-allocation scratch (the split target capped to what it holds, a call that still
+// needs more is refused), the staged work list must fit the staging capacity reserved at
+// creation, and no timing events are made or recorded: the call allocates nothing.
+static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
+                           float* out, float scale, uint64_t window, void* stream, bool noalloc) {
   if (!kv) return LMH_INVALID_ARGUMENT;
+  if (noalloc && !kv->scratch) return kv->fail(LMH_DEVICE_ERROR, "no-allocation scratch not resolved");
   if (layer >= kv->layers.size()) return kv->fail(LMH_INVALID_ARGUMENT, "layer out of range");
   if (!std::isfinite(scale)) return kv->fail(LMH_INVALID_ARGUMENT, "scale must be finite");
   uint64_t n_rows;
@@ -1402,8 +1431,11 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   // none waits for a slot to free up (a second, mostly empty round would double the kernel time).
   if (kv->decode_capacity[layer] == 0)
     kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd) * kv->n_cu;
-  const uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items
-                                                                     : kv->decode_capacity[layer], 1);
+  uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items
+                                                               : kv->decode_capacity[layer], 1);
+  // no-allocation calls: at most as many split slots (and merges) as the scratch holds
+  const size_t slot_bytes = (size_t)ng * (y.hdv + 4) * 4;
+  if (noalloc) target = std::max<uint64_t>(1, std::min<uint64_t>(target, NOALLOC_SCRATCH_BYTES / (slot_bytes + sizeof(MergeItem))));
   // Smallest chunk: 8 tiles for the matrix-core kernels (enough work per wave to stream at full
   // rate); 2 tiles for f32 rows, whose VALU kernel walks keys with dependent loads (latency-bound:
   // more, shorter items hide it better).
@@ -1464,11 +1496,27 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   int slot;
   hipError_t e;
   // the split partials' buffer first: growing it synchronises the device
+  float* part = (float*)kv->part_buf.p;
+  uint32_t* merge_dst = (uint32_t*)kv->merge_buf.p;
   if (slots > 0) {
-    if ((e = kv->part_buf.ensure((size_t)slots * ng * (y.hdv + 4) * 4)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
-    if ((e = kv->merge_buf.ensure(merges_bytes)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+    const size_t part_bytes = (size_t)slots * slot_bytes;
+    if (noalloc) {
+      const size_t part_pad = (part_bytes + 255) / 256 * 256;
+      if (part_pad + merges_bytes > NOALLOC_SCRATCH_BYTES)
+        return kv->fail(LMH_INVALID_ARGUMENT, "the call needs " + std::to_string(part_pad + merges_bytes) +
+                                                  " bytes of split-K scratch; lmh_attend_noalloc holds " +
+                                                  std::to_string(NOALLOC_SCRATCH_BYTES));
+      part = (float*)kv->scratch;
+      merge_dst = (uint32_t*)(kv->scratch + part_pad);
+    } else {
+      if ((e = kv->part_buf.ensure(part_bytes)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+      if ((e = kv->merge_buf.ensure(merges_bytes)) != hipSuccess) return kv->hip_fail(e, "hipMalloc");
+      part = (float*)kv->part_buf.p;
+      merge_dst = (uint32_t*)kv->merge_buf.p;
+    }
   }
-  if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot)) != LMH_OK) return rc;
+  if ((rc = kv->stage_rows(kv->payload.data(), kv->payload.size(), nullptr, 0, rs, rp, ex, slot, !noalloc)) != LMH_OK)
+    return rc;
   const PageGeom g = kv->geom(layer);
   RowGeom r{};
   r.row_seq = rs;
@@ -1484,40 +1532,55 @@ int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_s
   pg.scale_log2 = r.scale_log2;
   pg.window = r.window;
   pg.p_f16 = kv->prefill_p_f16 ? 1u : 0u;
-  const MergeCopy mc{(const uint32_t*)(ex + items_pad), (uint32_t*)kv->merge_buf.p,
+  const MergeCopy mc{(const uint32_t*)(ex + items_pad), merge_dst,
                      kv->merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
+  // timing events are made on first use: not on the no-allocation path
+  auto time_launch = [&](uint32_t kind, LaunchEv& ev) -> hipError_t {
+    ev = LaunchEv{};
+    return noalloc ? hipSuccess : kv->time_launch(kind, ev);
+  };
   // A mixed batch (prefill units and decode items) runs as one launch: the prefill workgroups
   // first (one per CU they reach), then the decode items, a wave each, on the CUs left free.
   const bool overlap = !kv->pitems.empty() && !kv->items.empty();
   LaunchEv ev;
   if (overlap) {
-    if ((e = kv->time_launch(LMH_KERNEL_MIXED, ev)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = time_launch(LMH_KERNEL_MIXED, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_mixed(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, r,
-                     (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st, ev);
+                     (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, part, mc, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "mixed kernel");
   }
   if (!overlap && !kv->pitems.empty()) {
-    if ((e = kv->time_launch(LMH_KERNEL_PREFILL, ev)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = time_launch(LMH_KERNEL_PREFILL, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_prefill(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, q, out,
                        st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
   }
   if (kv->items.empty()) return kv->release_rows(slot, st);
   if (!overlap) {
-    if ((e = kv->time_launch(LMH_KERNEL_DECODE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
-    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, (float*)kv->part_buf.p, mc, st,
+    if ((e = time_launch(LMH_KERNEL_DECODE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
+    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, part, mc, st,
                       ev);
     if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
   }
   if (!kv->merges.empty()) {
-    if ((e = kv->time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
+    if ((e = time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     uint32_t max_split = 0;
     for (const MergeItem& m : kv->merges) max_split = std::max(max_split, m.n_split);
-    e = launch_merge(r, y.hdv, (const MergeItem*)kv->merge_buf.p, (uint32_t)kv->merges.size(),
-                     (const float*)kv->part_buf.p, out, max_split, st, ev);
+    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->merges.size(),
+                     part, out, max_split, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
   }
   return kv->release_rows(slot, st);
+}
+
+int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q, float* out,
+                   float scale, uint64_t window, void* stream) {
+  return attend_impl(kv, layer, segs, n_segs, q, out, scale, window, stream, false);
+}
+
+int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
+                           float* out, float scale, uint64_t window, void* stream) {
+  return attend_impl(kv, layer, segs, n_segs, q, out, scale, window, stream, true);
 }
 
 int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {

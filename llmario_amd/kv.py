@@ -264,6 +264,14 @@ class HipKvCache:
                                        C.c_void_p(out.data_ptr()), float(scale), int(window or 0),
                                        _stream_ptr(stream)))
 
+    def attend_noalloc(self, layer: int, segs, q, out, scale: float, window: int = 0, stream=None):
+        """lmh_attend_noalloc: attend with nothing allocated (split-K scratch in the library's
+        per-device array); raises LmhError(INVALID_ARGUMENT) for a call that does not fit it."""
+        arr, n = _segs(segs)
+        self._check(N.lib().lmh_attend_noalloc(self.h, layer, arr, n, C.c_void_p(q.data_ptr()),
+                                               C.c_void_p(out.data_ptr()), float(scale), int(window or 0),
+                                               _stream_ptr(stream)))
+
     def set_tuning(self, *, prefill_p_f16: bool | None = None, prefill_min_rows: int | None = None,
                    decode_target_items: int | None = None, decode_min_tiles: int | None = None):
         """lmh_kv_set_tuning: change the given options, keep the others (0 = the default)."""

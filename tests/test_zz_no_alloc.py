@@ -1,0 +1,79 @@
+"""lmh_attend_noalloc (the entry point for callers that cannot allocate) through the C ABI: its
+outputs equal lmh_attend's on the same calls (decode with split-K, a mixed prefill + decode
+call, and a second, smaller call after a larger one on the same shared scratch), and a call that
+needs more split-K scratch than the library's per-device array holds is refused with
+INVALID_ARGUMENT and a message, having launched nothing."""
+
+import numpy as np
+import pytest
+
+from conftest import TOL, row_rel_err
+from llmario_amd import harness
+from llmario_amd.kv import HipKvCache, Layer, LmhError
+from llmario_amd.workloads import Generator, small
+
+pytestmark = pytest.mark.gpu
+
+
+def both(hc, w, q_np, segs=None, rows=None):
+    import torch
+    segs = segs or w.segments()
+    n = q_np.shape[0]
+    q = torch.from_numpy(np.ascontiguousarray(q_np)).cuda()
+    a = torch.full((n, w.layer.n_head, w.layer.hdv), float("nan"), device="cuda")
+    b = torch.full_like(a, float("nan"))
+    hc.attend(0, segs, q, a, w.scale, w.window)
+    hc.attend_noalloc(0, segs, q, b, w.scale, w.window)
+    torch.cuda.synchronize()
+    return a.cpu().numpy(), b.cpu().numpy()
+
+
+@pytest.mark.parametrize("kv", ["f16", "q8_0"])
+def test_noalloc_matches_attend_twice_second_smaller(cuda, kv):
+    # decode rows long enough to split (partials and merges in the scratch)
+    w = small("na", kv, Layer(32, 8, 128, 128), prior=[3000, 1700, 640, 4090], new=[1, 1, 1, 1], seed=3)
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    q = gen.q()
+    for call, rows in enumerate([4, 2]):          # the second call is smaller
+        segs = [sg for sg in w.segments()][:rows]
+        a, b = both(hc, w, q[:rows], segs)
+        assert np.isfinite(b).all()
+        err = row_rel_err(b, a)
+        print(f"{kv} call {call} ({rows} rows): noalloc vs attend {err:.3e}, identical={np.array_equal(a, b)}")
+        assert err <= TOL[kv], err
+        assert np.array_equal(a, b)   # same plan, same kernels: the same bits
+
+
+def test_noalloc_mixed_call_matches(cuda):
+    w = small("nam", "bf16", Layer(32, 8, 128, 128), prior=[2500, 0, 900], new=[1, 200, 1], seed=4)
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    q = gen.q()
+    a, b = both(hc, w, q)
+    err = row_rel_err(b, a)
+    print(f"mixed: noalloc vs attend {err:.3e}")
+    assert err <= TOL["bf16"] and np.array_equal(a, b)
+
+
+def test_noalloc_refuses_a_call_beyond_its_scratch(cuda):
+    import torch
+    # group 16 (16 heads per item) and 32 rows x 8 KV heads x 16 splits of 1024 keys: 4096 split
+    # slots of 8448 bytes, more than the 32 MiB scratch
+    L = Layer(128, 8, 128, 128)
+    ctx = 16384
+    hc = HipKvCache([L], max_ctx=ctx, n_seqs=32, kv_type="f16", block_tokens=16)
+    segs_l, n = hc.prepare_batch([(s, ctx) for s in range(32)])
+    hc.commit_batch(segs_l)
+    segs = [(s, s, 1, ctx - 1) for s in range(32)]
+    q = torch.zeros((32, 128, 128), device="cuda")
+    out = torch.full((32, 128, 128), 7.0, device="cuda")
+    with pytest.raises(LmhError) as ei:
+        hc.attend_noalloc(0, segs, q, out, 0.1, 0)
+    assert "INVALID_ARGUMENT" in str(ei.value) and "scratch" in str(ei.value)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())          # nothing ran
+    # the same call through lmh_attend allocates its partials and runs
+    hc.attend(0, segs, q, out, 0.1, 0)
+    torch.cuda.synchronize()
+    assert np.isfinite(out.cpu().numpy()).all()
