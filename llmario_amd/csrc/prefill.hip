@@ -75,6 +75,20 @@ __device__ inline uint32_t bf2_to_h2(uint32_t w) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
 }
 
+// Weights (a, b) as packed f16 hi parts and packed f16 lo parts (a - hi, b - hi), the lo parts each
+// one exact fma rounded once to f16 (v_fma_mix{lo,hi}_f16 read the f16 hi operand directly):
+// three instructions per pair instead of converting hi back to f32 and subtracting.
+__device__ inline void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const f2 v = {a, b};
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+  uint32_t l;
+  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l) : "v"(hi), "v"(a));
+  asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(l) : "v"(hi), "v"(b));
+  lo = l;
+}
+
 // Workgroup `wg` of a prefill launch: its list of units, items[wg * per_wg ..]. PLO: P carried
 // past f16 as hi + lo halves (two P.V products on the same V operand); without it P is rounded
 // to f16, the precision of the Metal sibling's prefill.
@@ -133,23 +147,50 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   const uint32_t my_tile = w >> 1, my_row = (w & 1) * (TILE / 2);   // f16: both sides
   const uint64_t k_head = g.k_off + (uint64_t)it.kvh * g.k_head;
   const uint64_t v_head = g.v_off + (uint64_t)it.kvh * g.v_head;
-  // block base and 16-token sub-tile index of page tile `tile` of tile ti
-  // (tiles 0 and 1 take their block ids from the unit descriptor, before the list is in LDS)
-  auto page = [&](uint32_t ti, uint32_t tile, const uint8_t*& base, uint32_t& sub) {
-    const uint32_t p = min(ti * 4 + tile, n_pages - 1);
-    const uint32_t id = ti < 2 ? units[unit].blk[ti * 4 + tile] : (uint32_t)blk_lds[p];
-    const uint64_t blk = (uint32_t)__builtin_amdgcn_readfirstlane(id);
-    sub = (((page0 + p) << 4) & ((1u << g.bt_shift) - 1u)) >> 4;
-    base = g.pool + blk * g.block_bytes;
+  // Scalar base address of page tile `tile` of tile ti, K side or V side. Tiles 0 and 1 take
+  // their block ids from the unit descriptor (the block-id list is not in LDS yet). Later tiles
+  // read lane-held addresses: lane i holds the K and V base of page 64c + i of the unit's range
+  // (clamped to its last page) for the current 64-page chunk c, computed from the block-id list
+  // once per 16 tiles, so a DMA costs two readlanes instead of an LDS read that waits for every
+  // LDS operation in flight (the operand reads of the tile being computed among them).
+  const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
+  uint32_t pk_lo = 0, pk_hi = 0, pv_lo = 0, pv_hi = 0, chunk = ~0u;
+  auto load_chunk = [&](uint32_t c) {
+    const uint32_t p = min(c * 64 + lane, n_pages - 1);
+    const uint64_t b = (uint64_t)(uintptr_t)g.pool + (uint64_t)(uint32_t)blk_lds[p] * g.block_bytes;
+    const uint32_t sub = (((page0 + p) << 4) & bt_mask) >> 4;
+    const uint64_t kb = b + k_head + (uint64_t)sub * g.k_tile, vb = b + v_head + (uint64_t)sub * g.v_tile;
+    pk_lo = (uint32_t)kb;
+    pk_hi = (uint32_t)(kb >> 32);
+    pv_lo = (uint32_t)vb;
+    pv_hi = (uint32_t)(vb >> 32);
+    chunk = c;
+  };
+  auto page_any = [&](uint32_t ti, uint32_t tile, bool v_side) -> const uint8_t* {
+    if (ti < 2) {
+      const uint32_t p = min(ti * 4 + tile, n_pages - 1);
+      const uint64_t blk = (uint32_t)__builtin_amdgcn_readfirstlane(units[unit].blk[ti * 4 + tile]);
+      const uint32_t sub = (((page0 + p) << 4) & bt_mask) >> 4;
+      return g.pool + blk * g.block_bytes + (v_side ? v_head + (uint64_t)sub * g.v_tile : k_head + (uint64_t)sub * g.k_tile);
+    }
+    const uint32_t p = ti * 4 + tile;
+    if ((p >> 6) != chunk) load_chunk(p >> 6);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane(v_side ? pv_lo : pk_lo, (int)(p & 63u));
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane(v_side ? pv_hi : pk_hi, (int)(p & 63u));
+    return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  };
+  auto page = [&](uint32_t ti, uint32_t tile, bool v_side) -> const uint8_t* {
+    const uint8_t* a = page_any(ti, tile, v_side);
+    const uint64_t u = (uint64_t)(uintptr_t)a;   // wave-uniform: kept in scalar registers
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
   };
   auto issue = [&](uint32_t ti) {
     uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
-    const uint8_t* base;
-    uint32_t sub;
     if constexpr (!PAIR_V) {
-      page(ti, my_tile, base, sub);
-      const uint8_t* kb = base + k_head + sub * g.k_tile;
-      const uint8_t* vb = base + v_head + sub * g.v_tile;
+      const uint8_t* kb = page(ti, my_tile, false);
+      const uint8_t* vb = page(ti, my_tile, true);
 #pragma unroll
       for (int k = 0; k < CPT; k++) {
         lds_dma16(kb, my_row + k * 1024 + lane * 16, stage + my_tile * TILE + my_row + k * 1024);
@@ -158,18 +199,15 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       return;
     }
     if (do_k) {
-      page(ti, k_tile, base, sub);
-      const uint8_t* kb = base + k_head + sub * g.k_tile;
+      const uint8_t* kb = page(ti, k_tile, false);
       lds_dma16(kb, k_row + lane * 16, stage + k_tile * TILE + k_row);
       lds_dma16(kb, k_row + 1024 + lane * 16, stage + k_tile * TILE + k_row + 1024);
     }
     if (do_v) {
 #pragma unroll
       for (int t2 = 0; t2 < 2; t2++) {
-        const uint32_t tile = 2 * v_half + t2;
-        page(ti, tile, base, sub);
-        const uint8_t* vb = base + v_head + sub * g.v_tile;
-        lds_dma16(vb, v_row + lane * 16, stage + 4 * TILE + tile * TILE + v_row);
+        const uint8_t* vb = page(ti, 2 * v_half + t2, true);
+        lds_dma16(vb, v_row + lane * 16, stage + 4 * TILE + (2 * v_half + t2) * TILE + v_row);
       }
     }
   };
@@ -179,10 +217,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // rewritten as A' = [A keys of d | B keys of d] and B' = [A keys of d+16 | B keys of d+16], so
   // one 16-byte read is a whole 32-key operand of the P.V product. f16 tiles are used as loaded
   // (the extra LDS pass would cost more than the operand assembly it saves).
+  bool widen_k = true;   // bf16 pages: false while the unit's Q.K products run on bf16 (below)
   auto settle = [&](uint32_t ti) {
     uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
     if constexpr (KVT == KV_BF16) {
-      if (do_k) {
+      if (do_k && widen_k) {
 #pragma unroll
         for (int r = 0; r < 2; r++) {
           uint4* p = (uint4*)(stage + k_tile * TILE + k_row + r * 1024 + lane * 16);
@@ -249,6 +288,27 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     }
     return nz;
   };
+  // bf16 pages: a Q held in bf16 values multiplies bf16 K exactly on the bf16 matrix cores, so K
+  // needs no widening; qf then holds bf16 bits (split_q_bf16). Any other Q takes the two-pass f16
+  // hi + lo path with K widened.
+  auto split_q_bf16 = [&](const float4 (&raw)[NC][2], h8 (&hi)[NC]) {
+    bool nz = false;
+#pragma unroll
+    for (int ch = 0; ch < NC; ch++) {
+      const float4 a = raw[ch][0], b = raw[ch][1];
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      uint32_t wd[4];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const uint16_t h0 = dtile::bf16_rne(x[i]), h1 = dtile::bf16_rne(x[i + 1]);
+        nz |= __uint_as_float((uint32_t)h0 << 16) != x[i];
+        nz |= __uint_as_float((uint32_t)h1 << 16) != x[i + 1];
+        wd[i / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+      }
+      hi[ch] = __builtin_bit_cast(h8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
+    }
+    return nz;
+  };
   h8 qf[2][NC];
   if (pass == 0) {
     bool lo_need = false;
@@ -259,9 +319,14 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       // ---- block ids of every key page this unit reads
       const int32_t* tab = g.table + (size_t)it.seq * g.bps;
       for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
-      h8 lo_unused[NC];   // the lo parts are only tested here
-      lo_need |= split_q(raw[0], qf[0], lo_unused);
-      lo_need |= split_q(raw[1], qf[1], lo_unused);
+      if constexpr (KVT == KV_BF16) {
+        lo_need |= split_q_bf16(raw[0], qf[0]);
+        lo_need |= split_q_bf16(raw[1], qf[1]);
+      } else {
+        h8 lo_unused[NC];   // the lo parts are only tested here
+        lo_need |= split_q(raw[0], qf[0], lo_unused);
+        lo_need |= split_q(raw[1], qf[1], lo_unused);
+      }
     }
     // workgroup-wide OR of the lo flags: one word per wave (written by its first lane) behind a
     // barrier (which also publishes the block-id list)
@@ -276,6 +341,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     for (int i = 0; i < PW; i++) lo_or |= lo_flags[i];
     lo_any = lo_or != 0;
   }
+  widen_k = KVT != KV_BF16 || lo_any;
   if (lo_any) {   // column block `pass` of each wave: its Q as hi (qf[0]) + lo (qf[1])
     float4 raw[NC][2];
     load_q(w * COLS + pass * 16 + hq, raw);
@@ -373,7 +439,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
           for (int cb = 0; cb < NCB; cb++) {
             const f4 acc = ch == 0 ? nmv[cb] : S[kk][cb];
-            S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], acc, 0, 0, 0);
+            if constexpr (KVT == KV_BF16)   // bf16 K as loaded, bf16 Q
+              S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(dtile::b8, ko.a[ch][kk]),
+                                                                 __builtin_bit_cast(dtile::b8, qf[cb][ch]), acc, 0, 0, 0);
+            else
+              S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], acc, 0, 0, 0);
           }
         }
       }
@@ -454,12 +524,21 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
     for (int x = 0; x < NX; x++) {
       l[x] += ps[x];
+      uint32_t hw[4], lw[4];
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const _Float16 h = (_Float16)pw[x][i];
-        Ph[x][i] = h;
-        if constexpr (PLO) Pl[x][i] = (_Float16)(pw[x][i] - (float)h);
+      for (int i = 0; i < 4; i++) {
+        if constexpr (PLO) {
+          split_pair(pw[x][2 * i], pw[x][2 * i + 1], hw[i], lw[i]);
+        } else {
+          typedef float f2 __attribute__((ext_vector_type(2)));
+          typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+          const f2 v = {pw[x][2 * i], pw[x][2 * i + 1]};
+          hw[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
+          lw[i] = 0;
+        }
       }
+      Ph[x] = __builtin_bit_cast(h8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+      Pl[x] = __builtin_bit_cast(h8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
     }
   };
   // O^T += V^T P^T over a half, 32 keys per MFMA
