@@ -13,12 +13,18 @@
  * the device work of one handle must be stream-ordered: issue it on one stream, or order the
  * streams yourself.
  *
- * Page layout: blocks of `block_tokens` positions (a multiple of 16), each holding every layer's
- * K then V for those positions, as the reference's block does (kv.rs:286-324, 402-497); inside a
- * block each (layer, KV head) owns a contiguous region whose bytes are in the order the decode
- * and prefill kernels' matrix-core operands want them (so one 16-byte load per lane per operand
- * chunk reads 1 KiB contiguous per wave). Block ids, reference counts and the LRU free queue follow BlockPool
- * (kv/src/lib.rs:36-176), so block tables and page indices match the reference bit for bit.
+ * Page layout: blocks of `block_tokens` positions (any power of two, kv.rs:402-406), each holding
+ * every layer's K then V for those positions, as the reference's block does (kv.rs:286-324,
+ * 402-497), with the same bytes per block; inside a block each (layer, KV head) owns a contiguous
+ * region. For the geometries with a matrix-core decode instance (f16 / bf16 head widths 32, 64, 96,
+ * 128, 192, 256 and 192 / 128; q8_0 64, 128, 192, 256; f32 64, 128, 256) on blocks of at least 16
+ * positions, its bytes are in the order the kernels' operands want them (one 16-byte load per lane
+ * per operand chunk reads 1 KiB contiguous per wave); every other geometry the reference accepts
+ * (any widths up to 512, q8_0 multiples of 32, hd != hdv, blocks under 16 positions) keeps
+ * row-major rows in the reference's row encoding, read by a VALU kernel (as Metal's
+ * attn_vec_generic covers widths off its instances). Block ids, reference counts and the LRU free
+ * queue follow BlockPool (kv/src/lib.rs:36-176), so block tables and page indices match the
+ * reference bit for bit.
  */
 #ifndef LLMARIO_HIP_H
 #define LLMARIO_HIP_H
@@ -258,7 +264,8 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
  *     (default 16; 1 .. 2^32).
  *   decode_target_items: split-K target of decode work items (default: the items the device holds
  *     at once, from the occupancy query).
- *   decode_min_tiles: smallest split-K chunk in 16-key tiles (default 8; 2 for f32 pages; 1 .. 64).
+ *   decode_min_tiles: smallest split-K chunk in 16-key tiles (default 8; 2 for f32 pages; 4 for
+ *     row-layout layers; 1 .. 64).
  * Out-of-range values fail with LMH_INVALID_ARGUMENT and change nothing. */
 typedef struct lmh_attend_tuning {
   uint32_t abi_version;        /* LMH_ABI_VERSION */

@@ -37,13 +37,14 @@ using namespace dtile;
 constexpr int WAVES = 4;  // waves (work items) per workgroup
 
 // Waves per SIMD the register allocator must allow: two tile buffers in flight per wave fit in
-// 256 VGPRs up to hd 128 (2 waves/SIMD); hd 256 needs the whole file (1 wave/SIMD).
+// 256 VGPRs up to hd 128 (and 192 / 128) (2 waves/SIMD); hd 256 and 192 / 192 need the whole
+// file (1 wave/SIMD).
 #ifndef LMH_DECODE_WPE
 #define LMH_DECODE_WPE 2
 #endif
-template <int HD>
+template <int HD, int HDV>
 constexpr int waves_per_eu() {
-  return HD >= 256 ? 1 : LMH_DECODE_WPE;
+  return (HD >= 256 || (HD >= 192 && HDV >= 192)) ? 1 : LMH_DECODE_WPE;
 }
 
 // Split-K merge (forward.rs:772-806), one wave per (task, query head), lanes over dims:
@@ -51,20 +52,19 @@ constexpr int waves_per_eu() {
 // A separate launch: the kernel boundary makes every split's partials visible across XCDs.
 // GROUPS: some item has more than 16 splits (rows past the first 16 are loaded in groups of 16;
 // without it the kernel keeps the lighter code that a call with at most 16 splits per item runs).
-template <int HDV, bool GROUPS>
-__global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* items, uint32_t n_items,
+template <int NP, bool GROUPS>
+__global__ __launch_bounds__(256) void merge_kernel(RowGeom r, uint32_t hdv, const MergeItem* items, uint32_t n_items,
                                                     const float* part, float* out) {
-  constexpr int ND = (HDV + 63) / 64;
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (wi >= n_items * r.ng) return;
   const MergeItem mi = items[wi / r.ng];
   const uint32_t h = wi % r.ng;
   if (mi.h0 + h >= r.group) return;
-  static_assert(HDV % 64 == 0, "two or more dims per lane");
-  constexpr int NP = HDV / 64;  // dims per lane, loaded as one NP-wide vector
-  const size_t stride = (size_t)r.ng * (HDV + 4);
-  const float* base = part + (size_t)mi.slot0 * stride + (size_t)h * (HDV + 4);
+  // lane L folds dims L*NP .. L*NP+NP-1 (NP = ceil(hdv / 64); lanes past hdv idle)
+  const bool lane_on = lane * NP < hdv;
+  const size_t stride = (size_t)r.ng * (hdv + 4);
+  const float* base = part + (size_t)mi.slot0 * stride + (size_t)h * (hdv + 4);
   float acc[NP];
 #pragma unroll
   for (int i = 0; i < NP; i++) acc[i] = 0.f;
@@ -77,16 +77,15 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
     const uint32_t n = (mi.n_split - s0) < 64u ? (mi.n_split - s0) : 64u;
     float ms = -INFINITY, ls = 0.f;
     if (s < mi.n_split) {
-      const float2 ml = *(const float2*)(base + s * stride + HDV);
-      ms = ml.x;
-      ls = ml.y;
+      ms = base[s * stride + hdv];   // separate loads: (m, l) are 8-byte aligned only for even hdv
+      ls = base[s * stride + hdv + 1];
     }
     float pre[16][NP];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
       const float* pp = base + (s0 + ((uint32_t)k < n ? k : 0)) * stride + lane * NP;
 #pragma unroll
-      for (int i = 0; i < NP; i++) pre[k][i] = pp[i];
+      for (int i = 0; i < NP; i++) pre[k][i] = lane_on && lane * NP + i < hdv ? pp[i] : 0.f;
     }
     float Mr = ms;
     for (int x = 32; x >= 1; x >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, x));
@@ -118,7 +117,7 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
           const uint32_t row = k0 + 16 + k < n ? k0 + 16 + k : k0 + 16;
           const float* pp = base + (s0 + row) * stride + lane * NP;
 #pragma unroll
-          for (int i = 0; i < NP; i++) nxt[k][i] = pp[i];
+          for (int i = 0; i < NP; i++) nxt[k][i] = lane_on && lane * NP + i < hdv ? pp[i] : 0.f;
         }
       }
 #pragma unroll
@@ -136,13 +135,14 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, const MergeItem* 
     }
   }
   const float inv = L > 0.f ? 1.0f / L : 0.f;
-  float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h) * HDV + lane * NP;
+  float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h) * hdv + lane * NP;
 #pragma unroll
-  for (int i = 0; i < NP; i++) op[i] = acc[i] * inv;
+  for (int i = 0; i < NP; i++)
+    if (lane_on && lane * NP + i < hdv) op[i] = acc[i] * inv;
 }
 
 template <int KVT, int HD, int HDV>
-__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD>(), waves_per_eu<HD>())))
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD, HDV>(), waves_per_eu<HD, HDV>())))
 void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q, float* out,
                         float* part, MergeCopy mc) {
   const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
@@ -316,6 +316,151 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
   }
 }
 
+// ---- row layout (any head widths up to 512, hd != hdv, blocks under 16 positions): VALU ------
+// One wave per item (row, KV head, up to RNG heads of the group, key range), the reference's
+// row encoding read directly: per 64-key chunk, lane = key for Q.K (each lane walks its key's row,
+// Q broadcast from LDS), lane = dim for P.V (each key's V row read across the lanes), fp32
+// throughout, online softmax in the log2 domain as the other decode kernels.
+constexpr int RNG = 4;                 // heads per item
+constexpr uint32_t ROWS_MAX_DIM = 512;
+
+template <int KVT>
+__device__ inline float row_elem(const uint8_t* row, uint32_t d) {
+  if constexpr (KVT == KV_F16) return h_to_f(((const uint16_t*)row)[d]);
+  else if constexpr (KVT == KV_BF16) return __uint_as_float((uint32_t)((const uint16_t*)row)[d] << 16);
+  else if constexpr (KVT == KV_F32) return ((const float*)row)[d];
+  else return (float)(int8_t)row[d];   // q8_0 code (the caller applies the block scale)
+}
+
+template <int KVT>
+__global__ __launch_bounds__(64 * WAVES) void decode_rows_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
+                                                                 uint32_t n_items, const float* q, float* out,
+                                                                 float* part, MergeCopy mc) {
+  constexpr uint32_t ES = KVT == KV_F32 ? 4 : KVT == KV_Q8 ? 1 : 2;   // bytes per value (q8_0: code)
+  __shared__ float qs[WAVES][RNG][ROWS_MAX_DIM];
+  __shared__ float ps[WAVES][RNG][64];
+  const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
+  const uint32_t wi = blockIdx.x * WAVES + w;
+  copy_merges(mc, blockIdx.x == 0);
+  if (wi >= n_items) return;   // no block-wide barrier below: each wave works alone
+  const DecodeItem it = items[wi];
+  const uint32_t hd = g.hd, hdv = g.hdv;
+  const uint32_t nh = (it.h0 + r.ng <= r.group) ? r.ng : r.group - it.h0;   // heads of this item (<= RNG)
+  for (uint32_t e = lane; e < nh * hd; e += 64) {
+    const uint32_t h = e / hd, d = e % hd;
+    qs[w][h][d] = q[((size_t)it.row * r.n_head + it.kvh * r.group + it.h0 + h) * hd + d];
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const int32_t* tab = g.table + (size_t)it.seq * g.bps;
+  const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
+  const uint32_t nd = (hdv + 63) / 64;   // V dims per lane in P.V (<= 8)
+  float m[RNG], l[RNG], o[RNG][ROWS_MAX_DIM / 64];
+#pragma unroll
+  for (int h = 0; h < RNG; h++) {
+    m[h] = -INFINITY;
+    l[h] = 0.f;
+#pragma unroll
+    for (int i = 0; i < (int)(ROWS_MAX_DIM / 64); i++) o[h][i] = 0.f;
+  }
+  // byte offsets of a key's K / V row (codes) and q8_0 scale rows inside its block
+  auto k_at = [&](int blk, uint32_t key, const uint8_t*& row, const uint8_t*& sc) {
+    const uint32_t ib = key & bt_mask;
+    const uint8_t* head = g.pool + (size_t)blk * g.block_bytes + g.k_off + it.kvh * g.k_head;
+    row = head + (ib >> 4) * g.k_tile + (ib & 15u) * hd * ES;
+    sc = head + g.k_scale + (ib >> 4) * g.k_tile_s + (ib & 15u) * (hd / 32) * 2;
+  };
+  auto v_at = [&](int blk, uint32_t key, const uint8_t*& row, const uint8_t*& sc) {
+    const uint32_t ib = key & bt_mask;
+    const uint8_t* head = g.pool + (size_t)blk * g.block_bytes + g.v_off + it.kvh * g.v_head;
+    row = head + (ib >> 4) * g.v_tile + (ib & 15u) * hdv * ES;
+    sc = head + g.v_scale + (ib >> 4) * g.v_tile_s + (ib & 15u) * (hdv / 32) * 2;
+  };
+  for (uint32_t c0 = it.p0; c0 < it.p1; c0 += 64) {
+    const uint32_t key = c0 + lane;
+    const bool valid = key < it.p1;
+    const uint32_t kk = valid ? key : it.p0;
+    const int blk = tab[kk >> g.bt_shift];
+    const uint32_t nk = (it.p1 - c0) < 64u ? (it.p1 - c0) : 64u;
+    const uint8_t *krow, *ksc;
+    k_at(blk, kk, krow, ksc);
+    float s[RNG] = {0.f, 0.f, 0.f, 0.f};
+    // Q.K over 32-dim blocks (q8_0: one scale per block) and a tail of hd % 32 dims
+    for (uint32_t d0 = 0; d0 < hd; d0 += 32) {
+      const uint32_t dn = hd - d0 < 32u ? hd - d0 : 32u;
+      float b[RNG] = {0.f, 0.f, 0.f, 0.f};
+      for (uint32_t d = 0; d < dn; d++) {
+        const float kx = row_elem<KVT>(krow, d0 + d);
+#pragma unroll
+        for (int h = 0; h < RNG; h++) b[h] = fmaf(qs[w][h][d0 + d], kx, b[h]);
+      }
+      const float ksc_b = KVT == KV_Q8 ? h_to_f(((const uint16_t*)ksc)[d0 / 32]) : 1.0f;
+#pragma unroll
+      for (int h = 0; h < RNG; h++) s[h] = fmaf(b[h], ksc_b, s[h]);
+    }
+#pragma unroll
+    for (int h = 0; h < RNG; h++) {
+      if (h >= (int)nh) break;
+      const float sc = valid ? s[h] * r.scale_log2 : -INFINITY;
+      float cm = sc;
+      for (int x = 32; x >= 1; x >>= 1) cm = fmaxf(cm, __shfl_xor(cm, x));
+      const float mn = fmaxf(m[h], cm);
+      const float alpha = exp2_fast(m[h] - mn);
+      const float p = exp2_fast(sc - mn);
+      float ssum = p;
+      for (int x = 32; x >= 1; x >>= 1) ssum += __shfl_xor(ssum, x);
+      l[h] = l[h] * alpha + ssum;
+      m[h] = mn;
+#pragma unroll
+      for (int i = 0; i < (int)(ROWS_MAX_DIM / 64); i++) o[h][i] *= alpha;
+      ps[w][h][lane] = p;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (uint32_t j = 0; j < nk; j++) {
+      const int bj = __builtin_amdgcn_readlane(blk, (int)j);   // lane j resolved key c0 + j's block
+      const uint8_t *vrow, *vsc;
+      v_at(bj, c0 + j, vrow, vsc);
+#pragma unroll
+      for (int i = 0; i < (int)(ROWS_MAX_DIM / 64); i++) {
+        const uint32_t d = lane + 64 * i;
+        if ((uint32_t)i < nd && d < hdv) {
+          float vx = row_elem<KVT>(vrow, d);
+          if constexpr (KVT == KV_Q8) vx *= h_to_f(((const uint16_t*)vsc)[d / 32]);
+#pragma unroll
+          for (int h = 0; h < RNG; h++)
+            if (h < (int)nh) o[h][i] = fmaf(ps[w][h][j], vx, o[h][i]);
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+#pragma unroll
+  for (int h = 0; h < RNG; h++) {
+    if (h >= (int)nh) break;
+    if (it.slot == NO_SLOT) {
+      float* op = out + ((size_t)it.row * r.n_head + it.kvh * r.group + it.h0 + h) * hdv;
+      const float inv = 1.0f / l[h];
+#pragma unroll
+      for (int i = 0; i < (int)(ROWS_MAX_DIM / 64); i++)
+        if (lane + 64 * i < hdv) op[lane + 64 * i] = o[h][i] * inv;
+    } else {
+      float* pp = part + ((size_t)it.slot * r.ng + h) * (hdv + 4);
+#pragma unroll
+      for (int i = 0; i < (int)(ROWS_MAX_DIM / 64); i++)
+        if (lane + 64 * i < hdv) pp[lane + 64 * i] = o[h][i];
+      if (lane == 0) {
+        pp[hdv] = m[h];
+        pp[hdv + 1] = l[h];
+      }
+    }
+  }
+}
+
 template <int KVT, int HD, int HDV>
 hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
@@ -334,34 +479,93 @@ hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* ite
   return hipGetLastError();
 }
 
+// The matrix-core (and f32) decode instances; any other geometry reads the row layout.
+#define LMH_TILE_GEOMS_MFMA(X) X(32, 32) X(64, 64) X(96, 96) X(128, 128) X(192, 192) X(256, 256) X(192, 128)
+#define LMH_TILE_GEOMS_Q8(X) X(64, 64) X(128, 128) X(192, 192) X(256, 256)
+#define LMH_TILE_GEOMS_F32(X) X(64, 64) X(128, 128) X(256, 256)
+
 template <int KVT>
 hipError_t dispatch_hd(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
                        const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
-  if (g.hd == 64 && g.hdv == 64) return launch_one<KVT, 64, 64>(g, r, items, n_items, q, out, part, mc, s, ev);
-  if (g.hd == 128 && g.hdv == 128) return launch_one<KVT, 128, 128>(g, r, items, n_items, q, out, part, mc, s, ev);
-  if (g.hd == 256 && g.hdv == 256) return launch_one<KVT, 256, 256>(g, r, items, n_items, q, out, part, mc, s, ev);
+#define LMH_HD(H, V) \
+  if (g.hd == H && g.hdv == V) return launch_one<KVT, H, V>(g, r, items, n_items, q, out, part, mc, s, ev);
+  if constexpr (KVT == KV_F32) {
+    LMH_TILE_GEOMS_F32(LMH_HD)
+  } else if constexpr (KVT == KV_Q8) {
+    LMH_TILE_GEOMS_Q8(LMH_HD)
+  } else {
+    LMH_TILE_GEOMS_MFMA(LMH_HD)
+  }
+#undef LMH_HD
   return hipErrorInvalidValue;
 }
 
-}  // namespace
+template <int KVT>
+hipError_t launch_rows(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
+                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
+  if (g.hd > ROWS_MAX_DIM || g.hdv > ROWS_MAX_DIM || r.ng > (uint32_t)RNG) return hipErrorInvalidValue;
+  const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
+  LMH_LAUNCH(ev, (decode_rows_kernel<KVT>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
+  return hipGetLastError();
+}
 
-namespace {
-template <int KVT, int HD>
-uint32_t resident_t() {
+// Work items (waves) one CU holds at once, from the occupancy of the instance a launch picks.
+template <int KVT, int HD, int HDV>
+uint32_t resident_t(uint32_t group) {
   int blocks = 0;
   hipError_t e;
-  if constexpr (KVT == KV_F32)
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HD, 16>, 64 * WAVES, 0);
-  else
-    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_mfma_kernel<KVT, HD, HD>, 64 * WAVES, 0);
+  if constexpr (KVT == KV_F32) {
+    switch (group) {   // the instance launch_one picks for this group
+      case 1: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HDV, 1>, 64 * WAVES, 0); break;
+      case 2: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HDV, 2>, 64 * WAVES, 0); break;
+      case 4: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HDV, 4>, 64 * WAVES, 0); break;
+      case 8: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HDV, 8>, 64 * WAVES, 0); break;
+      default: e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_f32_kernel<HD, HDV, 16>, 64 * WAVES, 0); break;
+    }
+  } else {
+    e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_mfma_kernel<KVT, HD, HDV>, 64 * WAVES, 0);
+  }
   return (e == hipSuccess && blocks > 0) ? (uint32_t)blocks * WAVES : WAVES;
 }
+
 template <int KVT>
-uint32_t resident_hd(uint32_t hd) {
-  if (hd == 64) return resident_t<KVT, 64>();
-  if (hd == 128) return resident_t<KVT, 128>();
-  return resident_t<KVT, 256>();
+uint32_t resident_rows() {
+  int blocks = 0;
+  const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, decode_rows_kernel<KVT>, 64 * WAVES, 0);
+  return (e == hipSuccess && blocks > 0) ? (uint32_t)blocks * WAVES : WAVES;
 }
+
+template <int KVT>
+uint32_t resident_geom(uint32_t hd, uint32_t hdv, uint32_t group, uint32_t layout) {
+  if (layout == LAYOUT_ROWS) return resident_rows<KVT>();
+#define LMH_RES(H, V) \
+  if (hd == H && hdv == V) return resident_t<KVT, H, V>(group);
+  if constexpr (KVT == KV_F32) {
+    LMH_TILE_GEOMS_F32(LMH_RES)
+  } else if constexpr (KVT == KV_Q8) {
+    LMH_TILE_GEOMS_Q8(LMH_RES)
+  } else {
+    LMH_TILE_GEOMS_MFMA(LMH_RES)
+  }
+#undef LMH_RES
+  return resident_rows<KVT>();
+}
+
+template <int KVT>
+bool tiles_geom(uint32_t hd, uint32_t hdv) {
+#define LMH_HAS(H, V) \
+  if (hd == H && hdv == V) return true;
+  if constexpr (KVT == KV_F32) {
+    LMH_TILE_GEOMS_F32(LMH_HAS)
+  } else if constexpr (KVT == KV_Q8) {
+    LMH_TILE_GEOMS_Q8(LMH_HAS)
+  } else {
+    LMH_TILE_GEOMS_MFMA(LMH_HAS)
+  }
+#undef LMH_HAS
+  return false;
+}
+
 }  // namespace
 
 // ---- scratch of lmh_attend_noalloc --------------------------------------------------------------
@@ -394,25 +598,40 @@ hipError_t noalloc_scratch(int device, uint8_t** out) {
   return hipSuccess;
 }
 
-uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd) {
+uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group, uint32_t layout) {
   switch (kv_type) {
-    case KV_F16: return resident_hd<KV_F16>(hd);
-    case KV_BF16: return resident_hd<KV_BF16>(hd);
-    case KV_Q8: return resident_hd<KV_Q8>(hd);
-    default: return resident_hd<KV_F32>(hd);
+    case KV_F16: return resident_geom<KV_F16>(hd, hdv, group, layout);
+    case KV_BF16: return resident_geom<KV_BF16>(hd, hdv, group, layout);
+    case KV_Q8: return resident_geom<KV_Q8>(hd, hdv, group, layout);
+    default: return resident_geom<KV_F32>(hd, hdv, group, layout);
   }
 }
 
-bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
-  if (hd != hdv) return false;
-  if (hd != 64 && hd != 128 && hd != 256) return false;
-  return kv_type <= KV_BF16;
+bool decode_tiles_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
+  switch (kv_type) {
+    case KV_F16: return tiles_geom<KV_F16>(hd, hdv);
+    case KV_BF16: return tiles_geom<KV_BF16>(hd, hdv);
+    case KV_Q8: return tiles_geom<KV_Q8>(hd, hdv);
+    case KV_F32: return tiles_geom<KV_F32>(hd, hdv);
+  }
+  return false;
 }
+
+uint32_t decode_rows_max_heads() { return RNG; }
 
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
                          const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,
                          const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
+  if (g.layout == LAYOUT_ROWS) {
+    switch (g.kv_type) {
+      case KV_F16: return launch_rows<KV_F16>(g, r, items, n_items, q, out, part, mc, s, ev);
+      case KV_BF16: return launch_rows<KV_BF16>(g, r, items, n_items, q, out, part, mc, s, ev);
+      case KV_Q8: return launch_rows<KV_Q8>(g, r, items, n_items, q, out, part, mc, s, ev);
+      case KV_F32: return launch_rows<KV_F32>(g, r, items, n_items, q, out, part, mc, s, ev);
+    }
+    return hipErrorInvalidValue;
+  }
   switch (g.kv_type) {
     case KV_F16: return dispatch_hd<KV_F16>(g, r, items, n_items, q, out, part, mc, s, ev);
     case KV_BF16: return dispatch_hd<KV_BF16>(g, r, items, n_items, q, out, part, mc, s, ev);
@@ -425,24 +644,20 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
                         float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
+  if (hdv == 0 || hdv > ROWS_MAX_DIM) return hipErrorInvalidValue;
   const uint32_t waves = n_items * r.ng;
   const dim3 grid((waves + 3) / 4), block(256);
-  switch (hdv) {
-    case 64:
-      if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<64, true>), grid, block, 0, s, r, items, n_items, part, out);
-      else LMH_LAUNCH(ev, (merge_kernel<64, false>), grid, block, 0, s, r, items, n_items, part, out);
-      break;
-    case 128:
-      if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<128, true>), grid, block, 0, s, r, items, n_items, part, out);
-      else LMH_LAUNCH(ev, (merge_kernel<128, false>), grid, block, 0, s, r, items, n_items, part, out);
-      break;
-    case 256:
-      if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<256, true>), grid, block, 0, s, r, items, n_items, part, out);
-      else LMH_LAUNCH(ev, (merge_kernel<256, false>), grid, block, 0, s, r, items, n_items, part, out);
-      break;
-    default: return hipErrorInvalidValue;
+  // dims per lane: ceil(hdv / 64) rounded up to a power of two
+  const uint32_t np = hdv <= 64 ? 1 : hdv <= 128 ? 2 : hdv <= 256 ? 4 : 8;
+#define LMH_MERGE(NP)                                                                                              \
+  if (np == NP) {                                                                                                  \
+    if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<NP, true>), grid, block, 0, s, r, hdv, items, n_items, part, out); \
+    else LMH_LAUNCH(ev, (merge_kernel<NP, false>), grid, block, 0, s, r, hdv, items, n_items, part, out);           \
+    return hipGetLastError();                                                                                      \
   }
-  return hipGetLastError();
+  LMH_MERGE(1) LMH_MERGE(2) LMH_MERGE(4) LMH_MERGE(8)
+#undef LMH_MERGE
+  return hipErrorInvalidValue;
 }
 
 }  // namespace lmh

@@ -19,6 +19,12 @@
 //   q8_0 scales (K and V alike), f16, after all code tiles of the head: [tile][key m][d/32]
 //   f32 K/V: plain row-major [key m][d] (the VALU decode path reads rows).
 //
+// Row layout (PageGeom::layout = 1), for the geometries the tile layouts above do not take (head
+// widths off the matrix-core instances, hd != hdv pairs without one, blocks under 16 positions):
+// each (layer, KV head) region holds min(bt, 16)-row tiles of key rows m in the reference's row
+// encoding, row-major [m][d] (f16 / bf16 bits, f32, q8_0 codes), q8_0 scales after the codes as
+// above. Same bytes per block; read by the VALU decode kernel (decode_rows_kernel).
+//
 // The total bytes per block equal the reference's `block_bytes` for the same geometry and type
 // (q8_0: 34 bytes per 32 values; f16/bf16: 2 bytes; f32: 4 bytes per value).
 #pragma once
@@ -46,7 +52,9 @@ struct PageGeom {
   uint32_t bps;       // blocks per sequence (table row length)
   const int32_t* table;  // [n_seqs][bps] block ids
   uint32_t kv_type, n_kv, hd, hdv;
+  uint32_t layout;  // 0: tiles in matrix-core operand order; 1: row-major rows (see above)
 };
+constexpr uint32_t LAYOUT_TILES = 0, LAYOUT_ROWS = 1;
 
 __host__ __device__ inline uint32_t k16_off(uint32_t m, uint32_t d) {
   return (d >> 5) * 1024u + ((((d >> 3) & 3u) << 4) + m) * 16u + (d & 7u) * 2u;
@@ -185,8 +193,13 @@ hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, 
 constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
 hipError_t noalloc_scratch(int device, uint8_t** out);
 // Decode work items (waves) one CU holds at once for a layer's decode kernel (occupancy query).
-uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd);
-bool decode_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
+// The instance a launch picks depends on the group for f32 pages and on the layout.
+uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group, uint32_t layout);
+// Whether (type, hd, hdv) has a tile-layout decode instance (matrix-core, or f32 VALU); every
+// other geometry up to 512 wide takes the row layout and its VALU kernel.
+bool decode_tiles_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
+// Query heads per work item the row-layout kernel takes (its items use ng <= this).
+uint32_t decode_rows_max_heads();
 
 // Prefill (multi-token segments on matrix cores): n_wg workgroups, workgroup b runs the units
 // items[b * per_wg ..] up to the first with n_tok == 0. `max_pages` bounds the key pages of any unit.

@@ -38,6 +38,7 @@ thread_local std::string g_create_error;
 
 struct LayerLayout {
   uint32_t n_head, n_kv, hd, hdv;
+  uint32_t layout;        // LAYOUT_TILES (matrix-core operand order) or LAYOUT_ROWS (row-major rows)
   bool win;               // sliding-window layer: offsets are inside a window-pool block
   uint64_t k_row, v_row;  // the reference's row bytes (encoded I/O)
   uint32_t k_off, v_off, k_head, v_head, k_tile, v_tile, k_scale, v_scale, k_tile_s, v_tile_s;
@@ -53,16 +54,18 @@ uint64_t ref_row_bytes(uint32_t t, uint64_t n) {  // kv.rs:94-99 (+ F32/BF16)
   return 0;
 }
 
-// Bytes of one 16-token tile of values (codes for q8_0) for `dim` dims, and of its q8_0 scales.
-uint32_t tile_bytes(uint32_t t, uint32_t dim) {
+// Bytes of one tile of `rows` positions (16, or the whole block when it is smaller) of values
+// (codes for q8_0) for `dim` dims, and of its q8_0 scales.
+uint32_t tile_bytes(uint32_t t, uint32_t dim, uint32_t rows) {
   switch (t) {
     case LMH_KV_F16:
-    case LMH_KV_BF16: return 16 * dim * 2;
-    case LMH_KV_Q8_0: return 16 * dim;
-    default: return 16 * dim * 4;
+    case LMH_KV_BF16: return rows * dim * 2;
+    case LMH_KV_Q8_0: return rows * dim;
+    default: return rows * dim * 4;
   }
 }
-uint32_t tile_scale_bytes(uint32_t t, uint32_t dim) { return t == LMH_KV_Q8_0 ? 16 * (dim / 32) * 2 : 0; }
+uint32_t tile_scale_bytes(uint32_t t, uint32_t dim, uint32_t rows) { return t == LMH_KV_Q8_0 ? rows * (dim / 32) * 2 : 0; }
+constexpr uint32_t MAX_HEAD_DIM = 512;  // the widest head any kernel takes (Metal's ATTN_MAX_HD)
 
 struct DirtyRows {  // the rows [lo, hi) of a host-side table that differ from the device copy
   uint64_t lo = ~0ull, hi = 0;
@@ -513,6 +516,7 @@ struct lmh_kv {
     g.n_kv = y.n_kv;
     g.hd = y.hd;
     g.hdv = y.hdv;
+    g.layout = y.layout;
     return g;
   }
 
@@ -708,10 +712,6 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
     g_create_error = "block size must be a power of two";
     return LMH_INVALID_ARGUMENT;
   }
-  if (bt < 16) {
-    g_create_error = "the HIP page layout needs blocks of at least 16 positions";
-    return LMH_UNSUPPORTED;
-  }
   if (o->n_layers == 0 || !o->layers) {
     g_create_error = "no attention layers";
     return LMH_INVALID_ARGUMENT;
@@ -746,9 +746,9 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
       g_create_error = "q8_0 cannot hold heads that are not a multiple of 32 wide";
       return LMH_INVALID_ARGUMENT;
     }
-    if (!decode_supported(o->kv_type, d.hd, d.hdv) || (o->kv_type == LMH_KV_Q8_0 && d.hd % 64 != 0)) {
+    if (d.hd > MAX_HEAD_DIM || d.hdv > MAX_HEAD_DIM) {  // Metal refuses the same (backend.rs:574-580)
       delete kv;
-      g_create_error = "unsupported head geometry for the HIP kernels (hd = hdv in {64, 128, 256})";
+      g_create_error = "head widths above 512 are not supported";
       return LMH_UNSUPPORTED;
     }
     LayerLayout y{};
@@ -756,13 +756,16 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
     y.n_kv = d.n_kv;
     y.hd = d.hd;
     y.hdv = d.hdv;
+    // tiles in matrix-core operand order where a decode instance takes the geometry; otherwise
+    // (other widths, hd != hdv without an instance, blocks under 16 positions) row-major rows
+    y.layout = (bt >= 16 && decode_tiles_supported(o->kv_type, d.hd, d.hdv)) ? LAYOUT_TILES : LAYOUT_ROWS;
     y.k_row = ref_row_bytes(o->kv_type, (uint64_t)d.n_kv * d.hd);
     y.v_row = ref_row_bytes(o->kv_type, (uint64_t)d.n_kv * d.hdv);
-    const uint32_t tiles = bt / 16;
-    y.k_tile = tile_bytes(o->kv_type, d.hd);
-    y.v_tile = tile_bytes(o->kv_type, d.hdv);
-    y.k_tile_s = tile_scale_bytes(o->kv_type, d.hd);
-    y.v_tile_s = tile_scale_bytes(o->kv_type, d.hdv);
+    const uint32_t rows = std::min<uint32_t>(bt, 16), tiles = bt / rows;
+    y.k_tile = tile_bytes(o->kv_type, d.hd, rows);
+    y.v_tile = tile_bytes(o->kv_type, d.hdv, rows);
+    y.k_tile_s = tile_scale_bytes(o->kv_type, d.hd, rows);
+    y.v_tile_s = tile_scale_bytes(o->kv_type, d.hdv, rows);
     y.k_scale = tiles * y.k_tile;
     y.v_scale = tiles * y.v_tile;
     y.k_head = tiles * (y.k_tile + y.k_tile_s);
@@ -1373,7 +1376,8 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
     return kv->fail(LMH_INVALID_ARGUMENT, "a window layer's attention window must be 1..its width");
   if ((rc = kv->check_window_rows(layer, segs, n_segs, window)) != LMH_OK) return rc;
   const uint32_t group = y.n_head / y.n_kv;
-  const uint32_t ng = std::min<uint32_t>(group, 16);
+  // heads per decode item: up to 16 (the matrix-core tile's columns), 4 on the row-layout kernel
+  const uint32_t ng = std::min<uint32_t>(group, y.layout == LAYOUT_ROWS ? decode_rows_max_heads() : 16);
   const uint32_t head_blocks = (group + ng - 1) / ng;
   hipStream_t st = (hipStream_t)stream;
 
@@ -1381,7 +1385,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over one
   // workgroup per CU.
   const uint64_t pf_min = kv->prefill_min_rows;
-  const bool pf_ok = scale > 0.f && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
+  const bool pf_ok = scale > 0.f && y.layout == LAYOUT_TILES && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
   std::vector<uint8_t> decode_row(n_rows, 1);
   kv->pitems.clear();
   uint32_t max_pages = 0, pf_wg = 0, pf_per_wg = 0;
@@ -1430,7 +1434,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   // Items the GPU holds at once: with at most that many, every item starts in the first round and
   // none waits for a slot to free up (a second, mostly empty round would double the kernel time).
   if (kv->decode_capacity[layer] == 0)
-    kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd) * kv->n_cu;
+    kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd, y.hdv, group, y.layout) * kv->n_cu;
   uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items
                                                                : kv->decode_capacity[layer], 1);
   // no-allocation calls: at most as many split slots (and merges) as the scratch holds
@@ -1439,8 +1443,8 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   // Smallest chunk: 8 tiles for the matrix-core kernels (enough work per wave to stream at full
   // rate); 2 tiles for f32 rows, whose VALU kernel walks keys with dependent loads (latency-bound:
   // more, shorter items hide it better).
-  const uint64_t min_chunk =
-      kv->decode_min_tiles ? kv->decode_min_tiles : (kv->kv_type == LMH_KV_F32 ? 2 : 8);
+  const uint64_t min_chunk = kv->decode_min_tiles ? kv->decode_min_tiles
+                                                  : (y.layout == LAYOUT_ROWS ? 4 : kv->kv_type == LMH_KV_F32 ? 2 : 8);
   // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane);
   // grown until the rows' rounded-up split counts fit the target
   auto n_items_for = [&](uint64_t c) {

@@ -46,8 +46,11 @@ __device__ inline uint16_t bf16_bits(float x) {
 }
 __device__ inline float bf16_val(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// Byte offset of element (m, d) of a 16-token tile, and of its q8_0 scale, for one side (K or V).
-__device__ inline uint32_t elem_off(uint32_t type, bool is_v, uint32_t m, uint32_t d, uint32_t dim) {
+// Byte offset of element (m, d) of a tile, for one side (K or V), in the tile layout (layout 0)
+// or the row layout (layout 1: row-major codes of the type's width).
+__device__ inline uint32_t elem_off(uint32_t type, bool is_v, uint32_t m, uint32_t d, uint32_t dim,
+                                    uint32_t layout = LAYOUT_TILES) {
+  if (layout == LAYOUT_ROWS) return (m * dim + d) * (type == KV_F32 ? 4u : type == KV_Q8 ? 1u : 2u);
   switch (type) {
     case KV_F16:
     case KV_BF16: return is_v ? v16_off(m, d) : k16_off(m, d);
@@ -80,7 +83,7 @@ __device__ void store_side(const PageGeom& g, const Slot& sl, bool is_v, const f
     const uint32_t h = e / sd.dim, d = e % sd.dim;
     uint8_t* head = sl.base + sd.off + h * sd.head;
     const float x = src[e];
-    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim, g.layout);
     switch (g.kv_type) {
       case KV_F16: *(uint16_t*)(head + o) = f16_bits(x); break;
       case KV_BF16: *(uint16_t*)(head + o) = bf16_bits(x); break;
@@ -122,7 +125,7 @@ __device__ void store_head_wave(const PageGeom& g, const Slot& sl, bool is_v, ui
   uint8_t* head = sl.base + sd.off + h * sd.head;
   for (uint32_t d = lane; d < sd.dim; d += 64) {
     const float v = x[d];
-    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim, g.layout);
     switch (g.kv_type) {
       case KV_F16: *(uint16_t*)(head + o) = f16_bits(v); break;
       case KV_BF16: *(uint16_t*)(head + o) = bf16_bits(v); break;
@@ -172,13 +175,13 @@ __device__ void store_head_lanes(const PageGeom& g, const Slot& sl, bool is_v, u
         }
       } else {
 #pragma unroll
-        for (int c = 0; c < VPL; c++) *(uint16_t*)(head + elem_off(g.kv_type, is_v, sl.m, d0 + c, sd.dim)) = b[c];
+        for (int c = 0; c < VPL; c++) *(uint16_t*)(head + elem_off(g.kv_type, is_v, sl.m, d0 + c, sd.dim, g.layout)) = b[c];
       }
       break;
     }
     case KV_F32: {
 #pragma unroll
-      for (int c = 0; c < VPL; c++) *(float*)(head + elem_off(KV_F32, is_v, sl.m, d0 + c, sd.dim)) = x[c];
+      for (int c = 0; c < VPL; c++) *(float*)(head + elem_off(KV_F32, is_v, sl.m, d0 + c, sd.dim, g.layout)) = x[c];
       break;
     }
     case KV_Q8: {
@@ -190,7 +193,7 @@ __device__ void store_head_lanes(const PageGeom& g, const Slot& sl, bool is_v, u
       const float dsc = amax / 127.0f;
       const float id = dsc != 0.0f ? 1.0f / dsc : 0.0f;
 #pragma unroll
-      for (int c = 0; c < VPL; c++) head[elem_off(KV_Q8, is_v, sl.m, d0 + c, sd.dim)] = (uint8_t)(int8_t)(int32_t)rintf(x[c] * id);
+      for (int c = 0; c < VPL; c++) head[elem_off(KV_Q8, is_v, sl.m, d0 + c, sd.dim, g.layout)] = (uint8_t)(int8_t)(int32_t)rintf(x[c] * id);
       if ((d0 & 31u) == 0) {
         uint8_t* sp = sl.base + sd.off + h * sd.head + sd.scale + sl.tile * sd.tile_s + (sl.m * (sd.dim >> 5) + (d0 >> 5)) * 2u;
         *(uint16_t*)sp = f16_bits(dsc);
@@ -421,7 +424,7 @@ __device__ void store_enc_side(const PageGeom& g, const Slot& sl, bool is_v, con
   for (uint32_t e = threadIdx.x; e < n; e += blockDim.x) {
     const uint32_t h = e / sd.dim, d = e % sd.dim;
     uint8_t* head = sl.base + sd.off + h * sd.head;
-    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim, g.layout);
     switch (g.kv_type) {
       case KV_F16:
       case KV_BF16: *(uint16_t*)(head + o) = (uint16_t)(src[2 * e] | (src[2 * e + 1] << 8)); break;
@@ -455,7 +458,7 @@ __device__ float load_elem(const PageGeom& g, const Slot& sl, bool is_v, uint32_
   const Side sd = side(g, is_v);
   const uint32_t h = e / sd.dim, d = e % sd.dim;
   const uint8_t* head = sl.base + sd.off + h * sd.head;
-  const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+  const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim, g.layout);
   switch (g.kv_type) {
     case KV_F16: return f16_val(*(const uint16_t*)(head + o));
     case KV_BF16: return bf16_val(*(const uint16_t*)(head + o));
@@ -482,7 +485,7 @@ __device__ void gather_enc_side(const PageGeom& g, const Slot& sl, bool is_v, ui
   for (uint32_t e = threadIdx.x; e < n; e += blockDim.x) {
     const uint32_t h = e / sd.dim, d = e % sd.dim;
     const uint8_t* head = sl.base + sd.off + h * sd.head;
-    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim);
+    const uint32_t o = sl.tile * sd.tile + elem_off(g.kv_type, is_v, sl.m, d, sd.dim, g.layout);
     switch (g.kv_type) {
       case KV_F16:
       case KV_BF16: {
@@ -1021,7 +1024,8 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
   const uint32_t vpl = g.hd / 64, half = r.half_rot;
   const bool neox = (r.flags & ROPE_NEOX) != 0;
   const bool pairs_ok = half == 0 || !neox || (half % vpl == 0 && ((half / vpl) & (half / vpl - 1)) == 0);
-  const bool reg = g.hd == g.hdv && g.hd % 64 == 0 && (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) && pairs_ok;
+  const bool reg = g.layout == LAYOUT_TILES && g.hd == g.hdv && g.hd % 64 == 0 &&
+                   (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) && pairs_ok;
   if (reg) {
     // aligned runs of 4 f16 / bf16 rows (when the caller found any) with the other rows, or a
     // short call of any type (decode rows), go to the split kernel: one launch, each row's heads
@@ -1068,7 +1072,8 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
                            uint64_t ref_off, uint32_t k_row, uint32_t v_row, uint8_t* bytes, hipStream_t s) {
   if (n_pos == 0) return hipSuccess;
   const uint32_t seg_k = k_row / g.n_kv, seg_v = v_row / g.n_kv;
-  if (g.hd == g.hdv && bt % 16 == 0 && (g.kv_type == KV_F16 || g.kv_type == KV_BF16 || g.kv_type == KV_Q8) &&
+  const bool tiles = g.layout == LAYOUT_TILES;
+  if (tiles && g.hd == g.hdv && bt % 16 == 0 && (g.kv_type == KV_F16 || g.kv_type == KV_BF16 || g.kv_type == KV_Q8) &&
       (g.hd == 64 || g.hd == 128 || g.hd == 256)) {
     const SnapGeom sg{seq, bt, k_row, v_row, bb, ref_off, seg_k, seg_v};
     const uint32_t ph = g.k_tile + (g.kv_type == KV_Q8 ? g.k_tile_s : 0);
@@ -1089,7 +1094,7 @@ hipError_t launch_snapshot(bool write, const PageGeom& g, uint32_t seq, uint32_t
 #undef LMH_SNAP
     }
   }
-  if (seg_k % 4 == 0 && seg_v % 4 == 0 && bt % 16 == 0) {
+  if (tiles && seg_k % 4 == 0 && seg_v % 4 == 0 && bt % 16 == 0) {
     const SnapGeom sg{seq, bt, k_row, v_row, bb, ref_off, seg_k, seg_v};
     const uint32_t tb = std::max(g.k_tile + (g.kv_type == KV_Q8 ? g.k_tile_s : 0),
                                  g.v_tile + (g.kv_type == KV_Q8 ? g.v_tile_s : 0));

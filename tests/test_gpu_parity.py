@@ -99,7 +99,7 @@ def test_block_tables_free_counts_and_kv_full_match(cuda):
 # ---- stores and gathers --------------------------------------------------------------------
 
 @pytest.mark.parametrize("kv", ["f32", "f16", "bf16", "q8_0"])
-@pytest.mark.parametrize("bt", [16, 32])
+@pytest.mark.parametrize("bt", [4, 16, 32])
 def test_store_then_gather_is_byte_exact(cuda, kv, bt):
     import torch
     L = Layer(8, 4, 128, 128)
@@ -168,6 +168,25 @@ SMALL = [
     ("f16", Layer(16, 4, 64, 64), [700, 64], [20, 1], 0, 16),
     ("bf16", Layer(32, 8, 128, 128), [1500, 10], [1, 40], 0, 16),
     ("bf16", Layer(8, 2, 64, 64), [90, 3000, 0], [1, 1, 70], 500, 32),
+    # more matrix-core widths (Metal's attn_vec instances and hd != hdv), decode and prompt rows
+    ("f16", Layer(16, 4, 32, 32), [300, 0], [1, 40], 0, 16),
+    ("bf16", Layer(12, 4, 96, 96), [700, 20], [1, 33], 0, 16),
+    ("f16", Layer(16, 8, 192, 192), [900, 3], [1, 20], 0, 16),
+    ("f16", Layer(32, 8, 192, 128), [1200, 10], [1, 25], 0, 32),
+    ("q8_0", Layer(16, 2, 192, 192), [2000, 7], [1, 3], 0, 16),
+    # the row layout: widths without an instance, q8_0 widths off 64, f32 off the instances,
+    # hd != hdv, 512-wide heads, blocks under 16 positions, a window
+    ("f16", Layer(32, 32, 80, 80), [500, 3], [1, 30], 0, 16),
+    ("f16", Layer(8, 2, 100, 100), [257, 0], [1, 18], 0, 16),
+    ("bf16", Layer(8, 1, 512, 512), [600], [2], 0, 16),
+    ("q8_0", Layer(8, 2, 32, 32), [700, 40], [1, 20], 0, 16),
+    ("q8_0", Layer(12, 4, 96, 96), [1100], [1], 0, 32),
+    ("f32", Layer(8, 4, 96, 96), [300], [1], 0, 16),
+    ("f16", Layer(16, 4, 64, 128), [800, 5], [1, 17], 0, 16),
+    ("bf16", Layer(8, 2, 64, 64), [130, 0], [1, 21], 0, 4),
+    ("q8_0", Layer(8, 2, 64, 64), [200], [3], 0, 8),
+    ("f32", Layer(4, 2, 64, 64), [70], [1], 0, 2),
+    ("f16", Layer(32, 32, 80, 80), [900, 60], [1, 20], 37, 16),
 ]
 
 
@@ -247,3 +266,43 @@ def test_golden_fixture(cuda, name, split):
     e1, e2 = row_rel_err(got, f.out), row_rel_err(got, f.out_f64)
     print(f"{name} split={split}: vs oracle {e1:.3e}, vs f64 {e2:.3e}")
     assert e1 <= TOL[f.kv_type] and e2 <= TOL[f.kv_type], (e1, e2)
+
+
+@pytest.mark.parametrize("kv,layers,bt", [
+    ("f16", [(16, 4, 80, 80), (8, 2, 64, 128)], 16),
+    ("q8_0", [(12, 4, 96, 96), (8, 2, 32, 32)], 16),
+    ("bf16", [(8, 2, 64, 64)], 4),
+    ("f32", [(8, 4, 96, 96)], 8),
+])
+def test_row_layout_store_gather_and_snapshot_are_byte_exact(cuda, kv, layers, bt):
+    """Row-layout layers (widths without a matrix-core instance, hd != hdv, small blocks): rows
+    stored through the C ABI gather back byte-exact in the reference's encoding, and a sequence's
+    snapshot is byte-identical to the oracle's reference-format snapshot."""
+    import torch
+    rng = np.random.default_rng(5)
+    hc = HipKvCache([Layer(*g) for g in layers], max_ctx=200, n_seqs=2, kv_type=kv, block_tokens=bt)
+    oc = O.Cache(layers, max_ctx=200, n_seqs=2, kv_type=kv, block_tokens=bt)
+    for c in (hc, oc):
+        segs, n = c.prepare_batch([(0, 150), (1, 37)])
+    assert hc.blocks(0) == oc.blocks(0) and hc.blocks(1) == oc.blocks(1)
+    for layer, (nh, nkv, hd, hdv) in enumerate(layers):
+        k = (rng.standard_normal((n, nkv * hd)) * 2).astype(np.float32)
+        v = (rng.standard_normal((n, nkv * hdv)) * 2).astype(np.float32)
+        hc.store(layer, segs, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
+        for (sq, start, cnt, pos0) in segs:
+            oc.store_rows(sq, layer, pos0, k[start:start + cnt], v[start:start + cnt])
+        li = oc.layer(layer)
+        kb = torch.zeros((n, li["k_row"]), dtype=torch.uint8, device="cuda")
+        vb = torch.zeros((n, li["v_row"]), dtype=torch.uint8, device="cuda")
+        hc.gather_encoded(layer, segs, kb, vb)
+        torch.cuda.synchronize()
+        kb, vb = kb.cpu().numpy(), vb.cpu().numpy()
+        for (sq, start, cnt, pos0) in segs:
+            rk, rv = oc.load_rows_raw(sq, layer, pos0, cnt)
+            assert np.array_equal(kb[start:start + cnt], rk) and np.array_equal(vb[start:start + cnt], rv), (layer, sq)
+    hc.commit_batch(segs)
+    oc.commit_batch(segs)
+    for sq in range(2):
+        got = hc.write_seq(sq)
+        torch.cuda.synchronize()
+        assert np.array_equal(got.cpu().numpy(), oc.write_seq(sq)), sq
