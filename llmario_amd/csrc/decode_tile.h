@@ -77,10 +77,16 @@ struct TileRegs {
   uint4 vs[NVS > 0 ? NVS : 1];
 };
 
-// 16 bytes of a page. Ordinary (caching) loads: successive decode steps re-read the same pages,
-// and a step whose pages fit the last-level cache keeps them there (measured on c2, 297 MB of
-// K/V: 50.7 us per step with these loads against 52.4 us with non-temporal ones).
-__device__ inline uint4 load_stream(const uint8_t* p) { return *(const uint4*)p; }
+// 16 bytes of a page, non-temporal: an engine's step reads each layer's pages once, and a layer's
+// pages were last read a whole step (every other layer's pages) earlier, so they come from HBM;
+// streaming them past the caches reads a cold 1.5 GB at 7.1 TB/s against 6.4 TB/s for ordinary
+// loads. (Re-reading one layer's 297 MB step after step, which fits the last-level cache, ordinary
+// loads were 3% faster.)
+__device__ inline uint4 load_stream(const uint8_t* p) {
+  typedef unsigned int u4 __attribute__((ext_vector_type(4)));
+  const u4 v = __builtin_nontemporal_load((const u4*)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
 
 template <int KVT, int HD, int HDV>
 __device__ inline void load_tile(TileRegs<KVT, HD, HDV>& t, const uint8_t* kb, const uint8_t* vb,
