@@ -46,11 +46,11 @@ def test_create_rejects_bad_options_without_touching_the_device():
     layer = (N.LayerDesc * 1)(N.LayerDesc(8, 8, 64, 64, 0, 0))
     o = N.KvOptions(N.ABI_VERSION, 0, 24, 1, ctypes.cast(layer, ctypes.POINTER(N.LayerDesc)), 16, 1, 0, 0, 0)
     assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.INVALID_ARGUMENT  # not a power of two
-    o.block_tokens = 8
-    assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.UNSUPPORTED  # below one 16-token tile
     o.block_tokens = 16
-    layer[0] = N.LayerDesc(8, 8, 80, 80, 0, 0)
-    assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.UNSUPPORTED  # head width
+    layer[0] = N.LayerDesc(8, 8, 576, 512, 0, 0)
+    assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.UNSUPPORTED  # wider than 512 (Metal's bound)
+    layer[0] = N.LayerDesc(8, 3, 64, 64, 0, 0)
+    assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.INVALID_ARGUMENT  # n_head % n_kv
     o.kv_type = N.KV_Q8_0
     layer[0] = N.LayerDesc(8, 8, 48, 48)
     assert N.lib().lmh_kv_create(ctypes.byref(o), ctypes.byref(h)) == N.INVALID_ARGUMENT  # kv.rs:103-109
