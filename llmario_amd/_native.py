@@ -10,7 +10,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libllmario_hip.so")
+# LLMARIO_HIP_LIB names another build of the same library (an instrumented one, say)
+LIB_PATH = os.environ.get("LLMARIO_HIP_LIB") or os.path.join(HERE, "libllmario_hip.so")
 
 OK, INVALID_ARGUMENT, KV_FULL, UNSUPPORTED, DEVICE_ERROR, OUT_OF_MEMORY = 0, 1, 2, 3, 4, 5
 STATUS_NAMES = {0: "OK", 1: "INVALID_ARGUMENT", 2: "KV_FULL", 3: "UNSUPPORTED", 4: "DEVICE_ERROR",

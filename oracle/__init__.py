@@ -17,7 +17,8 @@ import subprocess
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# LLMARIO_ORACLE_LIB names another build of the same library (an instrumented one, say)
+LIB_PATH = os.environ.get("LLMARIO_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 KV_F16, KV_Q8_0, KV_F32, KV_BF16 = 0, 1, 2, 3
 KV_NAMES = {"f16": KV_F16, "q8_0": KV_Q8_0, "f32": KV_F32, "bf16": KV_BF16}
