@@ -273,6 +273,8 @@ typedef struct lmh_attend_tuning {
   uint64_t prefill_min_rows;
   uint64_t decode_target_items;
   uint64_t decode_min_tiles;
+  uint64_t prefill_workgroups;  /* cap on the prefill kernel's workgroups (0: every slot of the device);
+                                   fewer workgroups run more units each */
 } lmh_attend_tuning;
 int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t);
 /* The options in force (defaults resolved; decode_target_items 0 = the occupancy default). */

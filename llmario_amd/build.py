@@ -27,6 +27,10 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I", os.path.join(HERE, "..", "include"),
 ]
+# build(verify=True): the backend also checks every machine instruction it emits, so an illegal
+# operand (which the object path would otherwise encode silently) fails the build. The check does
+# not change the code; it roughly quadruples the compile time.
+VERIFY = ["-mllvm", "-verify-machineinstrs"]
 
 
 # Per-source extras. prefill.hip: its scores come from matrix products and masks (-inf), never
@@ -36,13 +40,14 @@ FLAGS = [
 EXTRA = {"prefill.hip": ["-fno-honor-nans", "-Wno-inline-asm"]}
 
 
-def _compile(src: str) -> str:
+def _compile(src: str, verify: bool = False) -> str:
     obj = os.path.join(BUILD, os.path.basename(src) + ".o")
     if src in HOST_ONLY:
         cmd = [HIPCC, "-O3", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(HERE, "..", "include"),
                "-x", "c++", "-c", os.path.join(CSRC, src), "-o", obj]
     else:
-        cmd = [HIPCC, *FLAGS, *EXTRA.get(src, []), "-x", "hip", "-c", os.path.join(CSRC, src), "-o", obj]
+        cmd = [HIPCC, *FLAGS, *(VERIFY if verify else []), *EXTRA.get(src, []), "-x", "hip", "-c",
+               os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
@@ -53,10 +58,10 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, verify: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
+        objs = list(ex.map(lambda src: _compile(src, verify), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -213,6 +213,7 @@ hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillI
                         uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
                         uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
                         hipStream_t s, const LaunchEv& ev = {});
+uint32_t prefill_wg_per_cu();     // prefill workgroups a CU holds when their LDS fits (160 KiB / this)
 uint32_t prefill_cols_per_unit();
 // LDS the prefill kernels declare statically, beside prefill_lds_bytes() of dynamic LDS
 size_t prefill_static_lds_bytes();

@@ -243,6 +243,7 @@ struct lmh_kv {
   // ---- lmh_attend planning / precision options (lmh_kv_set_tuning)
   bool prefill_p_f16 = false;
   uint64_t prefill_min_rows = 16, decode_target_items = 0, decode_min_tiles = 0;  // 0: defaults
+  uint64_t prefill_workgroups = 0;                                                  // 0: every slot
   std::string err;
 
   ~lmh_kv() {
@@ -1197,13 +1198,13 @@ int32_t lmh_batch_commit(lmh_kv* kv, const lmh_seg* segs, uint64_t n_segs) {
   return LMH_OK;
 }
 
-// Prefill units grouped per workgroup: one workgroup per CU (the kernel's LDS admits one), each
-// running a list of units. Longest-processing-time-first: units by decreasing key pages (plus a
+// Prefill units grouped per workgroup: prefill_wg_per_cu() workgroups per CU, each running a
+// list of units. Longest-processing-time-first: units by decreasing key pages (plus a
 // fixed cost for the unit's Q load and output), each to the currently least loaded workgroup.
 // Lists are padded to the longest with empty units (n_tok = 0) at a fixed stride.
-static void assign_prefill_units(std::vector<PrefillItem>& items, uint64_t window, uint32_t n_cu, uint32_t& n_wg,
+static void assign_prefill_units(std::vector<PrefillItem>& items, uint64_t window, uint32_t slots, uint32_t& n_wg,
                                  uint32_t& per_wg) {
-  n_wg = (uint32_t)std::min<uint64_t>(items.size(), std::max<uint32_t>(n_cu, 1));
+  n_wg = (uint32_t)std::min<uint64_t>(items.size(), std::max<uint32_t>(slots, 1));
   per_wg = 0;
   if (n_wg == 0) return;
   auto work = [&](const PrefillItem& it) -> uint64_t {
@@ -1382,8 +1383,8 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   hipStream_t st = (hipStream_t)stream;
 
   // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
-  // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over one
-  // workgroup per CU.
+  // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over
+  // prefill_wg_per_cu() workgroups per CU.
   const uint64_t pf_min = kv->prefill_min_rows;
   const bool pf_ok = scale > 0.f && y.layout == LAYOUT_TILES && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
   std::vector<uint8_t> decode_row(n_rows, 1);
@@ -1411,7 +1412,10 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
       }
       for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
     }
-    assign_prefill_units(kv->pitems, window, kv->n_cu, pf_wg, pf_per_wg);
+    const uint32_t slots = kv->n_cu * prefill_wg_per_cu();
+    assign_prefill_units(kv->pitems, window,
+                         kv->prefill_workgroups ? (uint32_t)std::min<uint64_t>(kv->prefill_workgroups, slots) : slots,
+                         pf_wg, pf_per_wg);
     if (prefill_lds_bytes(y.hd, max_pages, pf_per_wg) + prefill_static_lds_bytes() > 160 * 1024) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
       kv->pitems.clear();
@@ -1594,7 +1598,9 @@ int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {
   if (t->prefill_min_rows > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_min_rows out of range");
   if (t->decode_min_tiles > 64) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: decode_min_tiles must be <= 64");
   if (t->decode_target_items > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: decode_target_items out of range");
+  if (t->prefill_workgroups > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_workgroups out of range");
   kv->prefill_p_f16 = t->prefill_p_f16 != 0;
+  kv->prefill_workgroups = t->prefill_workgroups;
   kv->prefill_min_rows = t->prefill_min_rows ? t->prefill_min_rows : 16;
   kv->decode_target_items = t->decode_target_items;
   kv->decode_min_tiles = t->decode_min_tiles;
@@ -1608,6 +1614,7 @@ int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t) {
   t->prefill_min_rows = kv->prefill_min_rows;
   t->decode_target_items = kv->decode_target_items;
   t->decode_min_tiles = kv->decode_min_tiles ? kv->decode_min_tiles : (kv->kv_type == LMH_KV_F32 ? 2 : 8);
+  t->prefill_workgroups = kv->prefill_workgroups;
   return LMH_OK;
 }
 

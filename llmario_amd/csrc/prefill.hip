@@ -57,13 +57,14 @@ __device__ inline float sum_over_groups(float x) {
 
 
 // 16 bytes per lane from global memory straight into LDS (global_load_lds_dwordx4): lane L reads
-// sbase + voff(L) and writes lds_dst + 16*L, where sbase and lds_dst are wave-uniform (an SGPR pair
-// and M0). Issued from inline assembly so the compiler does not track it: the kernel waits for
-// these loads itself (s_waitcnt vmcnt) before the barrier that publishes a stage, and nothing else
-// in the tile loop touches vector memory.
-__device__ inline void lds_dma16(const uint8_t* sbase, uint32_t voff, uint8_t* lds_dst) {
-  const uint32_t l = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(void __attribute__((address_space(3)))*)lds_dst);
+// sbase + voff(L) and writes LDS address lds_dst + 16*L, where sbase and lds_dst are wave-uniform
+// (an SGPR pair and M0). The LDS address is an integer (a generic pointer cast back to the LDS
+// address space needs a null test the backend can select illegally). Issued from inline assembly
+// so the compiler does not track it: the kernel waits for these loads itself (s_waitcnt vmcnt)
+// before the barrier that publishes a stage, and nothing else in the tile loop touches vector
+// memory.
+__device__ inline void lds_dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_dst);
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(sbase) : "memory", "m0");
 }
 
@@ -100,6 +101,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   constexpr int TILE = 16 * HD * 2;           // bytes of one 16-token page tile (K or V)
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint8_t* kv_lds = smem;                                          // [NSTAGE][K 4 tiles | V 4 tiles]
+  const uint32_t kv_lds_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
   PrefillItem* units = (PrefillItem*)(smem + NSTAGE * 8 * TILE);   // this workgroup's unit list
   int* blk_lds = (int*)(units + per_wg);                           // block id of each key page in range
 
@@ -139,7 +141,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   constexpr int R = TILE / 1024;
   constexpr int CPT = TILE / 2 / 1024;        // DMAs per wave per side per tile (on average)
   static_assert((R == 4 || R == 2) && CPT * 2048 == TILE, "page tiles of 2 or 4 KiB");
-  const uint32_t n_tiles = (n_pages + 3) / 4;
+  const uint32_t n_tiles = __builtin_amdgcn_readfirstlane((n_pages + 3) / 4);   // scalar: bounds barrier loops
   const bool do_k = R == 4 || w >= 4, do_v = R == 4 || w < 4;
   const uint32_t kw = R == 4 ? w : w - 4;
   const uint32_t k_tile = 2 * kw / R, k_row = (2 * kw) % R * 1024;   // K rows k_row, k_row + 1 KiB
@@ -187,7 +189,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
   };
   auto issue = [&](uint32_t ti) {
-    uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
+    const uint32_t stage = kv_lds_addr + (ti % NSTAGE) * 8 * TILE;
     if constexpr (!PAIR_V) {
       const uint8_t* kb = page(ti, my_tile, false);
       const uint8_t* vb = page(ti, my_tile, true);
@@ -709,6 +711,8 @@ hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const Prefil
 }  // namespace
 
 uint32_t prefill_cols_per_unit() { return PW * COLS; }
+
+uint32_t prefill_wg_per_cu() { return 1; }   // the LDS stages fill a CU
 
 size_t prefill_static_lds_bytes() { return 64; }  // lo_flags[PW], rounded up
 

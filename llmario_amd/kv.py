@@ -273,7 +273,8 @@ class HipKvCache:
                                                _stream_ptr(stream)))
 
     def set_tuning(self, *, prefill_p_f16: bool | None = None, prefill_min_rows: int | None = None,
-                   decode_target_items: int | None = None, decode_min_tiles: int | None = None):
+                   decode_target_items: int | None = None, decode_min_tiles: int | None = None,
+                   prefill_workgroups: int | None = None):
         """lmh_kv_set_tuning: change the given options, keep the others (0 = the default)."""
         t = N.AttendTuning()
         self._check(N.lib().lmh_kv_get_tuning(self.h, C.byref(t)))
@@ -285,6 +286,8 @@ class HipKvCache:
             t.decode_target_items = int(decode_target_items)
         if decode_min_tiles is not None:
             t.decode_min_tiles = int(decode_min_tiles)
+        if prefill_workgroups is not None:
+            t.prefill_workgroups = int(prefill_workgroups)
         self._check(N.lib().lmh_kv_set_tuning(self.h, C.byref(t)))
 
     def tuning(self) -> dict:

@@ -205,6 +205,38 @@ def test_attend_small(cuda, kv, layer, prior, new, window, bt, split):
     assert err <= TOL[kv], err
 
 
+# Prompt units streamed through few workgroups: each workgroup runs many units (and two passes
+# per unit when Q has bits below the cache's 16-bit type) back to back, fetching the next one's
+# first tiles, Q and block ids during the current one. Segments of different lengths give units
+# of one tile and of many; a window and a prefix make ranges that start past page 0.
+STREAM = [
+    ("bf16", Layer(32, 8, 128, 128), [0, 7, 300, 0], [300, 70, 16, 700], 0, 16),
+    ("f16", Layer(16, 4, 128, 128), [0, 1200], [200, 100], 500, 32),
+    ("bf16", Layer(8, 2, 64, 64), [0, 40, 0], [48, 190, 20], 0, 16),
+    ("f16", Layer(40, 8, 64, 64), [100, 0], [90, 260], 0, 64),
+    # decode rows beside the prompt units (one launch of the mixed kernel)
+    ("bf16", Layer(32, 8, 128, 128), [1500, 10, 0], [1, 40, 200], 0, 16),
+]
+
+
+@pytest.mark.parametrize("kv,layer,prior,new,window,bt", STREAM)
+@pytest.mark.parametrize("q_kind", ["rounded", "f32"])
+@pytest.mark.parametrize("wgs", [1, 3])
+def test_prefill_units_stream_through_few_workgroups(cuda, kv, layer, prior, new, window, bt, q_kind, wgs):
+    w = small("s", kv, layer, prior, new, window=window, seed=47, block_tokens=bt)
+    hc, oc, q = pair(w)
+    if q_kind == "f32":   # bits below f16 / bf16: the two-pass path
+        q = np.random.default_rng(5).standard_normal(q.shape).astype(np.float32)
+    hc.set_tuning(prefill_workgroups=wgs)
+    assert hc.tuning()["prefill_workgroups"] == wgs
+    got = run_gpu(hc, w, q)
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    assert np.isfinite(got).all()
+    err = row_rel_err(got, ref)
+    print(f"{kv} {layer} prior={prior} new={new} window={window} bt={bt} q={q_kind} wgs={wgs}: {err:.3e}")
+    assert err <= TOL[kv], err
+
+
 @pytest.mark.parametrize("name", ["c1", "c2", "c4"])
 def test_attend_config_all_rows(cuda, name):
     w = config(name)
