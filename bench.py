@@ -14,7 +14,8 @@ the same 297 MB) is reported beside it as `c2_warm`.
 Also reported (extra keys, each in isolation: a failing leg is recorded under `errors` and the
 headline line still prints): every other configuration's throughput and its launch roofline
 (max(bytes / HBM peak, FLOPs / MFMA peak) against the kernel time, with the decode and prefill
-parts of a mixed launch), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), the
+parts of a mixed launch), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), c3's
+prompts on q8_0 pages (`c3_q8`; `c3_q8_rows`: the same with every row sent to the decode kernels), the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
 of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), c5w
 with its layer in the sliding-window pool (`window_c5w`), and the CPU baseline (the C++
@@ -531,7 +532,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5,window_c5w",
+    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c3_q8,c3_q8_rows,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5,"
+                                       "window_c5w",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline budget (c2 on all threads and on 1, c1 on both)")
@@ -584,6 +586,8 @@ def main():
             name, layers = "c2", args.layers or COLD_LAYERS
         elif name.endswith("_p_f16"):
             name, tuning = name[:-len("_p_f16")], {"prefill_p_f16": True}
+        elif name.endswith("_rows"):
+            name, tuning = name[:-len("_rows")], {"prefill_min_rows": 1 << 32}
         res = time_config(name, args.steps, args.warmup, warmup_s=args.extra_warmup_s, n_layers=layers,
                           tuning=tuning, label=args.profile_config)
         print(json.dumps(res), flush=True)
@@ -605,6 +609,10 @@ def main():
         # the prefill with P rounded to f16 (Metal's prefill precision), beside c3's default
         "c3_p_f16": lambda: time_config("c3", short, 3, warmup_s=args.extra_warmup_s,
                                         tuning={"prefill_p_f16": True}, label="c3_p_f16"),
+        # c3's prompts on q8_0 pages routed as decode rows (every row re-reads its prefix), beside
+        # c3_q8 on the matrix-core prefill
+        "c3_q8_rows": lambda: time_config("c3_q8", max(3, short // 4), 1, warmup_s=args.extra_warmup_s,
+                                          tuning={"prefill_min_rows": 1 << 32}, label="c3_q8_rows"),
     }
     for name in [x for x in args.extra.split(",") if x]:
         fn = legs.get(name) or (lambda name=name: time_config(name, short, 3, warmup_s=args.extra_warmup_s))

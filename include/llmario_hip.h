@@ -235,7 +235,10 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
  * p_lo..=pos of its own sequence (p_lo = pos+1-window when window > 0 and pos+1 > window, else 0),
  * softmax(scale * q.K) V per query head with GQA head kvh = h / (n_head / n_kv); fp32
  * accumulation. q is [n_rows][n_head][hd] f32, out is [n_rows][n_head][hdv] f32 (device).
- * Decode rows, split-K over pages and prefill tiles are packed into one work list. */
+ * Decode rows, split-K over pages and prefill tiles are packed into one work list: segments of at
+ * least prefill_min_rows rows on f16, bf16 or q8_0 pages of head width 64 or 128 (hd = hdv) run on
+ * the matrix-core prefill kernel (Metal's attn_prefill_hd{64,128}[_q8_0], backend.rs:563-569); the
+ * other rows on the decode kernels. */
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
@@ -260,6 +263,7 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
  *   prefill_p_f16: 1 = the prefill products take P rounded to f16, the precision of Metal's
  *     attn_prefill (attn_prefill.metal: half P); 0 (default) = P as f16 hi + lo parts (~22 bits,
  *     the CPU path's f32 weights to within the 2e-3 bound even on rows whose output cancels).
+ *     Applies to f16 / bf16 pages: q8_0 prompts always carry their scaled weights as bf16 hi + lo.
  *   prefill_min_rows: segments of at least this many rows go to the matrix-core prefill kernel
  *     (default 16; 1 .. 2^32).
  *   decode_target_items: split-K target of decode work items (default: the items the device holds

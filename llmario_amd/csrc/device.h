@@ -120,7 +120,7 @@ struct PrefillGeom {
   uint32_t n_head, group;
   float scale_log2;  // scale * log2(e)
   uint32_t window;   // 0 = none
-  uint32_t p_f16;    // 1: P rounded to f16 for P.V (Metal's prefill precision); 0: f16 hi + lo
+  uint32_t p_f16;    // 1: P rounded to f16 for P.V (Metal's prefill precision); 0: f16 hi + lo (q8_0: always hi + lo)
 };
 
 // Fused per-row tail of attention_block (see lmh_qk_rope_store): flags as LMH_ROPE_*.
@@ -217,6 +217,6 @@ uint32_t prefill_wg_per_cu();     // prefill workgroups a CU holds when their LD
 uint32_t prefill_cols_per_unit();
 // LDS the prefill kernels declare statically, beside prefill_lds_bytes() of dynamic LDS
 size_t prefill_static_lds_bytes();
-size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg);
+size_t prefill_lds_bytes(uint32_t kv_type, uint32_t hd, uint32_t max_pages, uint32_t per_wg);
 
 }  // namespace lmh

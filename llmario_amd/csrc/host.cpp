@@ -1416,7 +1416,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
     assign_prefill_units(kv->pitems, window,
                          kv->prefill_workgroups ? (uint32_t)std::min<uint64_t>(kv->prefill_workgroups, slots) : slots,
                          pf_wg, pf_per_wg);
-    if (prefill_lds_bytes(y.hd, max_pages, pf_per_wg) + prefill_static_lds_bytes() > 160 * 1024) {
+    if (prefill_lds_bytes(kv->kv_type, y.hd, max_pages, pf_per_wg) + prefill_static_lds_bytes() > 160 * 1024) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
       kv->pitems.clear();
       std::fill(decode_row.begin(), decode_row.end(), 1);

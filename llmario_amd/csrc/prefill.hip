@@ -21,6 +21,17 @@
 // column's reference max enters as the initial accumulator of Q.K, so the products are the
 // exponent arguments directly. The reference max moves lazily (only when a score exceeds it by
 // more than 8 in the log2 domain), so the O accumulators are almost never rescaled.
+//
+// q8_0 pages (the Metal sibling's attn_prefill_hd{64,128}_q8_0, attn_prefill.metal:200-203) keep
+// the decode kernel's exact scheme rather than dequantising to 16 bits (d*q rounded to f16 misses
+// the per-row bound on rows whose output cancels): each wave's DMA brings a page tile's int8 codes
+// and its f16 scales into LDS, the thread that loaded the codes rewrites them in place as
+// int8-valued f16 (K) or bf16 (V), both exact, and the products apply the scales:
+//   S^T = sum over 32-dim chunks c of d_K[key][c] * (K_c . Q_c^T)   (one MFMA chain per chunk, Q as
+//         f16 hi + lo, so q8_0 units always run the two-pass form)
+//   O^T += V^T . (P * d_V[.][b])^T per 32-dim V block b, the scaled weights as bf16 hi + lo
+//         (v_mfma_f32_16x16x32_bf16; bf16 has f32's range, so no product of a weight and a scale
+//         leaves it)
 #include "decode_tile.h"
 
 namespace lmh {
@@ -90,6 +101,33 @@ __device__ inline void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) 
   lo = l;
 }
 
+// Weights (a, b) as packed bf16 hi parts and packed bf16 lo parts (a - hi, b - hi), both rounded to
+// nearest even: 16 significant bits per weight.
+__device__ inline void split_pair_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+  const f2 v = {a, b};
+  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+  const f2 r = {a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u)};
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf2));
+}
+
+// Eight int8 codes (two uint32) -> eight f16 (uint4), exact.
+__device__ inline uint4 i8x8_to_h8(uint32_t a, uint32_t b) {
+  const dtile::h4 x = dtile::i8x4_to_h4(a), y = dtile::i8x4_to_h4(b);
+  const uint2 u = __builtin_bit_cast(uint2, x), v = __builtin_bit_cast(uint2, y);
+  return make_uint4(u.x, u.y, v.x, v.y);
+}
+// Eight int8 codes -> eight bf16, exact (|q| <= 128 has at most 8 significant bits): each code
+// converted to f32, whose upper half is then the bf16 value.
+__device__ inline uint32_t i8x2_to_bf2(uint32_t w, int sh) {
+  const float f0 = (float)(int)(signed char)(w >> sh), f1 = (float)(int)(signed char)(w >> (sh + 8));
+  return (__float_as_uint(f0) >> 16) | (__float_as_uint(f1) & 0xffff0000u);
+}
+__device__ inline uint4 i8x8_to_bf8(uint32_t a, uint32_t b) {
+  return make_uint4(i8x2_to_bf2(a, 0), i8x2_to_bf2(a, 16), i8x2_to_bf2(b, 0), i8x2_to_bf2(b, 16));
+}
+
 // Workgroup `wg` of a prefill launch: its list of units, items[wg * per_wg ..]. PLO: P carried
 // past f16 as hi + lo halves (two P.V products on the same V operand); without it P is rounded
 // to f16, the precision of the Metal sibling's prefill.
@@ -98,11 +136,16 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
                                            uint32_t per_wg, const float* q, float* out, uint32_t wg) {
   constexpr int NC = HD / 32;                 // Q.K chunks of 32 dims
   constexpr int NJ = HD / 16;                 // O^T blocks of 16 dims
-  constexpr int TILE = 16 * HD * 2;           // bytes of one 16-token page tile (K or V)
+  constexpr int TILE = 16 * HD * 2;           // bytes of one 16-token page tile (K or V) in LDS
+  constexpr bool Q8 = KVT == KV_Q8;
+  // q8_0: each stage also holds the scales of its 8 page tiles (K tiles 0-3, V tiles 0-3), 16 keys x
+  // HD/32 f16 per tile (32*NC bytes, NSL lanes of 16 bytes)
+  constexpr int NSL = 2 * NC;
+  constexpr int STAGE = 8 * TILE + (Q8 ? 8 * 16 * NSL : 0);
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  uint8_t* kv_lds = smem;                                          // [NSTAGE][K 4 tiles | V 4 tiles]
+  uint8_t* kv_lds = smem;                                          // [NSTAGE][K 4 tiles | V 4 tiles | scales]
   const uint32_t kv_lds_addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
-  PrefillItem* units = (PrefillItem*)(smem + NSTAGE * 8 * TILE);   // this workgroup's unit list
+  PrefillItem* units = (PrefillItem*)(smem + NSTAGE * STAGE);      // this workgroup's unit list
   int* blk_lds = (int*)(units + per_wg);                           // block id of each key page in range
 
   // The workgroup's units (the host's balanced assignment, per_wg slots, an empty unit ends the
@@ -135,9 +178,12 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   //      2h+1 (the two tiles of half h), so the thread that loaded them can interleave them for
   //      the P.V products (settle, below). hd 128 (R = 4): every wave does two K rows and one V
   //      row pair; hd 64 (R = 2): waves 0-3 a V row pair each, waves 4-7 two K rows each.
+  //   q8_0: wave w copies page tile (w >> 1) of side (w & 1): its QR rows of int8 codes (1 KiB
+  //      each) into the upper half of the tile's LDS slot, and its scales (NSL lanes).
   // Pages past the range re-read the last page (finite values whose keys are masked), so stale
   // LDS never meets a zero weight.
   constexpr bool PAIR_V = KVT == KV_BF16;
+  constexpr int QR = TILE / 2048;             // q8_0: rows of codes per page tile
   constexpr int R = TILE / 1024;
   constexpr int CPT = TILE / 2 / 1024;        // DMAs per wave per side per tile (on average)
   static_assert((R == 4 || R == 2) && CPT * 2048 == TILE, "page tiles of 2 or 4 KiB");
@@ -188,8 +234,32 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
     return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
   };
+  // q8_0: the scales of the page tile whose codes start at `codes` (the same page, clamped as
+  // page_any clamps it): head base + scale offset + sub * scale stride.
+  auto page_scales = [&](uint32_t ti, uint32_t tile, bool v_side, const uint8_t* codes) -> const uint8_t* {
+    const uint32_t p = min(ti * 4 + tile, n_pages - 1);
+    const uint64_t sub = (((page0 + p) << 4) & bt_mask) >> 4;
+    const uint64_t off = v_side ? (uint64_t)g.v_scale + sub * g.v_tile_s - sub * g.v_tile
+                                : (uint64_t)g.k_scale + sub * g.k_tile_s - sub * g.k_tile;
+    const uint64_t u = (uint64_t)(uintptr_t)codes + off;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
+  };
   auto issue = [&](uint32_t ti) {
-    const uint32_t stage = kv_lds_addr + (ti % NSTAGE) * 8 * TILE;
+    const uint32_t stage = kv_lds_addr + (ti % NSTAGE) * STAGE;
+    if constexpr (Q8) {
+      const uint32_t side = w & 1u, pt = w >> 1;
+      const uint8_t* cb = page(ti, pt, side != 0);
+      const uint32_t slot = stage + side * 4 * TILE + pt * TILE;
+#pragma unroll
+      for (int r = 0; r < QR; r++) lds_dma16(cb, r * 1024 + lane * 16, slot + (QR + r) * 1024);
+      const uint8_t* sb = page_scales(ti, pt, side != 0, cb);
+      // the first NSL lanes: their LDS destinations are the slot's first NSL*16 bytes whether the
+      // DMA places a lane by its index or by its rank among the active lanes
+      if (lane < (uint32_t)NSL) lds_dma16(sb, lane * 16, stage + 8 * TILE + (side * 4 + pt) * (NSL * 16));
+      return;
+    }
     if constexpr (!PAIR_V) {
       const uint8_t* kb = page(ti, my_tile, false);
       const uint8_t* vb = page(ti, my_tile, true);
@@ -219,9 +289,32 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // rewritten as A' = [A keys of d | B keys of d] and B' = [A keys of d+16 | B keys of d+16], so
   // one 16-byte read is a whole 32-key operand of the P.V product. f16 tiles are used as loaded
   // (the extra LDS pass would cost more than the operand assembly it saves).
+  // q8_0: the thread's rows of codes (row r at LDS row QR + r of its slot, 16 bytes per lane) are
+  // rewritten as 16-bit values in place, read first and then written: the first 8 codes of row r
+  // (K: dims 64r + 8g .. +8 of key m, lane 16g + m; V: keys 4(lane/16) .. +4 of dims 64r + lane%16
+  // and 64r + 16 + lane%16) are the lane's 16 bytes of LDS row 2r in the f16 tile layout, the last
+  // 8 those of row 2r + 1. K becomes f16, V bf16 (the type its scaled weights are carried in).
   bool widen_k = true;   // bf16 pages: false while the unit's Q.K products run on bf16 (below)
   auto settle = [&](uint32_t ti) {
-    uint8_t* stage = kv_lds + (ti % NSTAGE) * 8 * TILE;
+    uint8_t* stage = kv_lds + (ti % NSTAGE) * STAGE;
+    if constexpr (Q8) {
+      const uint32_t side = w & 1u, pt = w >> 1;
+      uint8_t* slot = stage + side * 4 * TILE + pt * TILE + lane * 16;
+      uint4 c[QR];
+#pragma unroll
+      for (int r = 0; r < QR; r++) c[r] = *(const uint4*)(slot + (QR + r) * 1024);
+#pragma unroll
+      for (int r = 0; r < QR; r++) {
+        if (side == 0) {
+          *(uint4*)(slot + (2 * r) * 1024) = i8x8_to_h8(c[r].x, c[r].y);
+          *(uint4*)(slot + (2 * r + 1) * 1024) = i8x8_to_h8(c[r].z, c[r].w);
+        } else {
+          *(uint4*)(slot + (2 * r) * 1024) = i8x8_to_bf8(c[r].x, c[r].y);
+          *(uint4*)(slot + (2 * r + 1) * 1024) = i8x8_to_bf8(c[r].z, c[r].w);
+        }
+      }
+      return;
+    }
     if constexpr (KVT == KV_BF16) {
       if (do_k && widen_k) {
 #pragma unroll
@@ -312,7 +405,12 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     return nz;
   };
   h8 qf[2][NC];
-  if (pass == 0) {
+  if (Q8 && pass == 0) {   // q8_0: always the two-pass form (the scaled Q.K products take Q as hi + lo)
+    const int32_t* tab = g.table + (size_t)it.seq * g.bps;
+    for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
+    __syncthreads();
+    lo_any = true;
+  } else if (pass == 0) {
     bool lo_need = false;
     {
       float4 raw[2][NC][2];
@@ -401,13 +499,25 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 
   // Matrix-core operands of one 32-key half, read from LDS ahead of the products that use them
   // (the reads of one phase are in flight while the previous phase computes).
-  struct KOps { uint4 a[NC][2]; };   // K: chunk ch of page tile kk
-  struct VOps { uint4 a[NJ]; };      // V^T: dims 16j.. of both page tiles (8 bytes each)
+  // q8_0: s[kk] holds the scales of keys 4g .. 4g+3 of page tile kk (all HD/32 chunks, f16, key-major)
+  constexpr int NSC = Q8 ? NC / 2 : 1;
+  struct KOps { uint4 a[NC][2]; uint4 s[2][NSC]; };   // K: chunk ch of page tile kk
+  struct VOps { uint4 a[NJ]; uint4 s[2][NSC]; };      // V^T: dims 16j.. of both page tiles (8 bytes each)
+  // the scales of page tile `tile` on side `side` of the stage at `st`, this lane's keys
+  auto load_scales = [&](uint4 (&s)[NSC], const uint8_t* st, int side, int tile) {
+#pragma unroll
+    for (int c = 0; c < NSC; c++)
+      s[c] = *(const uint4*)(st + 8 * TILE + (side * 4 + tile) * (NSL * 16) + grp * (8 * NC) + c * 16);
+  };
   auto load_k = [&](KOps& o, const uint8_t* kt, int kp) {
 #pragma unroll
     for (int ch = 0; ch < NC; ch++)
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) o.a[ch][kk] = *(const uint4*)(kt + (2 * kp + kk) * TILE + ch * 1024 + lane * 16);
+    if constexpr (Q8) {
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++) load_scales(o.s[kk], kt, 0, 2 * kp + kk);
+    }
   };
   // k index 8g+i of the P.V product is key 4g+i of the half's first 16-key page tile (i < 4) or
   // key 4g+i-4 of its second: 8 bytes from each page tile (f16), or after settle (bf16) one
@@ -424,10 +534,29 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
         o.a[j] = make_uint4(v0.x, v0.y, v1.x, v1.y);
       }
     }
+    if constexpr (Q8) {
+#pragma unroll
+      for (int kk = 0; kk < 2; kk++) load_scales(o.s[kk], vt - 4 * TILE, 1, 2 * kp + kk);
+    }
   };
   // S^T for the 32 keys of a half (two 16-key page tiles) x the pass's columns (LO: the hi and
   // lo products of one column block, summed)
   auto qk = [&](f4 (&S)[2][NCB], const KOps& ko) {
+    if constexpr (Q8) {   // (two-pass form) per chunk: the hi + lo products, times the key's scale
+#pragma unroll
+      for (int ch = 0; ch < NC; ch++) {
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+          const h8 a = __builtin_bit_cast(h8, ko.a[ch][kk]);
+          f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][ch], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ch], t, 0, 0, 0);
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            S[kk][0][r] = fmaf(t[r], dtile::scale_at<NC>(ko.s[kk], r, ch), ch == 0 ? nm[0] : S[kk][0][r]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
 #pragma unroll
@@ -513,6 +642,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   };
   // P = 2^(c2 (s - m) + PUP) as f16 hi (+ lo) parts, row sums in f32 (Sn: the next half's scores,
   // see rebase)
+  // q8_0: the weights stay in f32 (pq) for pv, which scales them per V block
+  float pq[NCB][8];
   auto softmax = [&](f4 (&S)[2][NCB], h8 (&Ph)[NCB], h8 (&Pl)[NCB], f4 (&Sn)[2][NCB]) {
     float pw[NCB][8], ps[NCB];
     expo(S, pw, ps);
@@ -522,6 +653,15 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     if (__ballot(need)) {
       rebase(S, Sn);
       expo(S, pw, ps);
+    }
+    if constexpr (Q8) {
+#pragma unroll
+      for (int x = 0; x < NX; x++) {
+        l[x] += ps[x];
+#pragma unroll
+        for (int e = 0; e < 8; e++) pq[x][e] = pw[x][e];
+      }
+      return;
     }
 #pragma unroll
     for (int x = 0; x < NX; x++) {
@@ -545,6 +685,27 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   };
   // O^T += V^T P^T over a half, 32 keys per MFMA
   auto pv = [&](const h8 (&Ph)[NCB], const h8 (&Pl)[NCB], const VOps& vo) {
+    if constexpr (Q8) {   // (two-pass form) per 32-dim V block b: P * d_V[key][b] as bf16 hi + lo
+#pragma unroll
+      for (int b = 0; b < NC; b++) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const int e0 = 2 * i, e1 = 2 * i + 1;   // weight e: key 4g + e%4 of page tile e/4
+          split_pair_bf16(pq[0][e0] * dtile::scale_at<NC>(vo.s[e0 / 4], e0 % 4, b),
+                          pq[0][e1] * dtile::scale_at<NC>(vo.s[e1 / 4], e1 % 4, b), hw[i], lw[i]);
+        }
+        const dtile::b8 ph = __builtin_bit_cast(dtile::b8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+        const dtile::b8 pl = __builtin_bit_cast(dtile::b8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+#pragma unroll
+        for (int jj = 0; jj < 2; jj++) {
+          const dtile::b8 va = __builtin_bit_cast(dtile::b8, vo.a[2 * b + jj]);
+          O[2 * b + jj][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, O[2 * b + jj][0], 0, 0, 0);
+          O[2 * b + jj][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, O[2 * b + jj][0], 0, 0, 0);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; j++) {
       const h8 va = __builtin_bit_cast(h8, vo.a[j]);
@@ -569,9 +730,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // Every tile is computed (keys outside a column's range are masked), except by waves that own
   // no column at all.
   auto wait_tile = [&](uint32_t ti) {  // this thread's loads of tile ti have landed
-    if (ti + 1 < n_tiles) {
-      if constexpr (CPT == 1)
+    if (ti + 1 < n_tiles) {   // a thread's loads per tile: 2*CPT, or QR + 1 (q8_0: codes, scales)
+      if constexpr (Q8 ? QR + 1 == 2 : CPT == 1)
         asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+      else if constexpr (Q8)
+        asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
       else
         asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
     } else {
@@ -592,7 +755,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   }
   for (uint32_t ti = 0; ti < n_tiles; ti++) {
     if (ti + 2 < n_tiles) issue(ti + 2);
-    const uint8_t* kt = kv_lds + (ti % NSTAGE) * 8 * TILE;
+    const uint8_t* kt = kv_lds + (ti % NSTAGE) * STAGE;
     const uint8_t* vt = kt + 4 * TILE;
     const uint32_t key0 = (page0 + ti * 4) * 16;
     const bool need_mask = key0 + BK - 1 > wpos_min || key0 < wlo_max || key0 + BK - 1 > pos_last;
@@ -616,7 +779,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       // first half of the next tile (after the last tile: a stale stage, never used), issued
       // before this half's exponentials so its products overlap them and are complete when the
       // next iteration reads S0
-      load_k(ko, kv_lds + ((ti + 1) % NSTAGE) * 8 * TILE, 0);
+      load_k(ko, kv_lds + ((ti + 1) % NSTAGE) * STAGE, 0);
       qk(S0, ko);
       softmax(S1, Ph, Pl, S0);
       pv(Ph, Pl, vo);
@@ -642,7 +805,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   __syncthreads();
   };
 
-  if (!lo_any) {
+  if constexpr (Q8) {
+    run(std::true_type{}, pass);
+    pass ^= 1u;
+    if (pass == 0) unit++;
+  } else if (!lo_any) {
     run(std::false_type{}, 0);
     unit++;
   } else {
@@ -684,11 +851,16 @@ void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_
 template <int KVT, int HD>
 hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
                     uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s, const LaunchEv& ev) {
-  const uint32_t lds = (uint32_t)prefill_lds_bytes(HD, max_pages, per_wg);
-  if (pg.p_f16)
-    LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
-  else
-    LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+  const uint32_t lds = (uint32_t)prefill_lds_bytes(KVT, HD, max_pages, per_wg);
+  // q8_0 has one instance: its scaled weights are always carried as hi + lo (prefill_p_f16 applies to
+  // 16-bit pages)
+  if constexpr (KVT != KV_Q8) {
+    if (pg.p_f16) {
+      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+      return hipGetLastError();
+    }
+  }
+  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
   return hipGetLastError();
 }
 
@@ -697,14 +869,17 @@ hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const Prefil
                           uint32_t per_wg, uint32_t max_pages, const RowGeom& r, const DecodeItem* items,
                           uint32_t n_items, const float* q, float* out, float* part, const MergeCopy& mc,
                           hipStream_t s, const LaunchEv& ev) {
-  const uint32_t lds = (uint32_t)prefill_lds_bytes(HD, max_pages, per_wg);
+  const uint32_t lds = (uint32_t)prefill_lds_bytes(KVT, HD, max_pages, per_wg);
   const uint32_t n_wg = pf_wg + (n_items + PW - 1) / PW;
-  if (pg.p_f16)
-    LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
-               items, n_items, q, out, part, mc);
-  else
-    LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
-               items, n_items, q, out, part, mc);
+  if constexpr (KVT != KV_Q8) {
+    if (pg.p_f16) {
+      LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
+                 items, n_items, q, out, part, mc);
+      return hipGetLastError();
+    }
+  }
+  LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
+             items, n_items, q, out, part, mc);
   return hipGetLastError();
 }
 
@@ -716,13 +891,14 @@ uint32_t prefill_wg_per_cu() { return 1; }   // the LDS stages fill a CU
 
 size_t prefill_static_lds_bytes() { return 64; }  // lo_flags[PW], rounded up
 
-size_t prefill_lds_bytes(uint32_t hd, uint32_t max_pages, uint32_t per_wg) {
-  return NSTAGE * 8 * (16 * (size_t)hd * 2) + (size_t)per_wg * sizeof(PrefillItem) + (size_t)max_pages * 4;
+size_t prefill_lds_bytes(uint32_t kv_type, uint32_t hd, uint32_t max_pages, uint32_t per_wg) {
+  const size_t stage = 8 * (16 * (size_t)hd * 2) + (kv_type == KV_Q8 ? 8 * (size_t)hd : 0);   // + q8_0 scales
+  return NSTAGE * stage + (size_t)per_wg * sizeof(PrefillItem) + (size_t)max_pages * 4;
 }
 
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group) {
-  return (kv_type == KV_F16 || kv_type == KV_BF16) && hd == hdv && (hd == 64 || hd == 128) && group >= 1 &&
-         group <= PW * COLS;
+  return (kv_type == KV_F16 || kv_type == KV_BF16 || kv_type == KV_Q8) && hd == hdv && (hd == 64 || hd == 128) &&
+         group >= 1 && group <= PW * COLS;
 }
 
 hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* pitems, uint32_t pf_wg,
@@ -734,6 +910,7 @@ hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillI
   if (g.kv_type == T && g.hd == D)                                                                               \
     return launch_mixed_t<T, D>(g, pg, pitems, pf_wg, per_wg, max_pages, r, items, n_items, q, out, part, mc, s, ev);
   LMH_MIXED(KV_F16, 128) LMH_MIXED(KV_F16, 64) LMH_MIXED(KV_BF16, 128) LMH_MIXED(KV_BF16, 64)
+  LMH_MIXED(KV_Q8, 128) LMH_MIXED(KV_Q8, 64)
 #undef LMH_MIXED
   return hipErrorInvalidValue;
 }
@@ -748,6 +925,9 @@ hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const Prefil
   } else if (g.kv_type == KV_F16) {
     if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
     if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+  } else if (g.kv_type == KV_Q8) {
+    if (g.hd == 128) return launch_t<KV_Q8, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+    if (g.hd == 64) return launch_t<KV_Q8, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
   }
   return hipErrorInvalidValue;
 }

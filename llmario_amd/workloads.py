@@ -116,7 +116,7 @@ class Workload:
 
 
 def config(name: str) -> Workload:
-    """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096)."""
+    """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096); c3_q8 is c3 on q8_0 pages."""
     if name == "c1":
         return Workload("c1", "f32", Layer(8, 8, 64, 64), prior=[255], new=[1], seed=1)
     if name == "c2":
@@ -126,6 +126,8 @@ def config(name: str) -> Workload:
                         seed=2)
     if name == "c3":
         return Workload("c3", "bf16", Layer(32, 8, 128, 128), prior=[0] * 4, new=[2048] * 4, seed=3)
+    if name == "c3_q8":   # c3's prompts on a q8_0 cache (the planner's degraded KV type)
+        return Workload("c3_q8", "q8_0", Layer(32, 8, 128, 128), prior=[0] * 4, new=[2048] * 4, seed=3)
     if name == "c4":
         return Workload("c4", "q8_0", Layer(64, 8, 128, 128), prior=[32767] * 8, new=[1] * 8, seed=4)
     if name in ("c5", "c5w"):

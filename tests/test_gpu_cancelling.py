@@ -5,10 +5,11 @@ test: ||got - ref||_inf / ||ref||_inf <= 2e-3, with ref the f32 CPU path (the or
 of attend / attend_split, crates/engine/model/src/forward.rs:585-807, whose weights are f32,
 forward.rs:645-666).
 
-The head geometries are c2's (decode rows, f16), c3's (causal prefill, bf16) and c5's (decode rows
-and a prefill chunk in one launch, f16; also with a window), each with Q carrying bits below f16
-(the prefill kernel's two-pass path with hi + lo Q parts) and with Q held in the cache's 16-bit
-type (its one-pass path), and with automatic and forced split-K.
+The head geometries are c2's (decode rows, f16), c3's (causal prefill, bf16; also q8_0) and c5's
+(decode rows and a prefill chunk in one launch, f16; also with a window, and q8_0), each with Q
+carrying bits below f16 (the prefill kernel's two-pass path with hi + lo Q parts) and with Q held
+in the cache's 16-bit type (its one-pass path; q8_0 prompts always take the two-pass path), and
+with automatic and forced split-K.
 """
 
 import os
@@ -30,6 +31,8 @@ CASES = [
     ("c3_prefill", "bf16", Layer(32, 8, 128, 128), [0, 0], [640, 300], 0),
     ("c5_mixed", "f16", Layer(40, 8, 128, 128), [1200, 2500, 600, 1024], [1, 1, 1, 96], 0),
     ("c5w_mixed", "f16", Layer(40, 8, 128, 128), [1200, 2500, 600, 1024], [1, 1, 1, 96], 700),
+    ("c3_prefill_q8_0", "q8_0", Layer(32, 8, 128, 128), [0, 0], [640, 300], 0),
+    ("c5_mixed_q8_0", "q8_0", Layer(40, 8, 128, 128), [1200, 2500, 600, 1024], [1, 1, 1, 96], 0),
 ]
 
 

@@ -187,6 +187,12 @@ SMALL = [
     ("q8_0", Layer(8, 2, 64, 64), [200], [3], 0, 8),
     ("f32", Layer(4, 2, 64, 64), [70], [1], 0, 2),
     ("f16", Layer(32, 32, 80, 80), [900, 60], [1, 20], 37, 16),
+    # q8_0 prompts on the matrix-core prefill (scaled products), alone and beside decode rows
+    ("q8_0", Layer(32, 8, 128, 128), [0, 7, 300], [300, 70, 16], 0, 16),
+    ("q8_0", Layer(16, 2, 64, 64), [500, 0], [45, 100], 0, 64),
+    ("q8_0", Layer(40, 8, 128, 128), [600, 20], [130, 1], 37, 16),
+    ("q8_0", Layer(32, 8, 128, 128), [1500, 10], [1, 40], 0, 32),
+    ("q8_0", Layer(8, 2, 64, 64), [90, 3000, 0], [1, 1, 70], 500, 32),
 ]
 
 
@@ -216,6 +222,9 @@ STREAM = [
     ("f16", Layer(40, 8, 64, 64), [100, 0], [90, 260], 0, 64),
     # decode rows beside the prompt units (one launch of the mixed kernel)
     ("bf16", Layer(32, 8, 128, 128), [1500, 10, 0], [1, 40, 200], 0, 16),
+    ("q8_0", Layer(32, 8, 128, 128), [0, 7, 300, 0], [300, 70, 16, 700], 0, 16),
+    ("q8_0", Layer(8, 2, 64, 64), [0, 40, 0], [48, 190, 20], 500, 16),
+    ("q8_0", Layer(32, 8, 128, 128), [1500, 10, 0], [1, 40, 200], 0, 32),
 ]
 
 
@@ -248,7 +257,7 @@ def test_attend_config_all_rows(cuda, name):
     assert err <= TOL[w.kv_type], err
 
 
-@pytest.mark.parametrize("name", ["c3", "c5", "c5w"])
+@pytest.mark.parametrize("name", ["c3", "c3_q8", "c5", "c5w"])
 def test_attend_config_sampled_rows(cuda, name):
     w = config(name)
     hc, oc, q = pair(w)
