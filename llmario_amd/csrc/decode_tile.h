@@ -63,6 +63,34 @@ __device__ inline h4 bf4_to_h4(uint32_t a, uint32_t b) {
 
 __device__ inline float h_to_f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 
+// Weights (a, b) as packed f16 hi parts and packed f16 lo parts (a - hi, b - hi): each lo part one
+// v_fma_mix_f32 that reads the f16 hi part directly (hi * -1 + a), then one conversion per pair.
+// The -1 is hidden from constant folding (an empty asm statement, which emits nothing) so the
+// compiler keeps the fma form instead of converting hi back to f32 and subtracting; every
+// instruction is the compiler's own, so its hazard tracking sees them.
+__device__ inline void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  float m1 = -1.0f;
+  asm("" : "+v"(m1));
+  const h2 h = __builtin_convertvector((f2){a, b}, h2);
+  const f2 r = {__builtin_fmaf((float)h[0], m1, a), __builtin_fmaf((float)h[1], m1, b)};
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
+}
+
+// (p0 * d0, p1 * d1) as packed f16 hi parts and packed f16 lo parts (p*d - hi from one fma, rounded
+// once), for f16 scales d: the compiler forms both from v_fma_mix{lo,hi}_f16, which read the f32
+// weight and the f16 scale as they are.
+__device__ inline void scaled_split(float p0, _Float16 d0, float p1, _Float16 d1, uint32_t& hi, uint32_t& lo) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const h2 h = {(_Float16)__builtin_fmaf(p0, (float)d0, 0.0f), (_Float16)__builtin_fmaf(p1, (float)d1, 0.0f)};
+  const h2 l = {(_Float16)__builtin_fmaf(p0, (float)d0, -(float)h[0]),
+                (_Float16)__builtin_fmaf(p1, (float)d1, -(float)h[1])};
+  hi = __builtin_bit_cast(uint32_t, h);
+  lo = __builtin_bit_cast(uint32_t, l);
+}
+
 template <int KVT, int HD, int HDV>
 struct TileRegs {
   // f16/bf16: K one uint4 per 32 dims, V one uint4 per 32 dims.
@@ -106,6 +134,14 @@ __device__ inline void load_tile(TileRegs<KVT, HD, HDV>& t, const uint8_t* kb, c
   }
 }
 
+// f16 scale of key 4g+r, chunk c, from the lane's scale registers.
+template <int NCH>
+__device__ inline _Float16 scale_h(const uint4* s, int r, int c) {
+  const int idx = r * NCH + c;
+  const uint32_t w = ((const uint32_t*)s)[idx >> 1];
+  return __builtin_bit_cast(_Float16, (uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
+}
+
 // Scale (as f32) for key 4g+r, chunk c, from the lane's scale registers.
 template <int NCH>
 __device__ inline float scale_at(const uint4* s, int r, int c) {
@@ -132,7 +168,16 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   constexpr int PUP = KVT == KV_Q8 ? 0 : 7;  // weights scaled by 2^PUP (see the softmax step)
   using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
   const uint32_t lane = threadIdx.x & 63u;
-  const DecodeItem it = items[wi];
+  // the item is the same for the whole wave: its fields in scalar registers keep the tile loop's
+  // address arithmetic and range tests on the scalar unit
+  DecodeItem it = items[wi];
+  it.row = __builtin_amdgcn_readfirstlane(it.row);
+  it.kvh = __builtin_amdgcn_readfirstlane(it.kvh);
+  it.h0 = __builtin_amdgcn_readfirstlane(it.h0);
+  it.p0 = __builtin_amdgcn_readfirstlane(it.p0);
+  it.p1 = __builtin_amdgcn_readfirstlane(it.p1);
+  it.slot = __builtin_amdgcn_readfirstlane(it.slot);
+  it.seq = __builtin_amdgcn_readfirstlane(it.seq);
   const int seq = (int)it.seq;
   const int32_t* tab = g.table + (size_t)seq * g.bps;
   const uint32_t hq = lane & 15u, grp = lane >> 4;
@@ -225,10 +270,15 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
     // ---- online softmax (log2 domain), keys outside [p0, p1) masked
     const uint32_t kbase = (t << 4) + 4u * grp;
     float sc[4];
+    if ((t << 4) < it.p0 || (t << 4) + 16u > it.p1) {   // a tile at an end of the range (uniform)
 #pragma unroll
-    for (int rr = 0; rr < 4; rr++) {
-      const uint32_t key = kbase + rr;
-      sc[rr] = (key >= it.p0 && key < it.p1) ? s[rr] * r.scale_log2 : -INFINITY;
+      for (int rr = 0; rr < 4; rr++) {
+        const uint32_t key = kbase + rr;
+        sc[rr] = (key >= it.p0 && key < it.p1) ? s[rr] * r.scale_log2 : -INFINITY;
+      }
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < 4; rr++) sc[rr] = s[rr] * r.scale_log2;
     }
     // Lazy reference max: m (per head) moves only when a score exceeds it by more than 8, so
     // p = 2^(s - m) <= 2^8 and O is rescaled on few tiles; each lane checks its own 4 scores and
@@ -261,13 +311,13 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
       constexpr int NCH = HDV / 32;
 #pragma unroll
       for (int b = 0; b < HDV / 32; b++) {
-        h4 ph, pl;
+        uint32_t hw[2], lw[2];
 #pragma unroll
-        for (int rr = 0; rr < 4; rr++) {
-          const float x = p[rr] * scale_at<NCH>(cur.vs, rr, b);
-          ph[rr] = (_Float16)x;
-          pl[rr] = (_Float16)(x - (float)ph[rr]);
-        }
+        for (int i = 0; i < 2; i++)
+          scaled_split(p[2 * i], scale_h<NCH>(cur.vs, 2 * i, b), p[2 * i + 1], scale_h<NCH>(cur.vs, 2 * i + 1, b),
+                       hw[i], lw[i]);
+        const h4 ph = __builtin_bit_cast(h4, make_uint2(hw[0], hw[1]));
+        const h4 pl = __builtin_bit_cast(h4, make_uint2(lw[0], lw[1]));
 #pragma unroll
         for (int jj = 0; jj < 2; jj++) {
           const int j = 2 * b + jj;
@@ -278,12 +328,11 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
         }
       }
     } else {
-      h4 ph, pl;
+      uint32_t hw[2], lw[2];
 #pragma unroll
-      for (int rr = 0; rr < 4; rr++) {
-        ph[rr] = (_Float16)p[rr];
-        pl[rr] = (_Float16)(p[rr] - (float)ph[rr]);
-      }
+      for (int i = 0; i < 2; i++) split_pair(p[2 * i], p[2 * i + 1], hw[i], lw[i]);
+      const h4 ph = __builtin_bit_cast(h4, make_uint2(hw[0], hw[1]));
+      const h4 pl = __builtin_bit_cast(h4, make_uint2(lw[0], lw[1]));
 #pragma unroll
       for (int j = 0; j < NJ; j++) {
         const uint32_t* w = (const uint32_t*)&cur.v[j >> 1];
@@ -300,14 +349,15 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
     }
   };
 
-  // Two-deep ping-pong: tile t+1 is in flight while tile t is computed.
+  // Two-deep ping-pong: tile t+1 is in flight while tile t is computed. The fetches past the last
+  // tile re-read the last tile (in bounds, and unconditional, so the buffers need no copies).
   TileRegs<KVT, HD, HDV> b0, b1;
   fetch(b0, t0);
   for (uint32_t t = t0; t <= t1; t += 2) {
-    if (t + 1 <= t1) fetch(b1, t + 1);
+    fetch(b1, min(t + 1, t1));
     step(b0, t);
     if (t + 1 > t1) break;
-    if (t + 2 <= t1) fetch(b0, t + 2);
+    fetch(b0, min(t + 2, t1));
     step(b1, t + 1);
   }
   lsum = xsum_groups(lsum);

@@ -73,10 +73,16 @@ __device__ inline float sum_over_groups(float x) {
 // address space needs a null test the backend can select illegally). Issued from inline assembly
 // so the compiler does not track it: the kernel waits for these loads itself (s_waitcnt vmcnt)
 // before the barrier that publishes a stage, and nothing else in the tile loop touches vector
-// memory.
+// memory. The compiler cannot see inside the statement, so it carries its own wait states: the
+// base's SGPRs often come from v_readfirstlane right before it, and a vector-memory instruction
+// may read an SGPR that a VALU instruction wrote only 5 wait states later (s_nop 4); an LDS DMA
+// may read M0 one wait state after an SALU write (s_nop 0). The compiler puts the same wait
+// states before its own global_load_lds.
 __device__ inline void lds_dma16(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
   const uint32_t l = __builtin_amdgcn_readfirstlane(lds_dst);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff), "s"(sbase) : "memory", "m0");
+  asm volatile("s_nop 4\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(l), "v"(voff),
+               "s"(sbase)
+               : "memory", "m0");
 }
 
 // bf16 pair (one uint32) -> f16 pair (one uint32), exact in the normal f16 range.
@@ -85,20 +91,6 @@ __device__ inline uint32_t bf2_to_h2(uint32_t w) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const f2 x = {__uint_as_float(w << 16), __uint_as_float(w & 0xffff0000u)};
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, h2));
-}
-
-// Weights (a, b) as packed f16 hi parts and packed f16 lo parts (a - hi, b - hi), the lo parts each
-// one exact fma rounded once to f16 (v_fma_mix{lo,hi}_f16 read the f16 hi operand directly):
-// three instructions per pair instead of converting hi back to f32 and subtracting.
-__device__ inline void split_pair(float a, float b, uint32_t& hi, uint32_t& lo) {
-  typedef float f2 __attribute__((ext_vector_type(2)));
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-  const f2 v = {a, b};
-  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, h2));
-  uint32_t l;
-  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l) : "v"(hi), "v"(a));
-  asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "+v"(l) : "v"(hi), "v"(b));
-  lo = l;
 }
 
 // Weights (a, b) as packed bf16 hi parts and packed bf16 lo parts (a - hi, b - hi), both rounded to
@@ -670,7 +662,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         if constexpr (PLO) {
-          split_pair(pw[x][2 * i], pw[x][2 * i + 1], hw[i], lw[i]);
+          dtile::split_pair(pw[x][2 * i], pw[x][2 * i + 1], hw[i], lw[i]);
         } else {
           typedef float f2 __attribute__((ext_vector_type(2)));
           typedef _Float16 h2 __attribute__((ext_vector_type(2)));
