@@ -15,7 +15,9 @@ Also reported (extra keys, each in isolation: a failing leg is recorded under `e
 headline line still prints): every other configuration's throughput and its launch roofline
 (max(bytes / HBM peak, FLOPs / MFMA peak) against the kernel time, with the decode and prefill
 parts of a mixed launch), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), c3's
-prompts on q8_0 pages (`c3_q8`; `c3_q8_rows`: the same with every row sent to the decode kernels), the
+prompts on q8_0 pages (`c3_q8`; `c3_q8_rows`: the same with every row sent to the decode kernels), c3
+with Q keeping all f32 bits (`c3_q_f32`: the prefill's two-pass path; every other leg's Q is rounded
+to the cache's 16-bit type), the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
 of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), c5w
 with its layer in the sliding-window pool (`window_c5w`), and the CPU baseline (the C++
@@ -59,14 +61,15 @@ def read_ceiling(nbytes: int, iters: int = 50) -> float:
 
 
 def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, warmup_s: float = 0.0,
-                n_layers: int = 1, tuning: dict | None = None, label: str | None = None):
+                n_layers: int = 1, tuning: dict | None = None, label: str | None = None, q_f32: bool = False):
     """Time `steps` calls of one configuration after at least `warmup` untimed calls and at least
     `warmup_s` seconds of them (matrix-core work runs at a lower clock for the first tens of
     milliseconds of load, so the compute-bound configurations are warmed by time).
     n_layers > 1: the cache holds that many layers of the configuration (same rows in each) and
     step i attends layer i % n_layers, so each step reads K/V last touched n_layers - 1 steps
     earlier (an engine's layer loop): with n_layers x the K/V bytes well above the device's
-    last-level cache, every step's pages come from HBM. tuning: lmh_kv_set_tuning options."""
+    last-level cache, every step's pages come from HBM. tuning: lmh_kv_set_tuning options. q_f32: Q
+    keeps all f32 bits instead of being rounded to the cache's 16-bit type."""
     import torch
 
     from llmario_amd import harness
@@ -80,7 +83,7 @@ def time_config(name: str, steps: int, warmup: int, timing_kernel: bool = True, 
     if tuning:
         hc.set_tuning(**tuning)
     L = w.layer
-    q = torch.from_numpy(gen.q()).cuda()
+    q = torch.from_numpy(gen.q(rounded=not q_f32)).cuda()
     out = torch.empty((w.n_rows, L.n_head, L.hdv), device="cuda")
     segs = Segments(w.segments())
     stream = torch.cuda.current_stream()
@@ -413,7 +416,8 @@ def time_window(steps: int, warmup_s: float):
         v = torch.randn((m, L.n_kv * L.hdv), device="cuda", generator=g)
         hc.store(0, [(s, 0, m, first)], k, v)
     segs = Segments(segs_l)
-    q = torch.randn((n, L.n_head, L.hd), device="cuda", generator=g)
+    # Q rounded to f16 as c5w's rows are (an f32 Q with lower bits takes the prefill's two-pass path)
+    q = torch.randn((n, L.n_head, L.hd), device="cuda", generator=g).half().float()
     out = torch.empty((n, L.n_head, L.hdv), device="cuda")
     stream = torch.cuda.current_stream()
     t_w = time.perf_counter()
@@ -531,9 +535,11 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c3_q8,c3_q8_rows,c4,c5,c5w,rope_c3,snapshot_c4,sched_c5,"
-                                       "window_c5w",
+    # ~0.2 s of c2 steps: the clock needs tens of milliseconds of load to settle (10 warm-up steps
+    # left the cold decode kernel at 52.7 us against 50.3 us settled)
+    ap.add_argument("--warmup", type=int, default=3000)
+    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c5,c5w,rope_c3,snapshot_c4,"
+                                       "sched_c5,window_c5w",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline budget (c2 on all threads and on 1, c1 on both)")
@@ -588,8 +594,10 @@ def main():
             name, tuning = name[:-len("_p_f16")], {"prefill_p_f16": True}
         elif name.endswith("_rows"):
             name, tuning = name[:-len("_rows")], {"prefill_min_rows": 1 << 32}
+        q_f32 = name.endswith("_q_f32")
+        name = name[:-len("_q_f32")] if q_f32 else name
         res = time_config(name, args.steps, args.warmup, warmup_s=args.extra_warmup_s, n_layers=layers,
-                          tuning=tuning, label=args.profile_config)
+                          tuning=tuning, label=args.profile_config, q_f32=q_f32)
         print(json.dumps(res), flush=True)
         return
 
@@ -613,6 +621,9 @@ def main():
         # c3_q8 on the matrix-core prefill
         "c3_q8_rows": lambda: time_config("c3_q8", max(3, short // 4), 1, warmup_s=args.extra_warmup_s,
                                           tuning={"prefill_min_rows": 1 << 32}, label="c3_q8_rows"),
+        # c3 with Q keeping all f32 bits (the prefill's two passes: Q as f16 hi + lo)
+        "c3_q_f32": lambda: time_config("c3", short, 3, warmup_s=args.extra_warmup_s, q_f32=True,
+                                        label="c3_q_f32"),
     }
     for name in [x for x in args.extra.split(",") if x]:
         fn = legs.get(name) or (lambda name=name: time_config(name, short, 3, warmup_s=args.extra_warmup_s))

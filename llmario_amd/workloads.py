@@ -190,10 +190,12 @@ class Generator:
         rows[:, :, 2:] = codes.astype(np.int8).view(np.uint8)
         return rows.reshape(t, nb * 34)
 
-    def q(self) -> np.ndarray:
+    def q(self, rounded: bool = True) -> np.ndarray:
+        """Q rows: N(0, 1) rounded to the cache's 16-bit type (f16 for q8_0 pages), as activations an
+        engine keeps in that type; rounded=False keeps all f32 bits (the prefill's two-pass path)."""
         w, L = self.w, self.w.layer
         q = self.rng.standard_normal((w.n_rows, L.n_head, L.hd), dtype=np.float32)
-        return _round(q, "f16" if w.kv_type == "q8_0" else w.kv_type)
+        return _round(q, "f16" if w.kv_type == "q8_0" else w.kv_type) if rounded else q
 
 
 def dequant_q8_rows(rows: np.ndarray) -> np.ndarray:
