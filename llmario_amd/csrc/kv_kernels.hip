@@ -775,6 +775,25 @@ __global__ __launch_bounds__(256) void snapshot_tiles_kernel(PageGeom g, SnapGeo
 }
 
 
+// n16 16-byte chunks into LDS, chunk i from src(i) to dst(i), with up to 8 loads in flight per
+// thread: every load of a batch is issued before the first LDS store, so a workgroup pays one
+// memory round trip per batch instead of one per head.
+template <typename SrcF, typename DstF>
+__device__ __forceinline__ void stage16(uint32_t n16, SrcF src, DstF dst) {
+  const uint32_t tid = threadIdx.x;
+  for (uint32_t base = 0; base < n16; base += 8 * 256) {
+    uint4 v0, v1, v2, v3, v4, v5, v6, v7;
+    // chunks past the end re-read the last one (in bounds); only real chunks are stored
+    auto ld = [&](int k) { return *(const uint4*)src(min(base + k * 256 + tid, n16 - 1)); };
+    v0 = ld(0); v1 = ld(1); v2 = ld(2); v3 = ld(3); v4 = ld(4); v5 = ld(5); v6 = ld(6); v7 = ld(7);
+    auto st = [&](int k, const uint4& v) {
+      const uint32_t i = base + k * 256 + tid;
+      if (i < n16) *(uint4*)dst(i) = v;
+    };
+    st(0, v0); st(1, v1); st(2, v2); st(3, v3); st(4, v4); st(5, v5); st(6, v6); st(7, v7);
+  }
+}
+
 // One workgroup per (block, 16-token tile, side) covering every KV head: the page side of that
 // unit (each head's codes, then each head's q8_0 scales) and its reference side (16 rows of
 // n_kv * seg bytes, one contiguous run) are both staged whole, so HBM sees only 16-byte
@@ -797,6 +816,23 @@ __device__ inline void snapshot_side(const PageGeom& g, const SnapGeom& sg, uint
   uint8_t* rows = snap + (size_t)bi * sg.bb + sg.ref_off + (is_v ? (size_t)sg.bt * sg.k_row : 0) + (size_t)(t * 16) * row;
   uint8_t* pg_l = smem;                                  // [nkv][PH] page image
   uint8_t* rw_l = smem + ((nkv * PH + 15) & ~15u);       // [16 rows][row] (read direction)
+  // the page side (each head's codes, then its q8_0 scales) staged into pg_l, and the rows staged
+  // into rw_l, each with its loads batched
+  auto stage_page = [&]() {
+    constexpr uint32_t C16 = PH / 16, T16 = TB / 16;
+    stage16(
+        nkv * C16,
+        [&](uint32_t i) -> const uint8_t* {
+          const uint32_t h = i / C16, r = i - h * C16;
+          const uint8_t* src = head0 + (size_t)h * sd.head;
+          return r < T16 ? src + t * TB + r * 16 : src + sd.scale + t * TS + (r - T16) * 16;
+        },
+        [&](uint32_t i) -> uint8_t* { return pg_l + (size_t)i * 16; });
+  };
+  auto stage_rows = [&]() {
+    stage16(span / 16, [&](uint32_t i) -> const uint8_t* { return rows + (size_t)i * 16; },
+            [&](uint32_t i) -> uint8_t* { return rw_l + (size_t)i * 16; });
+  };
   // page byte of (token m, byte u of a head's row segment), relative to the head's staged bytes
   auto page_byte = [&](uint32_t m, uint32_t u) -> uint32_t {
     if constexpr (TYPE == KV_Q8) {
@@ -816,16 +852,10 @@ __device__ inline void snapshot_side(const PageGeom& g, const SnapGeom& sg, uint
     constexpr uint32_t NB = DIM / 32;
     auto scale_at = [&](uint32_t h, uint32_t m, uint32_t b) { return (uint16_t*)(pg_l + h * PH + TB + (m * NB + b) * 2u); };
     auto row_at = [&](uint32_t h, uint32_t m, uint32_t b) { return (uint16_t*)(rw_l + m * row + h * SEG + b * 34u); };
-    if (WRITE) {
-      for (uint32_t h = 0; h < nkv; h++) {
-        const uint8_t* src = head0 + (size_t)h * sd.head;
-        for (uint32_t o = tid * 16; o < TB; o += 256 * 16) *(uint4*)(pg_l + h * PH + o) = *(const uint4*)(src + t * TB + o);
-        for (uint32_t o = tid * 4; o < TS; o += 256 * 4)
-          *(uint32_t*)(pg_l + h * PH + TB + o) = *(const uint32_t*)(src + sd.scale + t * TS + o);
-      }
-    } else {
-      for (uint32_t o = tid * 16; o < span; o += 256 * 16) *(uint4*)(rw_l + o) = *(const uint4*)(rows + o);
-    }
+    if (WRITE)
+      stage_page();
+    else
+      stage_rows();
     __syncthreads();
     if constexpr (!IS_V) {
       for (uint32_t un = tid; un < 16 * nkv * NB; un += 256) {
@@ -903,13 +933,7 @@ __device__ inline void snapshot_side(const PageGeom& g, const SnapGeom& sg, uint
     return;
   }
   if (WRITE) {
-    for (uint32_t h = 0; h < nkv; h++) {
-      const uint8_t* src = head0 + (size_t)h * sd.head;
-      for (uint32_t o = tid * 16; o < TB; o += 256 * 16) *(uint4*)(pg_l + h * PH + o) = *(const uint4*)(src + t * TB + o);
-      if constexpr (TS > 0)
-        for (uint32_t o = tid * 4; o < TS; o += 256 * 4)
-          *(uint32_t*)(pg_l + h * PH + TB + o) = *(const uint32_t*)(src + sd.scale + t * TS + o);
-    }
+    stage_page();
     __syncthreads();
     for (uint32_t c = tid; c < span / 16; c += 256) {
       const uint32_t x0 = c * 16;
@@ -934,7 +958,7 @@ __device__ inline void snapshot_side(const PageGeom& g, const SnapGeom& sg, uint
       *(uint4*)(rows + x0) = make_uint4(w4[0], w4[1], w4[2], w4[3]);
     }
   } else {
-    for (uint32_t o = tid * 16; o < span; o += 256 * 16) *(uint4*)(rw_l + o) = *(const uint4*)(rows + o);
+    stage_rows();
     __syncthreads();
     for (uint32_t c = tid; c < span / 16; c += 256) {
       const uint32_t x0 = c * 16;
