@@ -266,8 +266,9 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
  *     Applies to f16 / bf16 pages: q8_0 prompts always carry their scaled weights as bf16 hi + lo.
  *   prefill_min_rows: segments of at least this many rows go to the matrix-core prefill kernel
  *     (default 16; 1 .. 2^32).
- *   decode_target_items: split-K target of decode work items (default: the items the device holds
- *     at once, from the occupancy query).
+ *   decode_target_items: split-K target of decode work items (default: half the items the device
+ *     holds at once, from the occupancy query, for the matrix-core decode kernel; all of them for
+ *     f32 and row-layout layers).
  *   decode_min_tiles: smallest split-K chunk in 16-key tiles (default 8; 2 for f32 pages; 4 for
  *     row-layout layers; 1 .. 64).
  * Out-of-range values fail with LMH_INVALID_ARGUMENT and change nothing. */

@@ -1473,10 +1473,17 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   total_tiles *= (uint64_t)y.n_kv * head_blocks;
   // Items the GPU holds at once: with at most that many, every item starts in the first round and
   // none waits for a slot to free up (a second, mostly empty round would double the kernel time).
+  // The matrix-core decode kernel targets half of them: one item per SIMD streams each key range
+  // with its two-deep prefetch as fast as two do, and half the items halve the per-item start-up,
+  // the partials and the merge (often to none: 128 rows of 512 keys become one item per row and
+  // KV head, 56.4 -> 42.6 us; c2 cold 51.2 -> 49.6 us; 4 rows of 16 K keys 54.0 -> 48.9 us; c4 and
+  // rows of a group of 8 unchanged). The f32 and row-layout kernels, latency-bound, keep all of them.
   if (kv->decode_capacity[layer] == 0)
     kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd, y.hdv, group, y.layout) * kv->n_cu;
-  uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items
-                                                               : kv->decode_capacity[layer], 1);
+  const bool mfma_decode = y.layout == LAYOUT_TILES && kv->kv_type != LMH_KV_F32;
+  const uint64_t cap_target = mfma_decode ? std::max<uint64_t>(kv->decode_capacity[layer] / 2, kv->n_cu)
+                                          : kv->decode_capacity[layer];
+  uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items : cap_target, 1);
   // no-allocation calls: at most as many split slots (and merges) as the scratch holds
   const size_t slot_bytes = (size_t)ng * (y.hdv + 4) * 4;
   if (noalloc) target = std::max<uint64_t>(1, std::min<uint64_t>(target, NOALLOC_SCRATCH_BYTES / (slot_bytes + sizeof(MergeItem))));
