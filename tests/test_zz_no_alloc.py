@@ -45,15 +45,16 @@ def test_noalloc_matches_attend_twice_second_smaller(cuda, kv):
         assert np.array_equal(a, b)   # same plan, same kernels: the same bits
 
 
-def test_noalloc_mixed_call_matches(cuda):
-    w = small("nam", "bf16", Layer(32, 8, 128, 128), prior=[2500, 0, 900], new=[1, 200, 1], seed=4)
+@pytest.mark.parametrize("kv", ["bf16", "q8_0"])
+def test_noalloc_mixed_call_matches(cuda, kv):
+    w = small("nam", kv, Layer(32, 8, 128, 128), prior=[2500, 0, 900], new=[1, 200, 1], seed=4)
     gen = Generator(w)
     hc = harness.load(w, gen)
     q = gen.q()
     a, b = both(hc, w, q)
     err = row_rel_err(b, a)
-    print(f"mixed: noalloc vs attend {err:.3e}")
-    assert err <= TOL["bf16"] and np.array_equal(a, b)
+    print(f"mixed {kv}: noalloc vs attend {err:.3e}")
+    assert err <= TOL[kv] and np.array_equal(a, b)
 
 
 def test_noalloc_refuses_a_call_beyond_its_scratch(cuda):
