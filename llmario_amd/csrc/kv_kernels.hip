@@ -703,6 +703,252 @@ __global__ __launch_bounds__(256) void qk_rope_store_quad_kernel(PageGeom g, Rop
                         row_seq, row_pos, q, k, v, q_out);
 }
 
+// Sum over each group of 8 lanes, the same bits in all 8 (DPP: lane l + lane 7-l, then the quad
+// swaps 1 and 2; every lane adds the same pairs, only in another order of operands).
+__device__ inline float lanes8_sum(float s) {
+  s += __builtin_amdgcn_update_dpp(0.f, s, 0x141, 0xf, 0xf, false);  // row_half_mirror
+  s += __builtin_amdgcn_update_dpp(0.f, s, 0xb1, 0xf, 0xf, false);   // quad_perm [1,0,3,2]
+  s += __builtin_amdgcn_update_dpp(0.f, s, 0x4e, 0xf, 0xf, false);   // quad_perm [2,3,0,1]
+  return s;
+}
+// Sum over each half wave (32 lanes), the same bits in all of them.
+__device__ inline float lanes32_sum(float s) {
+  s = lanes8_sum(s);
+  s += __builtin_amdgcn_update_dpp(0.f, s, 0x140, 0xf, 0xf, false);  // row_mirror: + lane 15-l
+  return s + __shfl_xor(s, 16);
+}
+// Two values in the page's 16-bit type (round to nearest even; v_cvt_pk_{bf16,f16}_f32).
+template <bool BF>
+__device__ inline uint32_t pack16x2(float a, float b) {
+  if constexpr (BF) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 h = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  } else {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const h2 h = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(uint32_t, h);
+  }
+}
+
+// An aligned run of 4 f16 / bf16 tokens when hd == hdv == HD (64, 128, 256) and every rotated
+// pair sits in one lane (Normal pairs; Neox over all HD dims): the same results as
+// rope_tokens<HD / 64, 4>, with the work counted in slots of two heads of one kind (Q, K or V) for
+// the run's four tokens, so every lane of a wave runs the same code, and every access 8 or 16
+// bytes wide.
+//   Q / K slot: lane L holds row (head 2s + (L >> 3 & 1), token L >> 4), the float4s
+//   sub + 8f (sub = L & 7, f < HD/64) of each half row: a row's loads are whole 128-byte runs,
+//   Neox partners (e, e + HD/2) share the lane, the sum of squares is an 8-lane DPP reduction,
+//   and each float4 of K is half of one 16-byte operand row of the tile (8 dims of one key).
+//   V slot: lane L takes head 2s + (L >> 5) and HD/64 consecutive 16-byte tile chunks: dims d and
+//   d + 16 of the four keys, loaded from the four rows and written with one store per chunk.
+// Slots y*spw .. y*spw+spw-1 of [Q pairs][K pairs][V pairs] are the workgroup's share.
+template <int HD, bool BF>
+__device__ void rope_quad_slots(const PageGeom& g, const RopeGeom& r, float2 (*cs)[ROPE_MAX_DIM / 2], uint32_t row0,
+                                uint32_t s0, uint32_t s1, const int32_t* row_seq, const int32_t* row_pos,
+                                const float* q, const float* k, const float* v, float* q_out) {
+  constexpr uint32_t NF = HD / 64, H2 = HD / 2;
+  typedef float fc __attribute__((ext_vector_type(NF)));
+  const uint32_t tid = threadIdx.x, lane = tid & 63u;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t qs = (r.n_head + 1) / 2, ks = (g.n_kv + 1) / 2;
+  const uint32_t sub = lane & 7u, hsel = (lane >> 3) & 1u, t = lane >> 4;
+  const size_t row = row0 + t;
+  const uint32_t q0 = (lane & 31u) * NF, d0 = 32u * (q0 >> 4) + (q0 & 15u);  // a V slot's dims
+  // the values of slot sn, requested one slot ahead of their use (the first before the
+  // workgroup's angles and page slot). Q / K: the lane's float4s of its row; V: dims d0 .. and
+  // d0+16 .. of the four tokens, as fc values 0..3 and 4..7 of the same registers
+  auto load_slot = [&](uint32_t sn, float4 (&x)[2][NF]) {
+    if (sn < qs + ks) {
+      const bool isq = sn < qs;
+      const uint32_t hh = 2 * (isq ? sn : sn - qs) + hsel;
+      const bool on = hh < (isq ? r.n_head : g.n_kv);
+      const float* src = isq ? q + (row * r.n_head + hh) * r.q_stride : k + (row * g.n_kv + hh) * HD;
+#pragma unroll
+      for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+        for (uint32_t f = 0; f < NF; f++)
+          x[hb][f] = on ? *(const float4*)(src + hb * H2 + 4 * (sub + 8 * f)) : make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      const uint32_t hv = 2 * (sn - qs - ks) + (lane >> 5);
+      const bool on = hv < g.n_kv;
+      fc* p = (fc*)&x[0][0];
+#pragma unroll
+      for (uint32_t tt = 0; tt < 4; tt++) {
+        const float* src = v + ((size_t)(row0 + tt) * g.n_kv + hv) * HD;
+        p[tt] = on ? *(const fc*)(src + d0) : fc{};
+        p[4 + tt] = on ? *(const fc*)(src + d0 + 16) : fc{};
+      }
+    }
+  };
+  float4 xn[2][NF];
+  if (s0 + w < s1) load_slot(s0 + w, xn);
+  const uint32_t pos0 = (uint32_t)row_pos[row0];
+  const uint32_t half = r.half_rot;
+  for (uint32_t i = tid; i < 4 * half; i += blockDim.x) {
+    const uint32_t tk = i / half, ii = i - tk * half;
+    float angle = (float)(pos0 + tk) * r.freq_scale * r.freq[ii];
+    if (r.freq_div) angle = angle / r.freq_div[ii];
+    float sn, cn;
+    sincosf(angle, &sn, &cn);
+    cs[tk][ii] = make_float2(cn * r.attn_factor, sn * r.attn_factor);
+  }
+  const Slot sl0 = locate(g, row_seq[row0], pos0);
+  __syncthreads();
+  const bool neox = (r.flags & ROPE_NEOX) != 0;
+  // rotation factors of the lane's elements, the same for every Q / K slot: Neox, element c of
+  // float4 f pairs with the same element of the other half (angle 4(sub+8f)+c); Normal, the two
+  // pairs of the first half's float4 ([0], [1]) and of the second half's ([2], [3])
+  float2 cf[NF][4];
+#pragma unroll
+  for (uint32_t f = 0; f < NF; f++) {
+    const uint32_t e = 4 * (sub + 8 * f);
+#pragma unroll
+    for (uint32_t c = 0; c < 4; c++) {
+      const uint32_t i = neox ? e + c : (c < 2 ? e / 2 + c : H2 / 2 + e / 2 + c - 2);
+      cf[f][c] = i < half ? cs[t][i] : make_float2(1.f, 0.f);
+    }
+  }
+  float4 wn[2][NF];   // norm weights of the lane's elements for the kind in hand
+  uint32_t wn_kind = 3;
+  for (uint32_t s = s0 + w; s < s1; s += 4) {
+    const uint32_t kind = s < qs ? 0u : s < qs + ks ? 1u : 2u;
+    float4 x[2][NF];
+#pragma unroll
+    for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+      for (uint32_t f = 0; f < NF; f++) x[hb][f] = xn[hb][f];
+    if (s + 4 < s1) load_slot(s + 4, xn);
+    if (kind < 2) {
+      const uint32_t hh = 2 * (kind == 0 ? s : s - qs) + hsel;
+      const bool on = hh < (kind == 0 ? r.n_head : g.n_kv);
+      if (kind == 0 ? (r.flags & ROPE_Q_NORM) != 0 : (r.flags & ROPE_K_NORM) != 0) {
+        if (wn_kind != kind) {
+          const float* wsrc = kind == 0 ? r.q_norm : r.k_norm;
+#pragma unroll
+          for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+            for (uint32_t f = 0; f < NF; f++)
+              wn[hb][f] = wsrc ? *(const float4*)(wsrc + hb * H2 + 4 * (sub + 8 * f)) : make_float4(1.f, 1.f, 1.f, 1.f);
+          wn_kind = kind;
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+          for (uint32_t f = 0; f < NF; f++)
+            ss += x[hb][f].x * x[hb][f].x + x[hb][f].y * x[hb][f].y + x[hb][f].z * x[hb][f].z + x[hb][f].w * x[hb][f].w;
+        const float scale = 1.0f / sqrtf(lanes8_sum(ss) / (float)HD + r.eps);
+#pragma unroll
+        for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+          for (uint32_t f = 0; f < NF; f++) {
+            x[hb][f].x = x[hb][f].x * scale * wn[hb][f].x;
+            x[hb][f].y = x[hb][f].y * scale * wn[hb][f].y;
+            x[hb][f].z = x[hb][f].z * scale * wn[hb][f].z;
+            x[hb][f].w = x[hb][f].w * scale * wn[hb][f].w;
+          }
+      }
+      if (half) {
+#pragma unroll
+        for (uint32_t f = 0; f < NF; f++) {
+          if (neox) {
+            float* a = (float*)&x[0][f];
+            float* b = (float*)&x[1][f];
+#pragma unroll
+            for (uint32_t c = 0; c < 4; c++) {
+              const float xa = a[c], xb = b[c];
+              a[c] = xa * cf[f][c].x - xb * cf[f][c].y;
+              b[c] = xa * cf[f][c].y + xb * cf[f][c].x;
+            }
+          } else {
+#pragma unroll
+            for (uint32_t hb = 0; hb < 2; hb++) {
+              float* a = (float*)&x[hb][f];
+#pragma unroll
+              for (uint32_t p = 0; p < 2; p++) {
+                const float2 c = cf[f][2 * hb + p];
+                const float x0 = a[2 * p], x1 = a[2 * p + 1];
+                a[2 * p] = x0 * c.x - x1 * c.y;
+                a[2 * p + 1] = x0 * c.y + x1 * c.x;
+              }
+            }
+          }
+        }
+      }
+      if (!on) continue;
+      if (kind == 0) {
+        float* dst = q_out + (row * r.n_head + hh) * HD;
+#pragma unroll
+        for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+          for (uint32_t f = 0; f < NF; f++) *(float4*)(dst + hb * H2 + 4 * (sub + 8 * f)) = x[hb][f];
+      } else {
+        uint8_t* head = sl0.base + g.k_off + hh * g.k_head + sl0.tile * g.k_tile;
+#pragma unroll
+        for (uint32_t hb = 0; hb < 2; hb++)
+#pragma unroll
+          for (uint32_t f = 0; f < NF; f++)
+            *(uint2*)(head + k16_off(sl0.m + t, hb * H2 + 4 * (sub + 8 * f))) =
+                make_uint2(pack16x2<BF>(x[hb][f].x, x[hb][f].y), pack16x2<BF>(x[hb][f].z, x[hb][f].w));
+      }
+    } else {
+      const uint32_t hv = 2 * (s - qs - ks) + (lane >> 5);
+      const bool on = hv < g.n_kv;
+      const fc* p = (const fc*)&x[0][0];
+      fc a[4], b[4];  // dims d0 .. d0+NF-1 and d0+16 .. of the four tokens
+#pragma unroll
+      for (uint32_t tt = 0; tt < 4; tt++) {
+        a[tt] = p[tt];
+        b[tt] = p[4 + tt];
+      }
+      if (r.flags & ROPE_V_NORM) {
+#pragma unroll
+        for (uint32_t tt = 0; tt < 4; tt++) {
+          float ss = 0.f;
+#pragma unroll
+          for (uint32_t c = 0; c < NF; c++) ss += a[tt][c] * a[tt][c] + b[tt][c] * b[tt][c];
+          const float scale = 1.0f / sqrtf(lanes32_sum(ss) / (float)HD + r.eps);
+#pragma unroll
+          for (uint32_t c = 0; c < NF; c++) {
+            a[tt][c] = a[tt][c] * scale;
+            b[tt][c] = b[tt][c] * scale;
+          }
+        }
+      }
+      if (!on) continue;
+      uint8_t* head = sl0.base + g.v_off + hv * g.v_head + sl0.tile * g.v_tile;
+#pragma unroll
+      for (uint32_t c = 0; c < NF; c++)
+        *(uint4*)(head + v16_off(sl0.m, d0 + c)) =
+            make_uint4(pack16x2<BF>(a[0][c], a[1][c]), pack16x2<BF>(a[2][c], a[3][c]),
+                       pack16x2<BF>(b[0][c], b[1][c]), pack16x2<BF>(b[2][c], b[3][c]));
+    }
+  }
+}
+
+// The launch of rope_quad_slots: workgroups x < n_quads take an aligned run of 4 tokens and
+// slots y*spw .. ; the others one remaining row and items y*ipw .. (rope_tokens<HD / 64, 1>).
+template <int HD, bool BF>
+__global__ __launch_bounds__(256) void qk_rope_store_slots_kernel(PageGeom g, RopeGeom r, const int32_t* quads,
+                                                                  uint32_t n_quads, const int32_t* rest,
+                                                                  const int32_t* row_seq, const int32_t* row_pos,
+                                                                  const float* q, const float* k, const float* v,
+                                                                  float* q_out, uint32_t ipw, uint32_t spw) {
+  __shared__ float2 cs[4][ROPE_MAX_DIM / 2];
+  if (blockIdx.x < n_quads) {
+    const uint32_t n_slots = (r.n_head + 1) / 2 + 2 * ((g.n_kv + 1) / 2);
+    const uint32_t s0 = blockIdx.y * spw, s1 = min(n_slots, s0 + spw);
+    if (s0 >= s1) return;
+    rope_quad_slots<HD, BF>(g, r, cs, (uint32_t)quads[blockIdx.x], s0, s1, row_seq, row_pos, q, k, v, q_out);
+  } else {
+    const uint32_t it0 = blockIdx.y * ipw, n_items = min(r.n_head + 2 * g.n_kv, it0 + ipw);
+    if (it0 >= n_items) return;
+    rope_tokens<HD / 64, 1>(g, r, cs, rest ? (uint32_t)rest[blockIdx.x - n_quads] : blockIdx.x - n_quads, it0,
+                            n_items, row_seq, row_pos, q, k, v, q_out);
+  }
+}
+
 struct SnapGeom {
   uint32_t seq, bt, k_row, v_row;
   uint64_t bb, ref_off;
@@ -1062,6 +1308,33 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
       n_quads = 0;
       rest = nullptr;
       n_rest = n_rows;
+    }
+    // the slot kernel: hd == hdv in {64, 128, 256}, rotated pairs inside a lane (Normal, or Neox
+    // over all dims), every row and weight vector 16-byte aligned
+    const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+    const bool slots = quad_ok && g.hd == g.hdv && (g.hd == 64 || g.hd == 128 || g.hd == 256) &&
+                       (!neox || half == 0 || half == g.hd / 2) && r.q_stride % 4 == 0 && al16(q) && al16(k) &&
+                       al16(v) && al16(q_out) && al16(r.q_norm) && al16(r.k_norm);
+    if (slots) {
+      // slots (two heads of one kind for a run's 4 tokens) split over workgroups until the grid
+      // holds about 1024 of them, at least one slot per wave; the remaining rows take items
+      // (heads) in as many shares
+      const uint32_t n_wg = n_quads + n_rest, n_items = r.n_head + 2 * g.n_kv;
+      const uint32_t n_slots = (r.n_head + 1) / 2 + 2 * ((g.n_kv + 1) / 2), max_split = (n_slots + 3) / 4;
+      const uint32_t split = std::min(max_split, std::max(1u, (1024u + n_wg - 1) / n_wg));
+      const uint32_t spw = (n_slots + split - 1) / split, ipw = ((n_items + split - 1) / split + 3) & ~3u;
+      const dim3 grid(n_wg, std::max((n_slots + spw - 1) / spw, (n_items + ipw - 1) / ipw));
+#define LMH_SLOTS(H, B)                                                                                            \
+  LMH_LAUNCH(ev, (qk_rope_store_slots_kernel<H, B>), grid, dim3(256), 0, s, g, r, quads, n_quads, rest, row_seq, \
+             row_pos, q, k, v, q_out, ipw, spw)
+      const bool bf = g.kv_type == KV_BF16;
+      switch (g.hd) {
+        case 64: if (bf) LMH_SLOTS(64, true); else LMH_SLOTS(64, false); break;
+        case 128: if (bf) LMH_SLOTS(128, true); else LMH_SLOTS(128, false); break;
+        default: if (bf) LMH_SLOTS(256, true); else LMH_SLOTS(256, false); break;
+      }
+#undef LMH_SLOTS
+      return hipGetLastError();
     }
     if (quad_ok || n_rows < 1024) {
       const uint32_t n_wg = n_quads + n_rest, n_items = r.n_head + 2 * g.n_kv, max_split = (n_items + 7) / 8;

@@ -58,6 +58,11 @@ CASES = [
     # Neox over 96 of 128 dims: partners 24 lanes apart, so the LDS-staged kernel runs
     ("f16", 8, 2, 128, 128, 96, True, True, True, True, 0, False, 1e4),
     ("q8_0", 8, 4, 128, 128, 96, True, False, True, False, 0, True, 1e6),
+    # the slot kernel's other widths and its odd head counts (a pair slot with one head)
+    ("bf16", 8, 2, 256, 256, 256, True, True, True, True, 0, False, 1e6),
+    ("f16", 6, 2, 64, 64, 64, True, True, False, True, 0, True, 1e4),
+    ("f16", 9, 3, 128, 128, 128, True, True, True, True, 0, False, 1e4),
+    ("bf16", 4, 1, 128, 128, 128, False, True, True, False, 256, False, 1e4),
 ]
 
 
