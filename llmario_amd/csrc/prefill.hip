@@ -27,8 +27,9 @@
 // the per-row bound on rows whose output cancels): each wave's DMA brings a page tile's int8 codes
 // and its f16 scales into LDS, the thread that loaded the codes rewrites them in place as
 // int8-valued f16 (K) or bf16 (V), both exact, and the products apply the scales:
-//   S^T = sum over 32-dim chunks c of d_K[key][c] * (K_c . Q_c^T)   (one MFMA chain per chunk, Q as
-//         f16 hi + lo, so q8_0 units always run the two-pass form)
+//   S^T = sum over 32-dim chunks c of d_K[key][c] * (K_c . Q_c^T)   (one MFMA per chunk and column
+//         block: a Q exact in f16 runs one pass of 32 columns, any other Q the two-pass form with
+//         its hi + lo products summed before the scale)
 //   O^T += V^T . (P * d_V[.][b])^T per 32-dim V block b, the scaled weights as bf16 hi + lo
 //         (v_mfma_f32_16x16x32_bf16; bf16 has f32's range, so no product of a weight and a scale
 //         leaves it)
@@ -386,7 +387,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   };
   // bf16 pages: a Q held in bf16 values multiplies bf16 K exactly on the bf16 matrix cores, so K
   // needs no widening; qf then holds bf16 bits (split_q_bf16). Any other Q takes the two-pass f16
-  // hi + lo path with K widened.
+  // hi + lo path with K widened. q8_0 pages: the codes are widened to f16 either way; a Q exact in
+  // f16 runs one pass.
   auto split_q_bf16 = [&](const float4 (&raw)[NC][2], h8 (&hi)[NC]) {
     bool nz = false;
 #pragma unroll
@@ -406,12 +408,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     return nz;
   };
   h8 qf[2][NC];
-  if (Q8 && pass == 0) {   // q8_0: always the two-pass form (the scaled Q.K products take Q as hi + lo)
-    const int32_t* tab = g.table + (size_t)it.seq * g.bps;
-    for (uint32_t p = tid; p < n_pages; p += NT) blk_lds[p] = tab[((page0 + p) << 4) >> g.bt_shift];
-    __syncthreads();
-    lo_any = true;
-  } else if (pass == 0) {
+  if (pass == 0) {
     bool lo_need = false;
     {
       float4 raw[2][NC][2];
@@ -543,6 +540,23 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // S^T for the 32 keys of a half (two 16-key page tiles) x the pass's columns (LO: the hi and
   // lo products of one column block, summed)
   auto qk = [&](f4 (&S)[2][NCB], const KOps& ko) {
+    if constexpr (Q8 && !LO) {   // per chunk: Q (exact in f16) against the codes, times the key's scale
+#pragma unroll
+      for (int ch = 0; ch < NC; ch++) {
+#pragma unroll
+        for (int kk = 0; kk < 2; kk++) {
+          const h8 a = __builtin_bit_cast(h8, ko.a[ch][kk]);
+#pragma unroll
+          for (int cb = 0; cb < NCB; cb++) {
+            const f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+              S[kk][cb][r] = fmaf(t[r], dtile::scale_at<NC>(ko.s[kk], r, ch), ch == 0 ? nm[cb] : S[kk][cb][r]);
+          }
+        }
+      }
+      return;
+    }
     if constexpr (Q8) {   // (two-pass form) per chunk: the hi + lo products, times the key's scale
 #pragma unroll
       for (int ch = 0; ch < NC; ch++) {
@@ -686,23 +700,26 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   };
   // O^T += V^T P^T over a half, 32 keys per MFMA
   auto pv = [&](const h8 (&Ph)[NCB], const h8 (&Pl)[NCB], const VOps& vo) {
-    if constexpr (Q8) {   // (two-pass form) per 32-dim V block b: P * d_V[key][b] as bf16 hi + lo
+    if constexpr (Q8) {   // per 32-dim V block b: P * d_V[key][b] as bf16 hi + lo
 #pragma unroll
       for (int b = 0; b < NC; b++) {
-        uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const int e0 = 2 * i, e1 = 2 * i + 1;   // weight e: key 4g + e%4 of page tile e/4
-          split_pair_bf16(pq[0][e0] * dtile::scale_at<NC>(vo.s[e0 / 4], e0 % 4, b),
-                          pq[0][e1] * dtile::scale_at<NC>(vo.s[e1 / 4], e1 % 4, b), hw[i], lw[i]);
-        }
-        const dtile::b8 ph = __builtin_bit_cast(dtile::b8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
-        const dtile::b8 pl = __builtin_bit_cast(dtile::b8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+        for (int x = 0; x < NX; x++) {
+          uint32_t hw[4], lw[4];
 #pragma unroll
-        for (int jj = 0; jj < 2; jj++) {
-          const dtile::b8 va = __builtin_bit_cast(dtile::b8, vo.a[2 * b + jj]);
-          O[2 * b + jj][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, O[2 * b + jj][0], 0, 0, 0);
-          O[2 * b + jj][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, O[2 * b + jj][0], 0, 0, 0);
+          for (int i = 0; i < 4; i++) {
+            const int e0 = 2 * i, e1 = 2 * i + 1;   // weight e: key 4g + e%4 of page tile e/4
+            split_pair_bf16(pq[x][e0] * dtile::scale_at<NC>(vo.s[e0 / 4], e0 % 4, b),
+                            pq[x][e1] * dtile::scale_at<NC>(vo.s[e1 / 4], e1 % 4, b), hw[i], lw[i]);
+          }
+          const dtile::b8 ph = __builtin_bit_cast(dtile::b8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+          const dtile::b8 pl = __builtin_bit_cast(dtile::b8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
+#pragma unroll
+          for (int jj = 0; jj < 2; jj++) {
+            const dtile::b8 va = __builtin_bit_cast(dtile::b8, vo.a[2 * b + jj]);
+            O[2 * b + jj][x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, ph, O[2 * b + jj][x], 0, 0, 0);
+            O[2 * b + jj][x] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pl, O[2 * b + jj][x], 0, 0, 0);
+          }
         }
       }
       return;
@@ -842,11 +859,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   __syncthreads();
   };
 
-  if constexpr (Q8) {
-    run(std::true_type{}, pass);
-    pass ^= 1u;
-    if (pass == 0) unit++;
-  } else if (!lo_any) {
+  if (!lo_any) {
     run(std::false_type{}, 0);
     unit++;
   } else {
