@@ -867,10 +867,12 @@ __device__ void rope_quad_slots(const PageGeom& g, const RopeGeom& r, float2 (*c
               float* a = (float*)&x[hb][f];
 #pragma unroll
               for (uint32_t p = 0; p < 2; p++) {
+                // pairs past the rotated dims keep their values as they are (no x*1 - y*0)
+                const bool rp = hb * (H2 / 2) + 2 * (sub + 8 * f) + p < half;
                 const float2 c = cf[f][2 * hb + p];
                 const float x0 = a[2 * p], x1 = a[2 * p + 1];
-                a[2 * p] = x0 * c.x - x1 * c.y;
-                a[2 * p + 1] = x0 * c.y + x1 * c.x;
+                a[2 * p] = rp ? x0 * c.x - x1 * c.y : x0;
+                a[2 * p + 1] = rp ? x0 * c.y + x1 * c.x : x1;
               }
             }
           }
