@@ -178,6 +178,7 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   it.p1 = __builtin_amdgcn_readfirstlane(it.p1);
   it.slot = __builtin_amdgcn_readfirstlane(it.slot);
   it.seq = __builtin_amdgcn_readfirstlane(it.seq);
+  it.blk0 = __builtin_amdgcn_readfirstlane(it.blk0);
   const int seq = (int)it.seq;
   const int32_t* tab = g.table + (size_t)seq * g.bps;
   const uint32_t hq = lane & 15u, grp = lane >> 4;
@@ -220,9 +221,10 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
   int my_blk = 0;
   if (t0 + lane <= t1) my_blk = tab[((t0 + lane) << 4) >> g.bt_shift];
-  auto ptrs = [&](uint32_t t, const uint8_t*& kb, const uint8_t*& vb, const uint8_t*& ksb, const uint8_t*& vsb) {
+  auto ptrs = [&](uint32_t t, const uint8_t*& kb, const uint8_t*& vb, const uint8_t*& ksb, const uint8_t*& vsb,
+                  bool first = false) {
     const uint32_t pos = t << 4;
-    const int blk = __builtin_amdgcn_readlane(my_blk, (int)(t - t0));
+    const int blk = first ? (int)it.blk0 : __builtin_amdgcn_readlane(my_blk, (int)(t - t0));
     const uint32_t sub = (pos & bt_mask) >> 4;
     const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
     const uint8_t* kh = base + g.k_off + it.kvh * g.k_head;
@@ -232,9 +234,9 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
     ksb = kh + g.k_scale + sub * g.k_tile_s;
     vsb = vh + g.v_scale + sub * g.v_tile_s;
   };
-  auto fetch = [&](TileRegs<KVT, HD, HDV>& buf, uint32_t t) {
+  auto fetch = [&](TileRegs<KVT, HD, HDV>& buf, uint32_t t, bool first = false) {
     const uint8_t *kb, *vb, *ksb, *vsb;
-    ptrs(t, kb, vb, ksb, vsb);
+    ptrs(t, kb, vb, ksb, vsb, first);
     load_tile(buf, kb, vb, ksb, vsb, lane);
   };
 
@@ -352,7 +354,7 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   // Two-deep ping-pong: tile t+1 is in flight while tile t is computed. The fetches past the last
   // tile re-read the last tile (in bounds, and unconditional, so the buffers need no copies).
   TileRegs<KVT, HD, HDV> b0, b1;
-  fetch(b0, t0);
+  fetch(b0, t0, true);   // block id from the item: in flight beside the Q and block-table reads
   for (uint32_t t = t0; t <= t1; t += 2) {
     fetch(b1, min(t + 1, t1));
     step(b0, t);

@@ -78,8 +78,8 @@ struct DecodeItem {
   uint32_t h0;
   uint32_t p0, p1;
   uint32_t slot;
-  uint32_t seq;  // the row's sequence (saves a dependent read of the row arrays)
-  uint32_t pad;  // 32-byte items
+  uint32_t seq;   // the row's sequence (saves a dependent read of the row arrays)
+  uint32_t blk0;  // block id of the first tile p0 >> 4 (the first fetch skips the block-table read)
 };
 constexpr uint32_t NO_SLOT = 0xffffffffu;
 

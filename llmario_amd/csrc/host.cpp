@@ -1509,6 +1509,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   kv->items.clear();
   kv->merges.clear();
   uint32_t slots = 0;
+  const int32_t* tab_l = y.win ? kv->h_wtable.data() : kv->h_table.data();   // the layer's block table
   for (uint64_t t = 0; t < n_rows; t++) {
     if (!decode_row[t]) continue;
     const uint64_t pos = (uint64_t)kv->row_pos[t];
@@ -1516,17 +1517,20 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
     const uint64_t hi = pos + 1;
     const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
     const uint64_t n_split = (n_t + chunk - 1) / chunk;
+    const uint32_t seq = (uint32_t)kv->row_seq[t];
+    // block id of the tile holding key p (the table entry the kernel would read for it)
+    auto blk_of = [&](uint64_t p) { return (uint32_t)tab_l[(size_t)seq * kv->bps + (((p >> 4) << 4) >> kv->bt_shift)]; };
     for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
       for (uint32_t hb = 0; hb < head_blocks; hb++) {
         if (n_split == 1) {
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, (uint32_t)kv->row_seq[t], 0});
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, seq, blk_of(lo)});
           continue;
         }
         kv->merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, slots, (uint32_t)n_split, 0});
         for (uint64_t s = 0; s < n_split; s++) {
           const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
           const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++, (uint32_t)kv->row_seq[t], 0});
+          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++, seq, blk_of(p0)});
         }
       }
     }
