@@ -534,7 +534,9 @@ def run_leg(name, fn, errors):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
+    # 200 steps (~11 ms of c2): the synchronisation at each end of the timed run costs ~0.1 ms,
+    # which over 50 steps added ~2 us to every step
+    ap.add_argument("--steps", type=int, default=200)
     # ~0.2 s of c2 steps: the clock needs tens of milliseconds of load to settle (10 warm-up steps
     # left the cold decode kernel at 52.7 us against 50.3 us settled)
     ap.add_argument("--warmup", type=int, default=3000)
