@@ -9,7 +9,8 @@
 // (row, KV head, contiguous key range aligned to 16-token tiles). The key range of a long row is
 // cut into several items (split-K, as attend_split does for long contexts, forward.rs:688-807);
 // their partial (o, m, l) go to `part`, and `merge_kernel` combines them with the exact
-// log-sum-exp merge of forward.rs:772-806.
+// log-sum-exp merge of forward.rs:772-806 (f32 pages with rows of at most 16 tiles: the row's
+// split items are waves of one workgroup and merge there, in LDS; see decode_f32_kernel).
 //
 // f16 / bf16 / q8_0 pages (matrix cores): per 16-token tile,
 //   S^T[16 keys x 16 heads] = K[16 x hd] . Q^T[hd x 16]     (v_mfma_f32_16x16x32_{f16,bf16})
@@ -154,18 +155,30 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
 // NG: query heads per item (the launch's ng when the group is 1, 2, 4 or 8; 16 otherwise, with a
 // run-time guard for a last head block shorter than 16), so the per-head loops carry no guards
 // for the common group sizes.
-template <int HD, int HDV, int NG>
-__global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
+// Instances that run a workgroup-local merge: the item's partials fit a wave's LDS share and the
+// 8-wave instance keeps its registers without spilling.
+template <int HD, int HDV, int N>
+constexpr bool f32_local_ok() {
+  return HD == HDV && N * HDV <= (int)LOCAL_MERGE_MAX && (HD == 64 || (HD == 128 && N <= 2) || (HD == 256 && N <= 4));
+}
+
+template <int HD, int HDV, int NG, int W = WAVES>
+__global__ __launch_bounds__(64 * W) void decode_f32_kernel(PageGeom g, RowGeom r, const DecodeItem* items,
                                                                 uint32_t n_items, const float* q, float* out,
                                                                 float* part, MergeCopy mc) {
   constexpr int ND = HDV / 64 > 0 ? HDV / 64 : 1;  // dims per lane in P.V
-  __shared__ float qs[WAVES][NG][HD];
-  __shared__ float ps[WAVES][NG][64];
+  constexpr int LPH = HDV + 2;                             // a head's partial in LDS: o, m, l
+  constexpr int LPN = NG * HDV <= LOCAL_MERGE_MAX ? NG * LPH : 1;
+  __shared__ float qs[W][NG][HD];
+  __shared__ float ps[W][NG][64];
+  __shared__ float lp[W][LPN];   // local merge: each wave's partials
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
-  const uint32_t wi = blockIdx.x * WAVES + w;
+  const uint32_t wi = blockIdx.x * W + w;
   copy_merges(mc, blockIdx.x == 0);
   const bool active = wi < n_items;
-  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 1, NO_SLOT, 0, 0};
+  // local merge: every wave reaches the workgroup barrier before the merge, active or not
+  const bool local = LPN > 1 && r.local_merge != 0;
+  DecodeItem it = active ? items[wi] : DecodeItem{0, 0, 0, 0, 0, NO_SLOT, 0, 0};
   const uint32_t ng = r.ng;
   // heads of this item; NG < 16 only when it equals the group size, so every item has NG heads
   const uint32_t nh = NG < 16 ? (uint32_t)NG : (it.h0 + ng <= r.group) ? ng : r.group - it.h0;
@@ -176,7 +189,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     }
   }
   __syncthreads();
-  if (!active) return;
+  if (!active && !local) return;
   const int seq = (int)it.seq;
   const int32_t* tab = g.table + (size_t)seq * g.bps;
   const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
@@ -197,7 +210,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     const uint32_t key = c0 + lane;
     return tab[(key < it.p1 ? key : it.p0) >> g.bt_shift];
   };
-  int blk = blk_of(it.p0);
+  int blk = active ? blk_of(it.p0) : 0;
   auto load_v16 = [&](float (&vv)[16][ND], uint32_t c0, uint32_t k0, uint32_t nk) {
 #pragma unroll
     for (int j = 0; j < 16; j++) {
@@ -288,7 +301,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     blk = blk_next;
   }
-  if (it.slot == NO_SLOT) {
+  if (active && it.slot == NO_SLOT) {
 #pragma unroll
     for (int h = 0; h < NG; h++) {
       if (h < (int)nh) {
@@ -299,20 +312,64 @@ __global__ __launch_bounds__(64 * WAVES) void decode_f32_kernel(PageGeom g, RowG
           if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = o[h][i] * inv;
       }
     }
-    return;
   }
+  const bool in_wg = active && it.slot != NO_SLOT && (it.slot & LOCAL_SLOT) != 0;
+  if (active && it.slot != NO_SLOT && !in_wg) {
 #pragma unroll
-  for (int h = 0; h < NG; h++) {
-    if (h < (int)nh) {
-      float* pp = part + ((size_t)it.slot * r.ng + h) * (HDV + 4);
+    for (int h = 0; h < NG; h++) {
+      if (h < (int)nh) {
+        float* pp = part + ((size_t)it.slot * r.ng + h) * (HDV + 4);
 #pragma unroll
-      for (int i = 0; i < ND; i++)
-        if (lane + 64 * i < (uint32_t)HDV) pp[lane + 64 * i] = o[h][i];
-      if (lane == 0) {
-        pp[HDV] = m[h];
-        pp[HDV + 1] = l[h];
+        for (int i = 0; i < ND; i++)
+          if (lane + 64 * i < (uint32_t)HDV) pp[lane + 64 * i] = o[h][i];
+        if (lane == 0) {
+          pp[HDV] = m[h];
+          pp[HDV + 1] = l[h];
+        }
       }
     }
+  }
+  if (!local) return;
+  // Local merge (forward.rs:772-806's log-sum-exp merge, in LDS): each split wave leaves its
+  // partial in lp; after the barrier the row's first wave folds its group's partials.
+  if (in_wg) {
+#pragma unroll
+    for (int h = 0; h < NG; h++) {
+      if (h < (int)nh) {
+#pragma unroll
+        for (int i = 0; i < ND; i++)
+          if (lane + 64 * i < (uint32_t)HDV) lp[w][h * LPH + lane + 64 * i] = o[h][i];
+        if (lane == 0) {
+          lp[w][h * LPH + HDV] = m[h];
+          lp[w][h * LPH + HDV + 1] = l[h];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (!in_wg || ((it.slot >> 8) & 0xffu) != 0) return;
+  const uint32_t n_split = it.slot & 0xffu;
+#pragma unroll
+  for (int h = 0; h < NG; h++) {
+    if (h >= (int)nh) break;
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < n_split; s++) M = fmaxf(M, lp[w + s][h * LPH + HDV]);
+    float L = 0.f, acc[ND];
+#pragma unroll
+    for (int i = 0; i < ND; i++) acc[i] = 0.f;
+    for (uint32_t s = 0; s < n_split; s++) {
+      const float ms = lp[w + s][h * LPH + HDV];
+      const float c = ms == -INFINITY ? 0.f : exp2_fast(ms - M);
+      L = fmaf(c, lp[w + s][h * LPH + HDV + 1], L);
+#pragma unroll
+      for (int i = 0; i < ND; i++)
+        if (lane + 64 * i < (uint32_t)HDV) acc[i] = fmaf(c, lp[w + s][h * LPH + lane + 64 * i], acc[i]);
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float* op = out + ((size_t)it.row * r.n_head + it.kvh * r.group + it.h0 + h) * HDV;
+#pragma unroll
+    for (int i = 0; i < ND; i++)
+      if (lane + 64 * i < (uint32_t)HDV) op[lane + 64 * i] = acc[i] * inv;
   }
 }
 
@@ -466,6 +523,24 @@ hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* ite
                       const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s, const LaunchEv& ev) {
   const dim3 grid((n_items + WAVES - 1) / WAVES), block(64 * WAVES);
   if constexpr (KVT == KV_F32) {
+    if (r.local_merge) {   // a row's split items (up to 8) are waves of one 8-wave workgroup
+      const dim3 grid8((n_items + LOCAL_WAVES - 1) / LOCAL_WAVES), block8(64 * LOCAL_WAVES);
+#define LMH_F32L(N)                                                                                        \
+  if constexpr (f32_local_ok<HD, HDV, N>())                                                                \
+    LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, N, LOCAL_WAVES>), grid8, block8, 0, s, g, r, items, n_items, q, out, \
+               part, mc);                                                                                  \
+  else                                                                                                     \
+    return hipErrorInvalidValue
+      switch (r.group) {
+        case 1: LMH_F32L(1); break;
+        case 2: LMH_F32L(2); break;
+        case 4: LMH_F32L(4); break;
+        case 8: LMH_F32L(8); break;
+        default: LMH_F32L(16); break;
+      }
+#undef LMH_F32L
+      return hipGetLastError();
+    }
     switch (r.group) {
       case 1: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 1>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
       case 2: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 2>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
@@ -618,6 +693,17 @@ bool decode_tiles_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
 }
 
 uint32_t decode_rows_max_heads() { return RNG; }
+
+bool decode_local_merge_ok(uint32_t hd, uint32_t hdv, uint32_t group) {
+  const uint32_t n = group == 1 || group == 2 || group == 4 || group == 8 ? group : 16;
+#define LMH_LOK(H)                                                                                         \
+  if (hd == H && hdv == H)                                                                                 \
+    return n == 1 ? f32_local_ok<H, H, 1>() : n == 2 ? f32_local_ok<H, H, 2>() : n == 4 ? f32_local_ok<H, H, 4>() \
+           : n == 8 ? f32_local_ok<H, H, 8>() : f32_local_ok<H, H, 16>();
+  LMH_LOK(64) LMH_LOK(128) LMH_LOK(256)
+#undef LMH_LOK
+  return false;
+}
 
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
                          const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,

@@ -82,6 +82,12 @@ struct DecodeItem {
   uint32_t blk0;  // block id of the first tile p0 >> 4 (the first fetch skips the block-table read)
 };
 constexpr uint32_t NO_SLOT = 0xffffffffu;
+// A split item merged inside its workgroup (f32 decode of short rows): LOCAL_SLOT | (its index in
+// the row's group << 8) | the group's size; the group's items are consecutive waves of one
+// workgroup, and the first merges their partials from LDS, so the call needs no merge launch.
+constexpr uint32_t LOCAL_SLOT = 0x80000000u;
+constexpr uint32_t LOCAL_MERGE_MAX = 1024;   // heads x hdv of an item whose partials a wave keeps in LDS
+constexpr int LOCAL_WAVES = 8;               // waves per workgroup of a local-merge call (its largest group)
 
 // Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..).
 struct MergeItem {
@@ -100,6 +106,7 @@ struct RowGeom {
   uint32_t ng;             // heads per item = min(group, 16)
   float scale_log2;        // scale * log2(e): scores kept in the log2 domain
   uint32_t window;         // 0 = none
+  uint32_t local_merge;    // f32 decode: split rows merge inside their workgroup (slots LOCAL_SLOT | ...)
 };
 
 // One prefill work unit: KV head `kvh` of sequence `seq`, tokens at positions pos0 .. pos0+n_tok-1
@@ -201,6 +208,8 @@ uint32_t decode_waves_per_cu(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32
 bool decode_tiles_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 // Query heads per work item the row-layout kernel takes (its items use ng <= this).
 uint32_t decode_rows_max_heads();
+// f32 decode: the calls whose split rows may merge inside their workgroup (tile layout instances).
+bool decode_local_merge_ok(uint32_t hd, uint32_t hdv, uint32_t group);
 
 // Prefill (multi-token segments on matrix cores): n_wg workgroups, workgroup b runs the units
 // items[b * per_wg ..] up to the first with n_tok == 0. `max_pages` bounds the key pages of any unit.

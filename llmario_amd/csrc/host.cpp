@@ -1510,7 +1510,48 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   kv->merges.clear();
   uint32_t slots = 0;
   const int32_t* tab_l = y.win ? kv->h_wtable.data() : kv->h_table.data();   // the layer's block table
-  for (uint64_t t = 0; t < n_rows; t++) {
+  // f32 pages, short rows (at most 16 tiles): a row's split items are consecutive waves of one
+  // 8-wave workgroup and merge there (no merge launch). A row splits into 1, 2, 4 or 8 items of
+  // at most 2 tiles (the f32 kernel's smallest chunk); groups of 8 go first, then 4, 2 and single
+  // items, so no group crosses a workgroup. Not with explicit split settings.
+  bool local = false;
+  if (y.layout == LAYOUT_TILES && kv->kv_type == LMH_KV_F32 && decode_local_merge_ok(y.hd, y.hdv, group) &&
+      !kv->decode_target_items && !kv->decode_min_tiles) {
+    uint64_t max_nt = 0;
+    for (uint64_t t = 0; t < n_rows; t++) {
+      if (!decode_row[t]) continue;
+      const uint64_t pos = (uint64_t)kv->row_pos[t];
+      const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+      max_nt = std::max<uint64_t>(max_nt, pos / 16 - lo / 16 + 1);
+    }
+    local = max_nt > 2 && max_nt <= 16;
+  }
+  if (local) {
+    std::vector<DecodeItem> by_size[4];   // groups of 8, 4, 2, single items
+    for (uint64_t t = 0; t < n_rows; t++) {
+      if (!decode_row[t]) continue;
+      const uint64_t pos = (uint64_t)kv->row_pos[t];
+      const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
+      const uint64_t hi = pos + 1;
+      const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
+      const uint32_t n = n_t <= 2 ? 1 : n_t <= 4 ? 2 : n_t <= 8 ? 4 : 8;
+      std::vector<DecodeItem>& dst = by_size[n == 8 ? 0 : n == 4 ? 1 : n == 2 ? 2 : 3];
+      const uint32_t seq = (uint32_t)kv->row_seq[t];
+      auto blk_of = [&](uint64_t p) { return (uint32_t)tab_l[(size_t)seq * kv->bps + (((p >> 4) << 4) >> kv->bt_shift)]; };
+      for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
+        for (uint32_t hb = 0; hb < head_blocks; hb++) {
+          for (uint32_t s = 0; s < n; s++) {
+            const uint64_t a = tlo + s * n_t / n, b = tlo + (s + 1) * n_t / n;
+            const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
+            const uint32_t slot = n == 1 ? NO_SLOT : LOCAL_SLOT | (s << 8) | n;
+            dst.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slot, seq, blk_of(p0)});
+          }
+        }
+      }
+    }
+    for (auto& v : by_size) kv->items.insert(kv->items.end(), v.begin(), v.end());
+  }
+  for (uint64_t t = 0; t < n_rows && !local; t++) {
     if (!decode_row[t]) continue;
     const uint64_t pos = (uint64_t)kv->row_pos[t];
     const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
@@ -1581,6 +1622,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   r.ng = ng;
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
+  r.local_merge = local ? 1u : 0u;
   PrefillGeom pg{};
   pg.n_head = y.n_head;
   pg.group = group;

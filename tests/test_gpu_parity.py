@@ -146,6 +146,12 @@ def test_store_then_gather_is_byte_exact(cuda, kv, bt):
 SMALL = [
     ("f32", Layer(8, 8, 64, 64), [255], [1], 0, 16),
     ("f32", Layer(16, 4, 128, 128), [100, 900], [1, 1], 0, 16),
+    # f32 rows of at most 16 tiles: split items merged inside their workgroup (groups of 8, 4, 2
+    # and single items; a last workgroup with idle waves; a window; a chunk's rows)
+    ("f32", Layer(8, 2, 64, 64), [10, 70, 130, 250, 40], [1, 1, 1, 1, 1], 0, 16),
+    ("f32", Layer(8, 4, 128, 128), [200, 100, 20], [1, 1, 1], 0, 16),
+    ("f32", Layer(8, 2, 64, 64), [300, 40], [1, 1], 100, 32),
+    ("f32", Layer(8, 2, 64, 64), [150], [12], 0, 16),
     ("f16", Layer(32, 8, 128, 128), [700, 33, 1500, 0], [1, 1, 1, 1], 0, 16),
     ("f16", Layer(16, 1, 128, 128), [5000], [1], 0, 32),
     ("f16", Layer(40, 8, 128, 128), [100, 333], [1, 17], 0, 16),
