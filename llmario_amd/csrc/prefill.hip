@@ -104,13 +104,22 @@ __device__ inline uint32_t bf2_to_h2(uint32_t w) {
 }
 
 // Weights (a, b) as packed bf16 hi parts and packed bf16 lo parts (a - hi, b - hi), both rounded to
-// nearest even: 16 significant bits per weight.
+// nearest even: 16 significant bits per weight (|w - hi - lo| <= 2^-18 |w|). Each difference is one
+// v_dot2c_f32_bf16 that reads the packed hi parts directly: (-1, 0) . (hi_a, hi_b) + a, exact (the
+// product is exact and a - hi is representable). The two constant pairs stay in VGPRs (an empty
+// asm statement hides their values): as an inline constant the compiler encodes (-1, 0) as -1.0,
+// which this instruction reads as the 32-bit pattern 0xbf800000, i.e. the pair (0, -1) (checked on
+// the GPU: every lane's first difference came out as a - hi_b).
 __device__ inline void split_pair_bf16(float a, float b, uint32_t& hi, uint32_t& lo) {
   typedef float f2 __attribute__((ext_vector_type(2)));
   typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
   const f2 v = {a, b};
-  hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
-  const f2 r = {a - __uint_as_float(hi << 16), b - __uint_as_float(hi & 0xffff0000u)};
+  const bf2 h = __builtin_convertvector(v, bf2);
+  uint32_t c0 = 0x0000bf80u, c1 = 0xbf800000u;   // the bf16 pairs (-1, 0) and (0, -1)
+  asm("" : "+v"(c0), "+v"(c1));
+  const bf2 m0 = __builtin_bit_cast(bf2, c0), m1 = __builtin_bit_cast(bf2, c1);
+  const f2 r = {__builtin_amdgcn_fdot2_f32_bf16(h, m0, a, false), __builtin_amdgcn_fdot2_f32_bf16(h, m1, b, false)};
+  hi = __builtin_bit_cast(uint32_t, h);
   lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf2));
 }
 

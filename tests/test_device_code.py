@@ -9,6 +9,10 @@ kernels use (the compiler applies the same numbers to its own code):
     must not read an SGPR that a VALU instruction wrote fewer than 5 wait states earlier, nor M0
     fewer than 1 wait state after an SALU write to it.
 The sources are compiled to device assembly (hipcc -S) with the library's flags; CPU only.
+
+One more rule comes from the compiler itself: v_dot2c_f32_bf16 must take its constant bf16 pairs
+from registers. As an inline constant the compiler encodes the pair (-1, 0) as -1.0, which the
+instruction reads as the 32-bit pattern 0xbf800000, i.e. the pair (0, -1).
 """
 
 import os
@@ -23,13 +27,19 @@ from llmario_amd import build as B
 DEVICE_SOURCES = ["prefill.hip", "decode.hip", "kv_kernels.hip"]
 
 
+_ASM = {}   # source -> assembly lines (each source compiled once per session)
+
+
 def _asm(src, tmp_path):
+    if src in _ASM:
+        return _ASM[src]
     out = tmp_path / (src + ".s")
     cmd = [B.HIPCC, *B.FLAGS, *B.EXTRA.get(src, []), "-x", "hip", "--cuda-device-only", "-S",
            os.path.join(B.CSRC, src), "-o", str(out)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     assert r.returncode == 0, r.stderr[-2000:]
-    return out.read_text().splitlines()
+    _ASM[src] = out.read_text().splitlines()
+    return _ASM[src]
 
 
 def _vregs(op):
@@ -115,6 +125,22 @@ def _scan(lines):
 def test_inline_asm_wait_states(src, tmp_path):
     problems = _scan(_asm(src, tmp_path))
     assert not problems, "\n".join(problems[:20])
+
+
+@pytest.mark.skipif(not os.path.exists(B.HIPCC) and shutil.which("hipcc") is None, reason="hipcc not available")
+@pytest.mark.parametrize("src", DEVICE_SOURCES)
+def test_bf16_dot2_sources_are_registers(src, tmp_path):
+    bad = []
+    for fn, _, op, ops in _instructions(_asm(src, tmp_path)):
+        if op.startswith("v_dot2") and "bf16" in op and any(not _vregs(o) for o in ops[1:]):
+            bad.append(f"{fn}: {op} {', '.join(ops)}")
+    assert not bad, "\n".join(bad[:10])
+
+
+def test_dot2_check_flags_a_constant_pair():
+    lines = ["_Zk:", "\tv_dot2c_f32_bf16_e32 v0, -1.0, v2", "\tv_dot2c_f32_bf16_e32 v1, v7, v5"]
+    flagged = [op for _, _, op, ops in _instructions(lines) if op.startswith("v_dot2") and any(not _vregs(o) for o in ops[1:])]
+    assert flagged == ["v_dot2c_f32_bf16_e32"]
 
 
 def test_scanner_flags_a_short_wait():
