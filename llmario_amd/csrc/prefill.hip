@@ -560,7 +560,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
             const f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
             for (int r = 0; r < 4; r++)
-              S[kk][cb][r] = fmaf(t[r], dtile::scale_at<NC>(ko.s[kk], r, ch), ch == 0 ? nm[cb] : S[kk][cb][r]);
+              S[kk][cb][r] = fmaf(t[r], (float)dtile::scale_h<NC>(ko.s[kk], r, ch), ch == 0 ? nm[cb] : S[kk][cb][r]);
           }
         }
       }
@@ -576,7 +576,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
           t = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ch], t, 0, 0, 0);
 #pragma unroll
           for (int r = 0; r < 4; r++)
-            S[kk][0][r] = fmaf(t[r], dtile::scale_at<NC>(ko.s[kk], r, ch), ch == 0 ? nm[0] : S[kk][0][r]);
+            S[kk][0][r] = fmaf(t[r], (float)dtile::scale_h<NC>(ko.s[kk], r, ch), ch == 0 ? nm[0] : S[kk][0][r]);
         }
       }
       return;
@@ -718,8 +718,10 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
           for (int i = 0; i < 4; i++) {
             const int e0 = 2 * i, e1 = 2 * i + 1;   // weight e: key 4g + e%4 of page tile e/4
-            split_pair_bf16(pq[x][e0] * dtile::scale_at<NC>(vo.s[e0 / 4], e0 % 4, b),
-                            pq[x][e1] * dtile::scale_at<NC>(vo.s[e1 / 4], e1 % 4, b), hw[i], lw[i]);
+            // weight x scale as v_fma_mix_f32 on the f16 scale in place (weights and scales >= 0)
+            split_pair_bf16(__builtin_fmaf(pq[x][e0], (float)dtile::scale_h<NC>(vo.s[e0 / 4], e0 % 4, b), 0.0f),
+                            __builtin_fmaf(pq[x][e1], (float)dtile::scale_h<NC>(vo.s[e1 / 4], e1 % 4, b), 0.0f),
+                            hw[i], lw[i]);
           }
           const dtile::b8 ph = __builtin_bit_cast(dtile::b8, make_uint4(hw[0], hw[1], hw[2], hw[3]));
           const dtile::b8 pl = __builtin_bit_cast(dtile::b8, make_uint4(lw[0], lw[1], lw[2], lw[3]));
