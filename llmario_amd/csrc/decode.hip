@@ -71,8 +71,10 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, uint32_t hdv, con
   for (int i = 0; i < NP; i++) acc[i] = 0.f;
   float M = -INFINITY, L = 0.f;
   // Up to 64 splits per round: lane s holds split s's (m, l); every lane then folds all of the
-  // round's partial rows into its NP dims. The first 16 rows are loaded together with (m, l), so
-  // a merge of up to 16 splits costs one memory round trip; later rows follow in groups of 16.
+  // round's partial rows into its NP dims. The round's first 16 rows (only those that exist: the
+  // row count is wave-uniform, so a merge of 4 splits issues 4 loads per lane, not 16) are loaded
+  // together with (m, l), so a merge of up to 16 splits costs one memory round trip; later rows
+  // follow in groups of 16.
   for (uint32_t s0 = 0; s0 < mi.n_split; s0 += 64) {
     const uint32_t s = s0 + lane;
     const uint32_t n = (mi.n_split - s0) < 64u ? (mi.n_split - s0) : 64u;
@@ -84,9 +86,9 @@ __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, uint32_t hdv, con
     float pre[16][NP];
 #pragma unroll
     for (int k = 0; k < 16; k++) {
-      const float* pp = base + (s0 + ((uint32_t)k < n ? k : 0)) * stride + lane * NP;
+      const float* pp = base + (s0 + k) * stride + lane * NP;   // loaded only for live rows (k < n)
 #pragma unroll
-      for (int i = 0; i < NP; i++) pre[k][i] = lane_on && lane * NP + i < hdv ? pp[i] : 0.f;
+      for (int i = 0; i < NP; i++) pre[k][i] = (uint32_t)k < n && lane_on && lane * NP + i < hdv ? pp[i] : 0.f;
     }
     float Mr = ms;
     for (int x = 32; x >= 1; x >>= 1) Mr = fmaxf(Mr, __shfl_xor(Mr, x));
