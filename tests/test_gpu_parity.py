@@ -218,8 +218,8 @@ def test_attend_small(cuda, kv, layer, prior, new, window, bt, split):
 
 
 # Prompt units streamed through few workgroups: each workgroup runs many units (and two passes
-# per unit when Q has bits below the cache's 16-bit type) back to back, fetching the next one's
-# first tiles, Q and block ids during the current one. Segments of different lengths give units
+# per unit when Q has bits below the cache's 16-bit type) back to back, reusing its LDS stages,
+# block-id list and Q registers from one to the next. Segments of different lengths give units
 # of one tile and of many; a window and a prefix make ranges that start past page 0.
 STREAM = [
     ("bf16", Layer(32, 8, 128, 128), [0, 7, 300, 0], [300, 70, 16, 700], 0, 16),
