@@ -11,16 +11,19 @@
 // heads of the KV group share every K/V tile. One workgroup of 8 waves (two per SIMD, one
 // workgroup per CU) runs a list of units the host balanced across the workgroups; wave w owns
 // columns 32w .. 32w+31 as two 16-column MFMA blocks. Per 64-key tile, in two 32-key halves:
-//   S^T[32 keys x 32 cols] = K . Q^T     v_mfma_f32_16x16x32_f16, Q resident in VGPRs
+//   S^T[32 keys x 32 cols] = K . Q^T     v_mfma_f32_16x16x32_{f16,bf16}, Q resident in VGPRs
 //   online softmax per column in the S^T layout (keys along the 4 lane groups and 4 registers)
-//   O^T[hd x 32 cols]     += V^T . P^T  v_mfma_f32_16x16x32_f16, P rounded to f16
+//   O^T[hd x 32 cols]     += V^T . P^T  v_mfma_f32_16x16x32_f16, P as f16 hi + lo (two products
+//                                        on the same V operand; without PLO, P rounded to f16)
 // K/V tiles go from HBM straight into LDS (global_load_lds, four stages, two tiles in flight)
-// in the page layout, which already holds each 16-token tile in MFMA operand order; bf16 K and V
-// are widened to f16 in LDS once per tile by the thread that loaded them (exact for |x| in
-// [2^-14, 65504]), so Q keeps 11 bits. Q carries the softmax scale (log2 domain) and each
-// column's reference max enters as the initial accumulator of Q.K, so the products are the
-// exponent arguments directly. The reference max moves lazily (only when a score exceeds it by
-// more than 8 in the log2 domain), so the O accumulators are almost never rescaled.
+// in the page layout, which already holds each 16-token tile in MFMA operand order. bf16 V is
+// widened to f16 in LDS once per tile by the thread that loaded it (exact for |x| in
+// [2^-14, 65504]); bf16 K too when Q is not exact in bf16 (Q then runs as f16 hi + lo parts), while
+// a Q exact in bf16 multiplies bf16 K as it is. Q stays unscaled; each column's reference max
+// enters (negated) as the initial accumulator of Q.K, so a product is s - m and its weight one fma
+// and one exp2 away. The reference max moves lazily (a lane's weight sum past a bound sends the
+// wave to a rare path that reduces the column max), so the O accumulators are almost never
+// rescaled.
 //
 // q8_0 pages (the Metal sibling's attn_prefill_hd{64,128}_q8_0, attn_prefill.metal:200-203) keep
 // the decode kernel's exact scheme rather than dequantising to 16 bits (d*q rounded to f16 misses
