@@ -20,9 +20,10 @@
 // softmax needs no data movement besides two cross-lane max/sum steps. The page bytes are
 // stored in operand order, so each operand is one 16-byte load per lane (1 KiB per wave).
 // Q is split into hi + lo halves of the MFMA input type, so scores keep ~22 bits of Q precision
-// (f16) or ~16 bits (bf16) against exactly represented K. P is rounded to f16 for P.V; bf16 V is
-// widened to f16 (exact for |v| in [2^-14, 65504]). q8_0: each 32-dim chunk of Q.K is one MFMA
-// whose result is scaled by that chunk's per-key scale; V scales fold into P per 32-dim block.
+// (f16) or ~16 bits (bf16) against exactly represented K. P is carried past f16 as hi + lo halves
+// (two P.V products on the same V operand); bf16 V is widened to f16 (exact for |v| in
+// [2^-14, 65504]). q8_0: each 32-dim chunk of Q.K is one MFMA whose result is scaled by that
+// chunk's per-key scale; V scales fold into P (and its hi + lo split) per 32-dim block.
 //
 // f32 pages (VALU): lane per key for Q.K, lane per dim for P.V, fp32 throughout.
 #include "decode_tile.h"
