@@ -7,8 +7,15 @@
 // encoded: the same rows given in the reference's row encoding (f16/bf16 bits, f32, q8_0
 //          34-byte blocks), transcoded into the page layout; the inverse read gives the bytes back.
 // gather:  LayerReader::row + KvType::load (kv.rs:1166-1179, 131-151) decoded to f32.
+// producer: the per-row tail of attention_block (forward.rs:427-453): QK-norm and RoPE of Q and K
+//          in place, then K and V stored as above, in one launch (qk_rope_store_*: per row, or per
+//          aligned run of 4 tokens and share of the heads for 16-bit caches).
+// snapshot: KvCache::write_seq / read_seq (kv.rs:1030-1130), one sequence's pages to and from the
+//          reference's byte format.
+// Also: zeroing of newly backed blocks, and two benchmark / staging helpers (a plain streaming
+// read, and a word copy on the caller's stream).
 //
-// One workgroup per row; these kernels move ~n_kv*(hd+hdv) values per row and are HBM-bound.
+// store / gather: one workgroup per row; like the rest they move bytes and are HBM-bound.
 #include "device.h"
 
 #include <algorithm>
