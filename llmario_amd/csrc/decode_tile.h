@@ -165,7 +165,7 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
                                             const float* q, float* out, float* part) {
   constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
   constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
-  constexpr int PUP = KVT == KV_Q8 ? 0 : 7;  // weights scaled by 2^PUP (see the softmax step)
+  constexpr bool Q8 = KVT == KV_Q8;
   using MT = typename std::conditional<KVT == KV_BF16, b8, h8>::type;
   const uint32_t lane = threadIdx.x & 63u;
   // the item is the same for the whole wave: its fields in scalar registers keep the tile loop's
@@ -210,10 +210,19 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
     }
   }
 
-  float m = -INFINITY, lsum = 0.0f;
+  // Weights are p = 2^(s - m + pup): the reference max shifted by pup (the partial's m is written
+  // as m - pup). f16 / bf16 pages: pup = 7, so every weight is <= 2^(8 + pup) and the f16 lo
+  // parts below stay normal for all weights above 2^(-pup - 2) of the largest. q8_0 pages: the
+  // f16 operand is weight x V scale, whose range is the scales' (f16 scales span 2^-24 .. 2^16),
+  // so pup follows them: pup = 7 - e with 2^e above the largest V scale seen, which keeps every
+  // product <= 2^15 (finite) and the products of the heaviest weights near 2^7 (22 bits through
+  // hi + lo, whatever the scales' magnitude). The first tile of the item sets it; a later tile
+  // with scales more than twice as large can overflow a product, which leaves O non-finite: the
+  // item then runs again with every tile's scales checked, lowering pup (and rescaling O and lsum
+  // exactly, by a power of two) before a tile whose scales need it.
+  float m, lsum, pup;
   f4 O[NJ];
-#pragma unroll
-  for (int j = 0; j < NJ; j++) O[j] = f4{0.f, 0.f, 0.f, 0.f};
+  bool checked = false;   // q8_0: every tile's V scales checked (the pass after an overflow)
 
   // The item's tiles t0..t1 (at most 64, the host caps chunks): lane i holds the block id of
   // tile t0 + i, so the loop reads ids with readlane instead of a dependent memory load.
@@ -296,11 +305,28 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
       for (int j = 0; j < NJ; j++) O[j] *= alpha;
       m = mn;
     }
-    // Weights p = 2^(s - m + PUP): the reference max shifted by PUP (the partial's m is written
-    // as m - PUP), so every weight is <= 2^(8 + PUP) and the f16 lo parts below stay normal for
-    // all weights above 2^(-PUP - 2) of the largest. q8_0 weights are multiplied by V scales
-    // first and keep PUP = 0 (their range is the scales').
-    const float mref = (m == -INFINITY ? 0.f : m) - (float)PUP;  // every score is -inf while m is
+    if constexpr (Q8) {
+      if (checked || t == t0) {   // uniform: the item's first tile, or every tile after an overflow
+        // the tile's largest |V scale| (a lane group's lanes hold the same 4 keys' scales)
+        constexpr int NCH = HDV / 32;
+        uint32_t mx = 0;
+#pragma unroll
+        for (int i = 0; i < 4 * NCH; i++) {
+          const uint32_t w = ((const uint32_t*)cur.vs)[i >> 1];
+          mx = max(mx, ((i & 1) ? (w >> 16) : w) & 0x7fffu);
+        }
+        const float dm = xmax_groups(h_to_f((uint16_t)mx));
+        const float pc = (float)(7 - __builtin_amdgcn_readfirstlane(__builtin_amdgcn_frexp_expf(dm)));
+        if (pc < pup) {   // O and lsum are zero on the first tile; otherwise an exact rescale
+          const float alpha = exp2_fast(pc - pup);
+          lsum *= alpha;
+#pragma unroll
+          for (int j = 0; j < NJ; j++) O[j] *= alpha;
+          pup = pc;
+        }
+      }
+    }
+    const float mref = (m == -INFINITY ? 0.f : m) - pup;  // every score is -inf while m is
     float p[4];
 #pragma unroll
     for (int rr = 0; rr < 4; rr++) p[rr] = exp2_fast(sc[rr] - mref);
@@ -354,13 +380,29 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   // Two-deep ping-pong: tile t+1 is in flight while tile t is computed. The fetches past the last
   // tile re-read the last tile (in bounds, and unconditional, so the buffers need no copies).
   TileRegs<KVT, HD, HDV> b0, b1;
-  fetch(b0, t0, true);   // block id from the item: in flight beside the Q and block-table reads
-  for (uint32_t t = t0; t <= t1; t += 2) {
-    fetch(b1, min(t + 1, t1));
-    step(b0, t);
-    if (t + 1 > t1) break;
-    fetch(b0, min(t + 2, t1));
-    step(b1, t + 1);
+  for (;;) {
+    m = -INFINITY;
+    lsum = 0.0f;
+    pup = Q8 ? INFINITY : 7.0f;   // q8_0: set by the first tile's scales
+#pragma unroll
+    for (int j = 0; j < NJ; j++) O[j] = f4{0.f, 0.f, 0.f, 0.f};
+    fetch(b0, t0, true);   // block id from the item: in flight beside the Q and block-table reads
+    for (uint32_t t = t0; t <= t1; t += 2) {
+      fetch(b1, min(t + 1, t1));
+      step(b0, t);
+      if (t + 1 > t1) break;
+      fetch(b0, min(t + 2, t1));
+      step(b1, t + 1);
+    }
+    if constexpr (!Q8) break;
+    if (checked) break;
+    // a product of weight and V scale that overflowed f16 leaves O non-finite (any sum with an
+    // inf or NaN term is); the second pass checks every tile's scales
+    float z = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; j++) z += (O[j][0] + O[j][1]) + (O[j][2] + O[j][3]);
+    if (!__ballot(hv && !__builtin_isfinite(z))) break;
+    checked = true;
   }
   lsum = xsum_groups(lsum);
 
@@ -380,7 +422,7 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
 #pragma unroll
     for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][0], O[j][1], O[j][2], O[j][3]);
     if (grp == 0) {
-      pp[HDV] = m - (float)PUP;  // the reference the weights were taken against
+      pp[HDV] = m - pup;  // the reference the weights were taken against
       pp[HDV + 1] = lsum;
     }
   }

@@ -57,7 +57,9 @@ def to_type(x, kv):
     return x
 
 
-def build(kv, L, prior, new, seed):
+def build(kv, L, prior, new, seed, v_scale=None):
+    """HIP and oracle caches holding the same closed-form rows; v_scale(positions) multiplies each
+    row's V (a per-position factor)."""
     import torch
     rng = np.random.default_rng(seed)
     totals = [p + n for p, n in zip(prior, new)]
@@ -74,6 +76,8 @@ def build(kv, L, prior, new, seed):
         toks += list(rng.integers(0, 1000, size=cnt))
         poss += list(range(pos0, pos0 + cnt))
     k, v = closed_form_rows(toks, poss, L.n_kv, L.hd, L.hdv)
+    if v_scale is not None:
+        v = (v * v_scale(np.asarray(poss, np.float64))[:, None]).astype(np.float32)
     hc.store(0, segs_h, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
     for (s, start, cnt, pos0) in segs_o:
         oc.store_rows(s, 0, pos0, k[start:start + cnt], v[start:start + cnt])
