@@ -153,6 +153,11 @@ int32_t lmh_kv_adopt_blocks(lmh_kv* kv, uint64_t seq, const uint32_t* blocks, ui
  * byte-identical to the one the reference's CPU cache writes for the same contents (stale slots
  * past len included). Pair snapshots with lmh_kv_fingerprint, as the reference does. */
 int32_t lmh_kv_snapshot_bytes(const lmh_kv* kv, uint64_t len, uint64_t* bytes);
+/* ModelBackend::snapshot_trimmable (backend.rs:64; CPU kv.rs:1003-1007, Metal
+ * metal/src/backend.rs:2141-2143): whether a restored snapshot can be cut back to a shorter prefix
+ * (*trimmable = 1): true for a cache of plain paged layers, false when it has window layers (their
+ * blocks behind the window are released, so a shorter prefix may need rows that are gone). */
+int32_t lmh_kv_snapshot_trimmable(const lmh_kv* kv, int32_t* trimmable);
 /* Writes snapshot_bytes(len(seq)) bytes to `dst` (device memory, `cap` bytes); *written = size. */
 int32_t lmh_kv_write_seq(lmh_kv* kv, uint64_t seq, void* dst, uint64_t cap, uint64_t* written, void* stream);
 /* Replaces the sequence with `len` tokens of snapshot `src` (device memory, n_bytes ==
@@ -238,13 +243,17 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
  * Decode rows, split-K over pages and prefill tiles are packed into one work list: segments of at
  * least prefill_min_rows rows on f16, bf16 or q8_0 pages of head width 64 or 128 (hd = hdv) run on
  * the matrix-core prefill kernel (Metal's attn_prefill_hd{64,128}[_q8_0], backend.rs:563-569); the
- * other rows on the decode kernels. */
+ * other rows on the decode kernels. A stream under graph capture is refused with LMH_UNSUPPORTED
+ * before anything is enqueued: the call's work list sits in a staging slot that later calls reuse,
+ * which a replayed graph would read. */
 int32_t lmh_attend(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const float* q,
                    float* out, float scale, uint64_t window, void* stream);
 
-/* lmh_attend for callers that cannot allocate (code under HIP graph capture, tight serving loops,
- * harnesses that forbid allocation); no counterpart in the reference. Same arguments, results and
- * errors as lmh_attend, and it allocates nothing: no device, pinned or event allocation. Split-K
+/* lmh_attend for callers that cannot allocate (tight serving loops, harnesses that forbid
+ * allocation); no counterpart in the reference. Same arguments, results and errors as lmh_attend
+ * (graph capture refused likewise), and it allocates nothing: no device, pinned or event
+ * allocation (the staging slots and their events are made at lmh_kv_create). It may wait for an
+ * earlier call's kernels before reusing the staging slot they read. Split-K
  * partials and the merge list live in a file-scope device array of 32 MiB per GPU, held until the
  * process ends (its address is resolved once per device when a handle is created there): the
  * split count is capped to what it holds, and a call that still needs more split-K scratch, or
@@ -259,7 +268,8 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
 
 /* Handle options of lmh_attend's planning and precision (no counterpart in the reference, whose
  * CPU path has no such choices; its thread-count split rule is forward.rs:613-633). Set once or
- * between calls; a zero field selects the default.
+ * between calls; a zero field selects the default (lmh_kv_get_tuning returns the fields as set, so
+ * reading the options and writing them back changes nothing).
  *   prefill_p_f16: 1 = the prefill products take P rounded to f16, the precision of Metal's
  *     attn_prefill (attn_prefill.metal: half P); 0 (default) = P as f16 hi + lo parts (~22 bits,
  *     the CPU path's f32 weights to within the 2e-3 bound even on rows whose output cancels).
@@ -282,7 +292,7 @@ typedef struct lmh_attend_tuning {
                                    fewer workgroups run more units each */
 } lmh_attend_tuning;
 int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t);
-/* The options in force (defaults resolved; decode_target_items 0 = the occupancy default). */
+/* The options as set (0 = the default, which each call resolves). */
 int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t);
 
 /* Timing hook for benchmarks: when enabled, lmh_attend and lmh_qk_rope_store time each kernel

@@ -66,6 +66,9 @@ uint32_t tile_bytes(uint32_t t, uint32_t dim, uint32_t rows) {
 }
 uint32_t tile_scale_bytes(uint32_t t, uint32_t dim, uint32_t rows) { return t == LMH_KV_Q8_0 ? rows * (dim / 32) * 2 : 0; }
 constexpr uint32_t MAX_HEAD_DIM = 512;  // the widest head any kernel takes (Metal's ATTN_MAX_HD)
+// Segments of at least this many rows run on the matrix-core prefill kernel (lmh_attend_tuning's
+// prefill_min_rows = 0)
+constexpr uint64_t DEFAULT_PREFILL_MIN_ROWS = 16;
 
 struct DirtyRows {  // the rows [lo, hi) of a host-side table that differ from the device copy
   uint64_t lo = ~0ull, hi = 0;
@@ -115,13 +118,15 @@ struct Uploader {
     for (int i = 0; i < N; i++)
       if (host[i]) (void)hipHostFree(host[i]);
   }
-  // Every slot allocated up front with at least `bytes`, so calls on the hot path do not pay for a
-  // pinned allocation the first time a slot comes round.
+  // Every slot allocated up front with at least `bytes`, and every completion event created, so
+  // calls on the hot path do not pay for a pinned allocation or an event the first time a slot
+  // comes round (and calls that may not allocate never make one).
   hipError_t reserve(size_t bytes) {
     for (int i = 0; i < N; i++) {
       int idx;
       uint8_t* p;
       hipError_t e = acquire(bytes, idx, p);
+      if (e == hipSuccess && !ev[i]) e = hipEventCreateWithFlags(&ev[i], hipEventDisableTiming);
       if (e != hipSuccess) return e;
     }
     reserved = bytes;
@@ -278,7 +283,7 @@ struct lmh_kv {
   std::vector<lmh_sched*> scheds;           // schedulers bound to this handle
   // ---- lmh_attend planning / precision options (lmh_kv_set_tuning)
   bool prefill_p_f16 = false;
-  uint64_t prefill_min_rows = 16, decode_target_items = 0, decode_min_tiles = 0;  // 0: defaults
+  uint64_t prefill_min_rows = 0, decode_target_items = 0, decode_min_tiles = 0;  // 0: defaults
   uint64_t prefill_workgroups = 0;                                                  // 0: every slot
   std::string err;
 
@@ -1025,6 +1030,14 @@ static int32_t snapshot_layers(lmh_kv* kv, bool write, uint64_t seq, uint64_t n_
   return LMH_OK;
 }
 
+// backend.rs:64; Metal's rule (metal/src/backend.rs:2141-2143): no window layer (this cache holds
+// no recurrent state)
+int32_t lmh_kv_snapshot_trimmable(const lmh_kv* kv, int32_t* trimmable) {
+  if (!kv || !trimmable) return LMH_INVALID_ARGUMENT;
+  *trimmable = kv->window == 0 ? 1 : 0;
+  return LMH_OK;
+}
+
 int32_t lmh_kv_write_seq(lmh_kv* kv, uint64_t seq, void* dst, uint64_t cap, uint64_t* written, void* stream) {
   if (!kv || seq >= kv->n_seqs) return LMH_INVALID_ARGUMENT;
   const uint64_t len = kv->seqs[seq].len;
@@ -1400,6 +1413,15 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
                            float* out, float scale, uint64_t window, void* stream, bool noalloc) {
   if (!kv) return LMH_INVALID_ARGUMENT;
   if (noalloc && !kv->scratch) return kv->fail(LMH_DEVICE_ERROR, "no-allocation scratch not resolved");
+  // A captured graph would replay this call's kernels against a staging slot that later calls
+  // overwrite (the work list is read from it when the kernels run), so capture is refused before
+  // anything is enqueued.
+  {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing((hipStream_t)stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return kv->fail(LMH_UNSUPPORTED, "lmh_attend cannot be captured into a graph: its work list lives in a "
+                                       "staging slot that later calls reuse");
+  }
   if (layer >= kv->layers.size()) return kv->fail(LMH_INVALID_ARGUMENT, "layer out of range");
   if (!std::isfinite(scale)) return kv->fail(LMH_INVALID_ARGUMENT, "scale must be finite");
   uint64_t n_rows;
@@ -1421,7 +1443,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
   // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over
   // prefill_wg_per_cu() workgroups per CU.
-  const uint64_t pf_min = kv->prefill_min_rows;
+  const uint64_t pf_min = kv->prefill_min_rows ? kv->prefill_min_rows : DEFAULT_PREFILL_MIN_ROWS;
   const bool pf_ok = scale > 0.f && y.layout == LAYOUT_TILES && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
   std::vector<uint8_t> decode_row(n_rows, 1);
   kv->pitems.clear();
@@ -1691,7 +1713,7 @@ int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {
   if (t->prefill_workgroups > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_workgroups out of range");
   kv->prefill_p_f16 = t->prefill_p_f16 != 0;
   kv->prefill_workgroups = t->prefill_workgroups;
-  kv->prefill_min_rows = t->prefill_min_rows ? t->prefill_min_rows : 16;
+  kv->prefill_min_rows = t->prefill_min_rows;
   kv->decode_target_items = t->decode_target_items;
   kv->decode_min_tiles = t->decode_min_tiles;
   return LMH_OK;
@@ -1703,7 +1725,7 @@ int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t) {
   t->prefill_p_f16 = kv->prefill_p_f16 ? 1u : 0u;
   t->prefill_min_rows = kv->prefill_min_rows;
   t->decode_target_items = kv->decode_target_items;
-  t->decode_min_tiles = kv->decode_min_tiles ? kv->decode_min_tiles : (kv->kv_type == LMH_KV_F32 ? 2 : 8);
+  t->decode_min_tiles = kv->decode_min_tiles;
   t->prefill_workgroups = kv->prefill_workgroups;
   return LMH_OK;
 }

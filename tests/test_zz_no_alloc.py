@@ -78,3 +78,61 @@ def test_noalloc_refuses_a_call_beyond_its_scratch(cuda):
     hc.attend(0, segs, q, out, 0.1, 0)
     torch.cuda.synchronize()
     assert np.isfinite(out.cpu().numpy()).all()
+
+
+def test_noalloc_first_calls_on_a_fresh_handle(cuda):
+    """A handle whose first attention calls are lmh_attend_noalloc ones (more of them than the
+    staging ring has slots, so every slot and its completion event comes round): device memory
+    stays as it was, and the results equal lmh_attend's, made afterwards on the same handle."""
+    import torch
+    w = small("naf", "f16", Layer(32, 8, 128, 128), prior=[3000, 1700, 640, 4090], new=[1, 1, 1, 1], seed=5)
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    q = torch.from_numpy(gen.q()).cuda()
+    shape = (w.n_rows, w.layer.n_head, w.layer.hdv)
+    b = torch.full(shape, float("nan"), device="cuda")
+    a = torch.full(shape, float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(40):
+        hc.attend_noalloc(0, w.segments(), q, b, w.scale)
+    torch.cuda.synchronize()
+    free1 = torch.cuda.mem_get_info()[0]
+    hc.attend(0, w.segments(), q, a, w.scale)
+    torch.cuda.synchronize()
+    print(f"device memory free before / after 40 noalloc calls: {free0} / {free1}")
+    assert free1 == free0
+    assert np.array_equal(a.cpu().numpy(), b.cpu().numpy())
+
+
+def test_attend_refuses_graph_capture(cuda):
+    """lmh_attend and lmh_attend_noalloc on a stream under graph capture fail with UNSUPPORTED
+    before enqueuing anything (their work list sits in a staging slot later calls reuse); the
+    captured graph then holds only the caller's own work."""
+    import torch
+    w = small("nag", "f16", Layer(32, 8, 128, 128), prior=[700, 90], new=[1, 1], seed=6)
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    q = torch.from_numpy(gen.q()).cuda()
+    out = torch.full((w.n_rows, w.layer.n_head, w.layer.hdv), 3.0, device="cuda")
+    x = torch.ones(16, device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    errs = []
+    with torch.cuda.graph(g):
+        y = x * 2.0
+        for fn in (hc.attend, hc.attend_noalloc):
+            try:
+                fn(0, w.segments(), q, out, w.scale)
+            except LmhError as e:
+                errs.append(str(e))
+    for _ in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert bool((y == 2.0).all())
+    assert len(errs) == 2 and all("UNSUPPORTED" in e for e in errs), errs
+    assert bool((out == 3.0).all())
+    # outside capture the same handle works
+    hc.attend(0, w.segments(), q, out, w.scale)
+    torch.cuda.synchronize()
+    assert np.isfinite(out.cpu().numpy()).all()
