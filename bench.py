@@ -642,6 +642,10 @@ def main():
             "kernel": "decode_mfma_kernel<f16,128,128>", "kernel_us": round(head["kernel_ms"] * 1e3, 2),
             "algorithmic_bytes": head["bytes"],
             "workload": f"c2, {COLD_LAYERS} layers in rotation (cold: K/V from HBM each step)"}
+    if traffic is not None:
+        # counters cannot be read in a timed run: the figure is carried from the committed profile
+        roof["traffic_source"] = ("carried from " + os.path.relpath(TRAFFIC_FILE, ROOT) + " (rocprofv3 --pmc "
+                                  "FETCH_SIZE / WRITE_SIZE of this kernel on this workload), not measured in this run")
     # the device's practical streaming-read rate over the same number of bytes (a plain read
     # kernel, lmh_bench_read_ceiling), beside the published peak the roofline uses
     ceil_gbs = run_leg("read_ceiling", lambda: read_ceiling(int(head["bytes"])), errors)

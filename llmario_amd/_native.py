@@ -128,6 +128,7 @@ SIGNATURES = {
     "lmh_kv_window_table": (i32, [P, u64, P, u64, C.POINTER(u64)]),
     "lmh_kv_adopt_blocks": (i32, [P, u64, P, u64]),
     "lmh_kv_snapshot_bytes": (i32, [P, u64, C.POINTER(u64)]),
+    "lmh_kv_snapshot_trimmable": (i32, [P, C.POINTER(i32)]),
     "lmh_kv_write_seq": (i32, [P, u64, P, u64, C.POINTER(u64), P]),
     "lmh_kv_read_seq": (i32, [P, u64, u64, P, u64, C.POINTER(u64), C.POINTER(u64), P]),
     "lmh_pool_refs": (i32, [P, u32, C.POINTER(u32)]),

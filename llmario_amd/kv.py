@@ -161,6 +161,13 @@ class HipKvCache:
         self._check(N.lib().lmh_kv_snapshot_bytes(self.h, length, C.byref(v)))
         return v.value
 
+    def snapshot_trimmable(self) -> bool:
+        """ModelBackend::snapshot_trimmable (backend.rs:64): a restored snapshot may be cut back to a
+        shorter prefix (no window layers)."""
+        v = N.i32()
+        self._check(N.lib().lmh_kv_snapshot_trimmable(self.h, C.byref(v)))
+        return bool(v.value)
+
     def write_seq(self, s: int, dst=None, stream=None):
         """The sequence's snapshot into `dst` (a uint8 cuda tensor of at least snapshot_bytes
         bytes; allocated when None). Returns the tensor trimmed to the snapshot's size."""

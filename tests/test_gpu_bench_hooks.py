@@ -40,3 +40,38 @@ def test_kernel_time_counts_each_launch(cuda):
     assert kt["decode"][1] == 3 and kt["decode"][0] > 0
     assert kt["mixed"][1] == 0 and kt["prefill"][1] == 0
     assert np.isfinite(out.cpu().numpy()).all()
+
+
+def test_tuning_read_back_changes_nothing(cuda):
+    """lmh_kv_get_tuning returns the options as set (0 = default), so changing one option through
+    HipKvCache.set_tuning (which reads all of them and writes them back) leaves the others at
+    their defaults: an f32 layer of short rows still merges its split items inside the workgroup
+    (no merge launch) after prefill_workgroups is set."""
+    import torch
+
+    import oracle as O
+    from conftest import TOL, row_rel_err
+    from llmario_amd import harness
+    from llmario_amd.workloads import Generator, config
+
+    w = config("c1")
+    gen = Generator(w)
+    oc = O.empty_cache_for(w)
+    hc = harness.load(w, gen, on_rows=lambda s, t, k, v: O.fill(oc, t, s, k, v, w.prior[s]))
+    assert hc.tuning() == {"prefill_p_f16": 0, "prefill_min_rows": 0, "decode_target_items": 0,
+                           "decode_min_tiles": 0, "prefill_workgroups": 0}
+    hc.set_tuning(prefill_workgroups=3)
+    assert hc.tuning() == {"prefill_p_f16": 0, "prefill_min_rows": 0, "decode_target_items": 0,
+                           "decode_min_tiles": 0, "prefill_workgroups": 3}
+    q = gen.q()
+    qd = torch.from_numpy(q).cuda()
+    out = torch.empty((w.n_rows, w.layer.n_head, w.layer.hdv), device="cuda")
+    hc.kernel_times()
+    hc.set_timing(True)
+    hc.attend(0, w.segments(), qd, out, w.scale)
+    torch.cuda.synchronize()
+    kt = hc.kernel_times()
+    hc.set_timing(False)
+    assert kt["decode"][1] == 1 and kt["merge"][1] == 0, kt
+    ref = oc.attend(0, w.segments(), q, w.scale, 0, 4)
+    assert row_rel_err(out.cpu().numpy(), ref) <= TOL["f32"]

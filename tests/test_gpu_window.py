@@ -184,3 +184,13 @@ def test_window_snapshot_is_metal_format_and_restores(cuda, kv_type):
         hc.attend(l, segs, q, out, L.hd ** -0.5, L.window)
         torch.cuda.synchronize()
         assert torch.equal(out[0], out[1]), f"layer {l}"
+
+
+def test_snapshot_trimmable_only_without_window_layers(cuda):
+    """ModelBackend::snapshot_trimmable (backend.rs:64), Metal's rule (metal/src/backend.rs:2141-2143):
+    a cache of plain paged layers can cut a restored snapshot back to a shorter prefix; one with a
+    window layer cannot (its blocks behind the window are released)."""
+    plain = HipKvCache([Layer(8, 2, 64, 64)], max_ctx=256, n_seqs=2, kv_type="f16", block_tokens=16)
+    assert plain.snapshot_trimmable()
+    windowed = HipKvCache(LAYERS, max_ctx=MAX_CTX, n_seqs=N_SEQS, kv_type="f16", block_tokens=BT, n_batch=N_BATCH)
+    assert not windowed.snapshot_trimmable()
