@@ -11,10 +11,14 @@
 
 #include <algorithm>
 #include <array>
+#include <atomic>
+#include <condition_variable>
 #include <cmath>
 #include <cstring>
 #include <deque>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -563,26 +567,127 @@ void rope(float* x, size_t n_heads, size_t hd, uint32_t pos, const orc_rope_para
   }
 }
 
-// ThreadPool::parallel_for (cpu/src/pool.rs:115-180): `n_chunks = threads` contiguous chunks of
-// ceil(n / n_chunks); the caller runs chunks too. Workers are spawned per call here (the
-// reference parks a persistent pool); the work split is the same.
+// ThreadPool (cpu/src/pool.rs:53-180): a persistent pool per thread count, its workers spinning
+// for a bounded time on a new region, then parked on a condition variable; the caller is worker
+// 0. parallel_for (pool.rs:115-180): `n_chunks = threads` contiguous chunks of ceil(n / n_chunks),
+// claimed from a per-region counter (so a late worker only touches its own region's counters),
+// and the caller waits until every chunk is done (spinning briefly, then sleeping).
+class Pool {
+ public:
+  explicit Pool(size_t n) : n_threads_(n) {
+    for (size_t i = 1; i < n; i++) workers_.emplace_back([this] { worker(); });
+  }
+  ~Pool() {
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      stop_ = true;
+    }
+    cv_.notify_all();
+    for (auto& t : workers_) t.join();
+  }
+  template <typename F>
+  void run(size_t n, F& f) {
+    auto job = std::make_shared<Job>();
+    job->n_chunks = std::min(n_threads_, n);
+    job->chunk = (n + job->n_chunks - 1) / job->n_chunks;
+    job->n = n;
+    job->ctx = &f;
+    job->fn = [](void* c, size_t s, size_t e) { (*(F*)c)(s, e); };
+    bool wake;
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      job_ = job;
+      gen_.store(gen_.load(std::memory_order_relaxed) + 1, std::memory_order_release);
+      wake = parked_ > 0;
+    }
+    if (wake) cv_.notify_all();
+    run_chunks(*job);
+    for (int i = 0; i < DONE_SPIN && job->done.load(std::memory_order_acquire) < job->n_chunks; i++) spin_pause();
+    if (job->done.load(std::memory_order_acquire) < job->n_chunks) {
+      std::unique_lock<std::mutex> g(done_mu_);
+      done_cv_.wait(g, [&] { return job->done.load(std::memory_order_acquire) >= job->n_chunks; });
+    }
+    std::lock_guard<std::mutex> g(mu_);
+    if (job_ == job) job_.reset();
+  }
+
+ private:
+  struct Job {
+    size_t n_chunks = 0, chunk = 0, n = 0;
+    void* ctx = nullptr;
+    void (*fn)(void*, size_t, size_t) = nullptr;
+    std::atomic<size_t> next{0}, done{0};
+  };
+  static constexpr int SPIN = 40000, DONE_SPIN = 20000;   // pool.rs:60-62
+  static void spin_pause() { __builtin_ia32_pause(); }
+  void run_chunks(Job& j) {
+    for (;;) {
+      const size_t c = j.next.fetch_add(1, std::memory_order_acq_rel);
+      if (c >= j.n_chunks) return;
+      const size_t s = c * j.chunk, e = std::min(j.n, s + j.chunk);
+      if (s < e) j.fn(j.ctx, s, e);
+      if (j.done.fetch_add(1, std::memory_order_acq_rel) + 1 == j.n_chunks) {
+        std::lock_guard<std::mutex> g(done_mu_);   // the caller may be about to sleep
+        done_cv_.notify_all();
+      }
+    }
+  }
+  void worker() {
+    uint64_t seen = 0;
+    for (;;) {
+      std::shared_ptr<Job> job;
+      for (int i = 0; i < SPIN && !job; i++) {
+        if (gen_.load(std::memory_order_acquire) != seen) {
+          std::lock_guard<std::mutex> g(mu_);
+          if (stop_) return;
+          seen = gen_.load(std::memory_order_relaxed);
+          job = job_;
+        } else {
+          spin_pause();
+        }
+      }
+      if (!job) {
+        std::unique_lock<std::mutex> g(mu_);
+        parked_++;
+        cv_.wait(g, [&] { return stop_ || gen_.load(std::memory_order_relaxed) != seen; });
+        parked_--;
+        if (stop_) return;
+        seen = gen_.load(std::memory_order_relaxed);
+        job = job_;
+      }
+      if (job) run_chunks(*job);
+    }
+  }
+  size_t n_threads_;
+  std::vector<std::thread> workers_;
+  std::mutex mu_, done_mu_;
+  std::condition_variable cv_, done_cv_;
+  std::shared_ptr<Job> job_;
+  std::atomic<uint64_t> gen_{0};
+  size_t parked_ = 0;
+  bool stop_ = false;
+};
+
+// One pool per thread count, created on first use and kept (the reference's engine holds one
+// pool for its lifetime).
+Pool& pool_for(size_t threads) {
+  static std::mutex mu;
+  static std::map<size_t, std::unique_ptr<Pool>> pools;
+  std::lock_guard<std::mutex> g(mu);
+  auto& p = pools[threads];
+  if (!p) p = std::make_unique<Pool>(threads);
+  return *p;
+}
+
 template <typename F>
 void parallel_for(size_t n, size_t threads, F f) {
   if (n == 0) return;
-  size_t n_chunks = std::min(std::max<size_t>(threads, 1), n);
+  const size_t n_chunks = std::min(std::max<size_t>(threads, 1), n);
   if (threads <= 1 || n_chunks == 1) {
     f(0, n);
     return;
   }
-  size_t chunk = (n + n_chunks - 1) / n_chunks;
-  std::vector<std::thread> ws;
-  for (size_t c = 1; c < n_chunks; c++) {
-    size_t s = c * chunk, e = std::min(n, s + chunk);
-    if (s >= e) continue;
-    ws.emplace_back([&f, s, e] { f(s, e); });
-  }
-  f(0, std::min(n, chunk));
-  for (auto& t : ws) t.join();
+  pool_for(threads).run(n, f);
 }
 
 constexpr size_t SPLIT_MIN_KEYS = 128;  // forward.rs:681
