@@ -316,6 +316,39 @@ int32_t lmh_kv_kernel_time(lmh_kv* kv, uint32_t kernel, double* ms, uint64_t* la
  * lmh_attend's kernels are timed). Synchronous; frees what it allocated. */
 int32_t lmh_bench_read_ceiling(int32_t device, uint64_t bytes, uint32_t iters, double* gbps);
 
+/* Test hook (no counterpart in the reference; for CPU tests of the planner, which run under the
+ * sanitizers): lmh_attend's work-list planner on host data alone, no device touched. `d` gives a
+ * layer geometry as lmh_kv_create takes it, the device facts the planner uses (n_cu; the decode
+ * items the device holds at once, 0 = 8 per CU) and a block table [n_seqs][bps] (-1: no block);
+ * the segments are validated as lmh_attend validates them (every block a row's key range
+ * starts or ends in must be in the table). The plan lmh_attend would run is copied out as its
+ * internal records: decode items, split-K merges and prefill units (pf_wg lists of pf_per_wg
+ * units, an empty unit ending a list), `counts` giving the number of records and the uint32
+ * words per record. Lists too small for the plan: LMH_INVALID_ARGUMENT with `counts` filled. */
+typedef struct lmh_plan_desc {
+  uint32_t abi_version;   /* LMH_ABI_VERSION */
+  uint32_t kv_type;
+  uint32_t n_head, n_kv, hd, hdv;
+  uint32_t block_tokens;
+  uint32_t n_cu;
+  uint64_t decode_capacity;
+  uint64_t n_seqs, bps;
+  const int32_t* table;
+  uint64_t window;
+  float scale;
+  uint32_t noalloc;       /* 1: plan as lmh_attend_noalloc does */
+  lmh_attend_tuning tuning;
+} lmh_plan_desc;
+typedef struct lmh_plan_counts {
+  uint64_t n_items, n_merges, n_units;
+  uint32_t item_words, merge_words, unit_words;
+  uint32_t ng, slots, pf_wg, pf_per_wg, max_pages, local, layout;
+  uint32_t chunk;   /* decode split chunk in 16-key tiles */
+} lmh_plan_counts;
+int32_t lmh_plan_attend(const lmh_plan_desc* d, const lmh_seg* segs, uint64_t n_segs, uint32_t* items,
+                        uint64_t items_cap, uint32_t* merges, uint64_t merges_cap, uint32_t* units,
+                        uint64_t units_cap, lmh_plan_counts* counts);
+
 /* ---- request scheduler: the host side of the batch hand-off ----
  * Scheduler (crates/engine/sched/src/lib.rs:75-282) over the block pool, with Sequence
  * (kv/src/lib.rs:262-335) for admission. Each step takes every decoding slot's next token, then

@@ -64,6 +64,18 @@ class AttendTuning(C.Structure):
                 ("decode_target_items", u64), ("decode_min_tiles", u64), ("prefill_workgroups", u64)]
 
 
+class PlanDesc(C.Structure):
+    _fields_ = [("abi_version", u32), ("kv_type", u32), ("n_head", u32), ("n_kv", u32), ("hd", u32), ("hdv", u32),
+                ("block_tokens", u32), ("n_cu", u32), ("decode_capacity", u64), ("n_seqs", u64), ("bps", u64),
+                ("table", P), ("window", u64), ("scale", C.c_float), ("noalloc", u32), ("tuning", AttendTuning)]
+
+
+class PlanCounts(C.Structure):
+    _fields_ = [("n_items", u64), ("n_merges", u64), ("n_units", u64), ("item_words", u32), ("merge_words", u32),
+                ("unit_words", u32), ("ng", u32), ("slots", u32), ("pf_wg", u32), ("pf_per_wg", u32),
+                ("max_pages", u32), ("local", u32), ("layout", u32), ("chunk", u32)]
+
+
 PRIORITY_BATCH, PRIORITY_API, PRIORITY_INTERACTIVE = 0, 1, 2
 
 
@@ -146,6 +158,7 @@ SIGNATURES = {
     "lmh_attend_noalloc": (i32, [P, u32, P, u64, P, P, C.c_float, u64, P]),
     "lmh_kv_set_tuning": (i32, [P, C.POINTER(AttendTuning)]),
     "lmh_kv_get_tuning": (i32, [P, C.POINTER(AttendTuning)]),
+    "lmh_plan_attend": (i32, [C.POINTER(PlanDesc), P, u64, P, u64, P, u64, P, u64, C.POINTER(PlanCounts)]),
     "lmh_kv_set_timing": (i32, [P, i32]),
     "lmh_kv_kernel_time": (i32, [P, u32, C.POINTER(C.c_double), C.POINTER(u64)]),
     "lmh_bench_read_ceiling": (i32, [i32, u64, u32, C.POINTER(C.c_double)]),

@@ -16,9 +16,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libllmario_hip.so")
-SOURCES = ["host.cpp", "sched.cpp", "sha256.cpp", "kv_kernels.hip", "decode.hip", "prefill.hip"]
+SOURCES = ["host.cpp", "plan.cpp", "sched.cpp", "sha256.cpp", "kv_kernels.hip", "decode.hip", "prefill.hip"]
 # host-only sources (no device code): compiled as plain C++ by the same compiler
-HOST_ONLY = {"sched.cpp", "sha256.cpp"}
+HOST_ONLY = {"plan.cpp", "sched.cpp", "sha256.cpp"}
 ARCH = os.environ.get("LMH_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -60,7 +60,7 @@ def _compile(src: str, verify: bool = False) -> str:
 
 def build(verbose: bool = False, verify: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), 7)) as ex:
         objs = list(ex.map(lambda src: _compile(src, verify), SOURCES))
     tmp = LIB + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]

@@ -33,9 +33,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-namespace lmh {
+#include "work.h"
 
-enum : uint32_t { KV_F16 = 0, KV_Q8 = 1, KV_F32 = 2, KV_BF16 = 3 };
+namespace lmh {
 
 // Where one layer's pages live. Tile t (16 positions) of KV head h in block b:
 //   K values at pool + b*block_bytes + k_off + h*k_head + t*k_tile
@@ -54,7 +54,6 @@ struct PageGeom {
   uint32_t kv_type, n_kv, hd, hdv;
   uint32_t layout;  // 0: tiles in matrix-core operand order; 1: row-major rows (see above)
 };
-constexpr uint32_t LAYOUT_TILES = 0, LAYOUT_ROWS = 1;
 
 __host__ __device__ inline uint32_t k16_off(uint32_t m, uint32_t d) {
   return (d >> 5) * 1024u + ((((d >> 3) & 3u) << 4) + m) * 16u + (d & 7u) * 2u;
@@ -69,36 +68,6 @@ __host__ __device__ inline uint32_t vq8_off(uint32_t k, uint32_t d) {
   return (d >> 6) * 1024u + (((k >> 2) << 4) + (d & 15u)) * 16u + ((d >> 4) & 3u) * 4u + (k & 3u);
 }
 
-// One decode work item: row `row` (its sequence and position come from the row arrays), KV head
-// `kvh`, query heads kvh*group + h0 .. + n_heads, keys [p0, p1). `slot` is the partial-result slot
-// (split-K) or NO_SLOT when the item covers the row's whole key range and writes the output.
-struct DecodeItem {
-  uint32_t row;
-  uint32_t kvh;
-  uint32_t h0;
-  uint32_t p0, p1;
-  uint32_t slot;
-  uint32_t seq;   // the row's sequence (saves a dependent read of the row arrays)
-  uint32_t blk0;  // block id of the first tile p0 >> 4 (the first fetch skips the block-table read)
-};
-constexpr uint32_t NO_SLOT = 0xffffffffu;
-// A split item merged inside its workgroup (f32 decode of short rows): LOCAL_SLOT | (its index in
-// the row's group << 8) | the group's size; the group's items are consecutive waves of one
-// workgroup, and the first merges their partials from LDS, so the call needs no merge launch.
-constexpr uint32_t LOCAL_SLOT = 0x80000000u;
-constexpr uint32_t LOCAL_MERGE_MAX = 1024;   // heads x hdv of an item whose partials a wave keeps in LDS
-constexpr int LOCAL_WAVES = 8;               // waves per workgroup of a local-merge call (its largest group)
-
-// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..).
-struct MergeItem {
-  uint32_t row;
-  uint32_t kvh;
-  uint32_t h0;
-  uint32_t slot0;
-  uint32_t n_split;
-  uint32_t pad;
-};
-
 struct RowGeom {
   const int32_t* row_seq;  // [n_rows]
   const int32_t* row_pos;  // [n_rows]
@@ -107,20 +76,6 @@ struct RowGeom {
   float scale_log2;        // scale * log2(e): scores kept in the log2 domain
   uint32_t window;         // 0 = none
   uint32_t local_merge;    // f32 decode: split rows merge inside their workgroup (slots LOCAL_SLOT | ...)
-};
-
-// One prefill work unit: KV head `kvh` of sequence `seq`, tokens at positions pos0 .. pos0+n_tok-1
-// which are stacked rows row0 .. row0+n_tok-1 (n_tok * group <= prefill_cols_per_unit()).
-// blk: the block ids of the unit's first 8 key pages (page i of its key range, clamped to the last
-// page), so the first K/V tiles are fetched without waiting for the block table.
-struct PrefillItem {
-  uint32_t seq;
-  uint32_t kvh;
-  uint32_t row0;
-  uint32_t pos0;
-  uint32_t n_tok;
-  uint32_t pad0, pad1, pad2;
-  uint32_t blk[8];
 };
 
 struct PrefillGeom {

@@ -28,6 +28,7 @@
 #include "../../include/llmario_hip.h"
 #include "device.h"
 #include "kv_hooks.h"
+#include "plan.h"
 #include "pool.h"
 
 using namespace lmh;
@@ -66,9 +67,6 @@ uint32_t tile_bytes(uint32_t t, uint32_t dim, uint32_t rows) {
 }
 uint32_t tile_scale_bytes(uint32_t t, uint32_t dim, uint32_t rows) { return t == LMH_KV_Q8_0 ? rows * (dim / 32) * 2 : 0; }
 constexpr uint32_t MAX_HEAD_DIM = 512;  // the widest head any kernel takes (Metal's ATTN_MAX_HD)
-// Segments of at least this many rows run on the matrix-core prefill kernel (lmh_attend_tuning's
-// prefill_min_rows = 0)
-constexpr uint64_t DEFAULT_PREFILL_MIN_ROWS = 16;
 
 struct DirtyRows {  // the rows [lo, hi) of a host-side table that differ from the device copy
   uint64_t lo = ~0ull, hi = 0;
@@ -269,8 +267,7 @@ struct lmh_kv {
   uint8_t* scratch = nullptr;               // this device's copy of the no-allocation scratch
   // ---- per-call host scratch
   std::vector<int32_t> row_seq, row_pos;
-  std::vector<DecodeItem> items;
-  std::vector<MergeItem> merges;
+  PlanOut plan;   // the latest lmh_attend call's work lists
   // ---- timing
   bool timing = false;
   std::vector<std::pair<hipEvent_t, hipEvent_t>> evs;
@@ -278,7 +275,6 @@ struct lmh_kv {
   size_t ev_used = 0;
   double acc_ms[6] = {0, 0, 0, 0, 0, 0};
   uint64_t launches[6] = {0, 0, 0, 0, 0, 0};
-  std::vector<PrefillItem> pitems;
   std::vector<uint8_t> payload;
   std::vector<lmh_sched*> scheds;           // schedulers bound to this handle
   // ---- lmh_attend planning / precision options (lmh_kv_set_tuning)
@@ -1247,39 +1243,6 @@ int32_t lmh_batch_commit(lmh_kv* kv, const lmh_seg* segs, uint64_t n_segs) {
   return LMH_OK;
 }
 
-// Prefill units grouped per workgroup: prefill_wg_per_cu() workgroups per CU, each running a
-// list of units. Longest-processing-time-first: units by decreasing key pages (plus a
-// fixed cost for the unit's Q load and output), each to the currently least loaded workgroup.
-// Lists are padded to the longest with empty units (n_tok = 0) at a fixed stride.
-static void assign_prefill_units(std::vector<PrefillItem>& items, uint64_t window, uint32_t slots, uint32_t& n_wg,
-                                 uint32_t& per_wg) {
-  n_wg = (uint32_t)std::min<uint64_t>(items.size(), std::max<uint32_t>(slots, 1));
-  per_wg = 0;
-  if (n_wg == 0) return;
-  auto work = [&](const PrefillItem& it) -> uint64_t {
-    const uint64_t last = (uint64_t)it.pos0 + it.n_tok - 1;
-    const uint64_t lo = (window > 0 && it.pos0 + 1 > window) ? it.pos0 + 1 - window : 0;
-    return last / 16 - lo / 16 + 1 + 8;
-  };
-  std::stable_sort(items.begin(), items.end(),
-                   [&](const PrefillItem& a, const PrefillItem& b) { return work(a) > work(b); });
-  std::vector<std::vector<uint32_t>> lists(n_wg);
-  std::priority_queue<std::pair<uint64_t, uint32_t>, std::vector<std::pair<uint64_t, uint32_t>>,
-                      std::greater<std::pair<uint64_t, uint32_t>>> load;
-  for (uint32_t b = 0; b < n_wg; b++) load.push({0, b});
-  for (uint32_t i = 0; i < items.size(); i++) {
-    auto [l, b] = load.top();
-    load.pop();
-    lists[b].push_back(i);
-    load.push({l + work(items[i]), b});
-  }
-  for (const auto& li : lists) per_wg = std::max<uint32_t>(per_wg, (uint32_t)li.size());
-  std::vector<PrefillItem> out((size_t)n_wg * per_wg, PrefillItem{});
-  for (uint32_t b = 0; b < n_wg; b++)
-    for (size_t j = 0; j < lists[b].size(); j++) out[(size_t)b * per_wg + j] = items[lists[b][j]];
-  items.swap(out);
-}
-
 static int32_t kv_io(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint64_t n_segs, const void* a, const void* b,
                      void* stream, int mode) {
   if (!kv) return LMH_INVALID_ARGUMENT;
@@ -1405,6 +1368,17 @@ int32_t lmh_qk_rope_store(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint6
   return kv->release_rows(slot, st);
 }
 
+// What the planner needs to know of the kernel modules for a layer's geometry.
+static void fill_kernel_facts(PlanIn& in, uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group) {
+  in.prefill_supported = prefill_supported(kv_type, hd, hdv, group);
+  in.unit_cols = prefill_cols_per_unit();
+  in.prefill_wg_per_cu = prefill_wg_per_cu();
+  in.prefill_lds_fixed = in.prefill_supported ? prefill_lds_bytes(kv_type, hd, 0, 0) + prefill_static_lds_bytes() : 0;
+  in.lds_limit = 160 * 1024;
+  in.rows_max_heads = decode_rows_max_heads();
+  in.local_merge_ok = decode_local_merge_ok(hd, hdv, group);
+}
+
 // lmh_attend and lmh_attend_noalloc. noalloc: split-K partials and the merge list go to the
 // device's no-allocation scratch (the split target capped to what it holds, a call that still
 // needs more is refused), the staged work list must fit the staging capacity reserved at
@@ -1435,180 +1409,51 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
     return kv->fail(LMH_INVALID_ARGUMENT, "a window layer's attention window must be 1..its width");
   if ((rc = kv->check_window_rows(layer, segs, n_segs, window)) != LMH_OK) return rc;
   const uint32_t group = y.n_head / y.n_kv;
-  // heads per decode item: up to 16 (the matrix-core tile's columns), 4 on the row-layout kernel
-  const uint32_t ng = std::min<uint32_t>(group, y.layout == LAYOUT_ROWS ? decode_rows_max_heads() : 16);
-  const uint32_t head_blocks = (group + ng - 1) / ng;
   hipStream_t st = (hipStream_t)stream;
-
-  // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
-  // in units of up to prefill_cols_per_unit()/group tokens per KV head, balanced over
-  // prefill_wg_per_cu() workgroups per CU.
-  const uint64_t pf_min = kv->prefill_min_rows ? kv->prefill_min_rows : DEFAULT_PREFILL_MIN_ROWS;
-  const bool pf_ok = scale > 0.f && y.layout == LAYOUT_TILES && prefill_supported(kv->kv_type, y.hd, y.hdv, group);
-  std::vector<uint8_t> decode_row(n_rows, 1);
-  kv->pitems.clear();
-  uint32_t max_pages = 0, pf_wg = 0, pf_per_wg = 0;
-  if (pf_ok) {
-    const uint32_t unit_tok = prefill_cols_per_unit() / group;
-    for (uint64_t i = 0; i < n_segs; i++) {
-      const lmh_seg& sg = segs[i];
-      if (sg.n < pf_min) continue;
-      for (uint64_t u = 0; u < sg.n; u += unit_tok) {
-        const uint32_t n_tok = (uint32_t)std::min<uint64_t>(unit_tok, sg.n - u);
-        const uint64_t pos0 = sg.pos0 + u, last = pos0 + n_tok - 1;
-        const uint64_t lo = (window > 0 && pos0 + 1 > window) ? pos0 + 1 - window : 0;
-        max_pages = std::max<uint32_t>(max_pages, (uint32_t)(last / 16 - lo / 16 + 1));
-        PrefillItem it{(uint32_t)sg.seq, 0, (uint32_t)(sg.start + u), (uint32_t)pos0, n_tok, 0, 0, 0, {}};
-        const uint64_t page0 = lo / 16, n_pages = last / 16 - lo / 16 + 1;
-        const int32_t* row = (y.win ? kv->h_wtable.data() : kv->h_table.data()) + sg.seq * kv->bps;
-        for (uint64_t b = 0; b < 8; b++)
-          it.blk[b] = (uint32_t)row[((page0 + std::min<uint64_t>(b, n_pages - 1)) << 4) >> kv->bt_shift];
-        for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
-          it.kvh = kvh;
-          kv->pitems.push_back(it);
-        }
-      }
-      for (uint64_t j = 0; j < sg.n; j++) decode_row[sg.start + j] = 0;
-    }
-    const uint32_t slots = kv->n_cu * prefill_wg_per_cu();
-    assign_prefill_units(kv->pitems, window,
-                         kv->prefill_workgroups ? (uint32_t)std::min<uint64_t>(kv->prefill_workgroups, slots) : slots,
-                         pf_wg, pf_per_wg);
-    if (prefill_lds_bytes(kv->kv_type, y.hd, max_pages, pf_per_wg) + prefill_static_lds_bytes() > 160 * 1024) {
-      // key ranges too long to list in LDS: those segments go through the decode kernel
-      kv->pitems.clear();
-      std::fill(decode_row.begin(), decode_row.end(), 1);
-      max_pages = 0;
-      pf_wg = pf_per_wg = 0;
-    }
-  }
-
-  // ---- decode work list: per (row, KV head, head block), the key range [lo, pos] cut into
-  // chunks of whole 16-token tiles, spread evenly; rows whose range fits one chunk write the output.
-  uint64_t total_tiles = 0;
-  for (uint64_t t = 0; t < n_rows; t++) {
-    if (!decode_row[t]) continue;
-    const uint64_t pos = (uint64_t)kv->row_pos[t];
-    const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
-    total_tiles += pos / 16 - lo / 16 + 1;
-  }
-  total_tiles *= (uint64_t)y.n_kv * head_blocks;
-  // Items the GPU holds at once: with at most that many, every item starts in the first round and
-  // none waits for a slot to free up (a second, mostly empty round would double the kernel time).
-  // The matrix-core decode kernel targets half of them: one item per SIMD streams each key range
-  // with its two-deep prefetch as fast as two do, and half the items halve the per-item start-up,
-  // the partials and the merge (often to none: 128 rows of 512 keys become one item per row and
-  // KV head, 56.4 -> 42.6 us; c2 cold 51.2 -> 49.6 us; 4 rows of 16 K keys 54.0 -> 48.9 us; c4 and
-  // rows of a group of 8 unchanged). The f32 and row-layout kernels, latency-bound, keep all of them.
   if (kv->decode_capacity[layer] == 0)
     kv->decode_capacity[layer] = decode_waves_per_cu(kv->kv_type, y.hd, y.hdv, group, y.layout) * kv->n_cu;
-  const bool mfma_decode = y.layout == LAYOUT_TILES && kv->kv_type != LMH_KV_F32;
-  const uint64_t cap_target = mfma_decode ? std::max<uint64_t>(kv->decode_capacity[layer] / 2, kv->n_cu)
-                                          : kv->decode_capacity[layer];
-  uint64_t target = std::max<uint64_t>(kv->decode_target_items ? kv->decode_target_items : cap_target, 1);
-  // no-allocation calls: at most as many split slots (and merges) as the scratch holds
+  PlanIn pin;
+  pin.row_seq = kv->row_seq.data();
+  pin.row_pos = kv->row_pos.data();
+  pin.n_rows = n_rows;
+  pin.segs = segs;
+  pin.n_segs = n_segs;
+  pin.table = y.win ? kv->h_wtable.data() : kv->h_table.data();
+  pin.bps = kv->bps;
+  pin.bt_shift = kv->bt_shift;
+  pin.n_head = y.n_head;
+  pin.n_kv = y.n_kv;
+  pin.hd = y.hd;
+  pin.hdv = y.hdv;
+  pin.layout = y.layout;
+  pin.kv_type = kv->kv_type;
+  pin.window = window;
+  pin.scale = scale;
+  pin.n_cu = kv->n_cu;
+  pin.decode_capacity = kv->decode_capacity[layer];
+  pin.prefill_min_rows = kv->prefill_min_rows;
+  pin.decode_target_items = kv->decode_target_items;
+  pin.decode_min_tiles = kv->decode_min_tiles;
+  pin.prefill_workgroups = kv->prefill_workgroups;
+  pin.noalloc = noalloc;
+  pin.noalloc_bytes = NOALLOC_SCRATCH_BYTES;
+  fill_kernel_facts(pin, kv->kv_type, y.hd, y.hdv, group);
+  PlanOut& pl = kv->plan;
+  plan_attend(pin, pl);
+  const uint32_t ng = pl.ng, slots = pl.slots, pf_wg = pl.pf_wg, pf_per_wg = pl.pf_per_wg, max_pages = pl.max_pages;
+  const bool local = pl.local;
   const size_t slot_bytes = (size_t)ng * (y.hdv + 4) * 4;
-  if (noalloc) target = std::max<uint64_t>(1, std::min<uint64_t>(target, NOALLOC_SCRATCH_BYTES / (slot_bytes + sizeof(MergeItem))));
-  // Smallest chunk: 8 tiles for the matrix-core kernels (enough work per wave to stream at full
-  // rate); 2 tiles for f32 rows, whose VALU kernel walks keys with dependent loads (latency-bound:
-  // more, shorter items hide it better).
-  const uint64_t min_chunk = kv->decode_min_tiles ? kv->decode_min_tiles
-                                                  : (y.layout == LAYOUT_ROWS ? 4 : kv->kv_type == LMH_KV_F32 ? 2 : 8);
-  // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane);
-  // grown until the rows' rounded-up split counts fit the target
-  auto n_items_for = [&](uint64_t c) {
-    uint64_t n = 0;
-    for (uint64_t t = 0; t < n_rows; t++) {
-      if (!decode_row[t]) continue;
-      const uint64_t pos = (uint64_t)kv->row_pos[t];
-      const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
-      n += (pos / 16 - lo / 16 + 1 + c - 1) / c;
-    }
-    return n * y.n_kv * head_blocks;
-  };
-  uint64_t chunk = std::min<uint64_t>(64, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / target));
-  while (chunk < 64 && n_items_for(chunk) > target) chunk++;
-  kv->items.clear();
-  kv->merges.clear();
-  uint32_t slots = 0;
-  const int32_t* tab_l = y.win ? kv->h_wtable.data() : kv->h_table.data();   // the layer's block table
-  // f32 pages, short rows (at most 16 tiles): a row's split items are consecutive waves of one
-  // 8-wave workgroup and merge there (no merge launch). A row splits into 1, 2, 4 or 8 items of
-  // at most 2 tiles (the f32 kernel's smallest chunk); groups of 8 go first, then 4, 2 and single
-  // items, so no group crosses a workgroup. Not with explicit split settings.
-  bool local = false;
-  if (y.layout == LAYOUT_TILES && kv->kv_type == LMH_KV_F32 && decode_local_merge_ok(y.hd, y.hdv, group) &&
-      !kv->decode_target_items && !kv->decode_min_tiles) {
-    uint64_t max_nt = 0;
-    for (uint64_t t = 0; t < n_rows; t++) {
-      if (!decode_row[t]) continue;
-      const uint64_t pos = (uint64_t)kv->row_pos[t];
-      const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
-      max_nt = std::max<uint64_t>(max_nt, pos / 16 - lo / 16 + 1);
-    }
-    local = max_nt > 2 && max_nt <= 16;
-  }
-  if (local) {
-    std::vector<DecodeItem> by_size[4];   // groups of 8, 4, 2, single items
-    for (uint64_t t = 0; t < n_rows; t++) {
-      if (!decode_row[t]) continue;
-      const uint64_t pos = (uint64_t)kv->row_pos[t];
-      const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
-      const uint64_t hi = pos + 1;
-      const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
-      const uint32_t n = n_t <= 2 ? 1 : n_t <= 4 ? 2 : n_t <= 8 ? 4 : 8;
-      std::vector<DecodeItem>& dst = by_size[n == 8 ? 0 : n == 4 ? 1 : n == 2 ? 2 : 3];
-      const uint32_t seq = (uint32_t)kv->row_seq[t];
-      auto blk_of = [&](uint64_t p) { return (uint32_t)tab_l[(size_t)seq * kv->bps + (((p >> 4) << 4) >> kv->bt_shift)]; };
-      for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
-        for (uint32_t hb = 0; hb < head_blocks; hb++) {
-          for (uint32_t s = 0; s < n; s++) {
-            const uint64_t a = tlo + s * n_t / n, b = tlo + (s + 1) * n_t / n;
-            const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
-            const uint32_t slot = n == 1 ? NO_SLOT : LOCAL_SLOT | (s << 8) | n;
-            dst.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slot, seq, blk_of(p0)});
-          }
-        }
-      }
-    }
-    for (auto& v : by_size) kv->items.insert(kv->items.end(), v.begin(), v.end());
-  }
-  for (uint64_t t = 0; t < n_rows && !local; t++) {
-    if (!decode_row[t]) continue;
-    const uint64_t pos = (uint64_t)kv->row_pos[t];
-    const uint64_t lo = (window > 0 && pos + 1 > window) ? pos + 1 - window : 0;
-    const uint64_t hi = pos + 1;
-    const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
-    const uint64_t n_split = (n_t + chunk - 1) / chunk;
-    const uint32_t seq = (uint32_t)kv->row_seq[t];
-    // block id of the tile holding key p (the table entry the kernel would read for it)
-    auto blk_of = [&](uint64_t p) { return (uint32_t)tab_l[(size_t)seq * kv->bps + (((p >> 4) << 4) >> kv->bt_shift)]; };
-    for (uint32_t kvh = 0; kvh < y.n_kv; kvh++) {
-      for (uint32_t hb = 0; hb < head_blocks; hb++) {
-        if (n_split == 1) {
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, seq, blk_of(lo)});
-          continue;
-        }
-        kv->merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, slots, (uint32_t)n_split, 0});
-        for (uint64_t s = 0; s < n_split; s++) {
-          const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
-          const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
-          kv->items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slots++, seq, blk_of(p0)});
-        }
-      }
-    }
-  }
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
-  const size_t items_bytes = kv->items.size() * sizeof(DecodeItem);
+  const size_t items_bytes = kv->plan.items.size() * sizeof(DecodeItem);
   const size_t items_pad = (items_bytes + 255) / 256 * 256;
-  const size_t merges_bytes = kv->merges.size() * sizeof(MergeItem);
+  const size_t merges_bytes = kv->plan.merges.size() * sizeof(MergeItem);
   const size_t merges_pad = (merges_bytes + 255) / 256 * 256;
   // one staged payload: [decode items | merges | prefill items]
-  kv->payload.resize(items_pad + merges_pad + kv->pitems.size() * sizeof(PrefillItem));
-  if (items_bytes) std::memcpy(kv->payload.data(), kv->items.data(), items_bytes);
-  if (merges_bytes) std::memcpy(kv->payload.data() + items_pad, kv->merges.data(), merges_bytes);
-  if (!kv->pitems.empty())
-    std::memcpy(kv->payload.data() + items_pad + merges_pad, kv->pitems.data(), kv->pitems.size() * sizeof(PrefillItem));
+  kv->payload.resize(items_pad + merges_pad + kv->plan.pitems.size() * sizeof(PrefillItem));
+  if (items_bytes) std::memcpy(kv->payload.data(), kv->plan.items.data(), items_bytes);
+  if (merges_bytes) std::memcpy(kv->payload.data() + items_pad, kv->plan.merges.data(), merges_bytes);
+  if (!kv->plan.pitems.empty())
+    std::memcpy(kv->payload.data() + items_pad + merges_pad, kv->plan.pitems.data(), kv->plan.pitems.size() * sizeof(PrefillItem));
   const int32_t *rs, *rp;
   const uint8_t* ex;
   int slot;
@@ -1653,7 +1498,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   pg.p_f16 = kv->prefill_p_f16 ? 1u : 0u;
   pg.q_bytes_32 = (uint64_t)n_rows * y.n_head * y.hd * 4 <= 0xffffffffull ? 1u : 0u;
   const MergeCopy mc{(const uint32_t*)(ex + items_pad), merge_dst,
-                     kv->merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
+                     kv->plan.merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
   // timing events are made on first use: not on the no-allocation path
   auto time_launch = [&](uint32_t kind, LaunchEv& ev) -> hipError_t {
     ev = LaunchEv{};
@@ -1661,32 +1506,32 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   };
   // A mixed batch (prefill units and decode items) runs as one launch: the prefill workgroups
   // first (one per CU they reach), then the decode items, a wave each, on the CUs left free.
-  const bool overlap = !kv->pitems.empty() && !kv->items.empty();
+  const bool overlap = !kv->plan.pitems.empty() && !kv->plan.items.empty();
   LaunchEv ev;
   if (overlap) {
     if ((e = time_launch(LMH_KERNEL_MIXED, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_mixed(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, r,
-                     (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, part, mc, st, ev);
+                     (const DecodeItem*)ex, (uint32_t)kv->plan.items.size(), q, out, part, mc, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "mixed kernel");
   }
-  if (!overlap && !kv->pitems.empty()) {
+  if (!overlap && !kv->plan.pitems.empty()) {
     if ((e = time_launch(LMH_KERNEL_PREFILL, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_prefill(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, q, out,
                        st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
   }
-  if (kv->items.empty()) return kv->release_rows(slot, st);
+  if (kv->plan.items.empty()) return kv->release_rows(slot, st);
   if (!overlap) {
     if ((e = time_launch(LMH_KERNEL_DECODE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
-    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->items.size(), q, out, part, mc, st,
+    e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->plan.items.size(), q, out, part, mc, st,
                       ev);
     if (e != hipSuccess) return kv->hip_fail(e, "decode kernel");
   }
-  if (!kv->merges.empty()) {
+  if (!kv->plan.merges.empty()) {
     if ((e = time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     uint32_t max_split = 0;
-    for (const MergeItem& m : kv->merges) max_split = std::max(max_split, m.n_split);
-    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->merges.size(),
+    for (const MergeItem& m : kv->plan.merges) max_split = std::max(max_split, m.n_split);
+    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->plan.merges.size(),
                      part, out, max_split, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
   }
@@ -1703,14 +1548,20 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   return attend_impl(kv, layer, segs, n_segs, q, out, scale, window, stream, true);
 }
 
+// nullptr, or what is wrong with the options
+static const char* tuning_error(const lmh_attend_tuning* t) {
+  if (!t || t->abi_version != LMH_ABI_VERSION) return "tuning: null or ABI version";
+  if (t->prefill_p_f16 > 1) return "tuning: prefill_p_f16 must be 0 or 1";
+  if (t->prefill_min_rows > (1ull << 32)) return "tuning: prefill_min_rows out of range";
+  if (t->decode_min_tiles > 64) return "tuning: decode_min_tiles must be <= 64";
+  if (t->decode_target_items > (1ull << 32)) return "tuning: decode_target_items out of range";
+  if (t->prefill_workgroups > (1ull << 32)) return "tuning: prefill_workgroups out of range";
+  return nullptr;
+}
+
 int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {
   if (!kv) return LMH_INVALID_ARGUMENT;
-  if (!t || t->abi_version != LMH_ABI_VERSION) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: null or ABI version");
-  if (t->prefill_p_f16 > 1) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_p_f16 must be 0 or 1");
-  if (t->prefill_min_rows > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_min_rows out of range");
-  if (t->decode_min_tiles > 64) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: decode_min_tiles must be <= 64");
-  if (t->decode_target_items > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: decode_target_items out of range");
-  if (t->prefill_workgroups > (1ull << 32)) return kv->fail(LMH_INVALID_ARGUMENT, "tuning: prefill_workgroups out of range");
+  if (const char* why = tuning_error(t)) return kv->fail(LMH_INVALID_ARGUMENT, why);
   kv->prefill_p_f16 = t->prefill_p_f16 != 0;
   kv->prefill_workgroups = t->prefill_workgroups;
   kv->prefill_min_rows = t->prefill_min_rows;
@@ -1727,6 +1578,85 @@ int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t) {
   t->decode_target_items = kv->decode_target_items;
   t->decode_min_tiles = kv->decode_min_tiles;
   t->prefill_workgroups = kv->prefill_workgroups;
+  return LMH_OK;
+}
+
+// The planner alone on host data (no device): validates like lmh_kv_create / lmh_attend, plans as
+// lmh_attend would for a layer of this geometry, and copies the work lists out.
+int32_t lmh_plan_attend(const lmh_plan_desc* d, const lmh_seg* segs, uint64_t n_segs, uint32_t* items,
+                        uint64_t items_cap, uint32_t* merges, uint64_t merges_cap, uint32_t* units, uint64_t units_cap,
+                        lmh_plan_counts* counts) {
+  if (!d || !counts || d->abi_version != LMH_ABI_VERSION || (n_segs > 0 && !segs)) return LMH_INVALID_ARGUMENT;
+  const uint32_t bt = d->block_tokens;
+  if (d->kv_type > LMH_KV_BF16 || bt == 0 || (bt & (bt - 1)) != 0 || d->n_kv == 0 || d->n_head == 0 ||
+      d->n_head % d->n_kv != 0 || d->hd == 0 || d->hdv == 0 || d->hd > MAX_HEAD_DIM || d->hdv > MAX_HEAD_DIM ||
+      (d->kv_type == LMH_KV_Q8_0 && (d->hd % 32 != 0 || d->hdv % 32 != 0)) || d->n_cu == 0 || d->n_seqs == 0 ||
+      d->bps == 0 || !d->table || !std::isfinite(d->scale) || tuning_error(&d->tuning))
+    return LMH_INVALID_ARGUMENT;
+  uint32_t bt_shift = 0;
+  while ((1u << bt_shift) < bt) bt_shift++;
+  std::vector<int32_t> row_seq, row_pos;
+  uint64_t n_rows = 0;
+  for (uint64_t i = 0; i < n_segs; i++) {
+    const lmh_seg& sg = segs[i];
+    if (sg.seq >= d->n_seqs || sg.start != n_rows || sg.pos0 + sg.n > d->bps * bt || sg.pos0 + sg.n > 0x7fffffffull)
+      return LMH_INVALID_ARGUMENT;
+    for (uint64_t j = 0; j < sg.n; j++) {   // every block the row's range touches is in the table
+      const uint64_t pos = sg.pos0 + j, lo = (d->window > 0 && pos + 1 > d->window) ? pos + 1 - d->window : 0;
+      if (d->table[sg.seq * d->bps + (pos >> bt_shift)] < 0 || d->table[sg.seq * d->bps + (lo >> bt_shift)] < 0)
+        return LMH_INVALID_ARGUMENT;
+      row_seq.push_back((int32_t)sg.seq);
+      row_pos.push_back((int32_t)pos);
+    }
+    n_rows += sg.n;
+  }
+  PlanIn in;
+  in.row_seq = row_seq.data();
+  in.row_pos = row_pos.data();
+  in.n_rows = n_rows;
+  in.segs = segs;
+  in.n_segs = n_segs;
+  in.table = d->table;
+  in.bps = d->bps;
+  in.bt_shift = bt_shift;
+  in.n_head = d->n_head;
+  in.n_kv = d->n_kv;
+  in.hd = d->hd;
+  in.hdv = d->hdv;
+  in.layout = (bt >= 16 && decode_tiles_supported(d->kv_type, d->hd, d->hdv)) ? LAYOUT_TILES : LAYOUT_ROWS;
+  in.kv_type = d->kv_type;
+  in.window = d->window;
+  in.scale = d->scale;
+  in.n_cu = d->n_cu;
+  in.decode_capacity = d->decode_capacity ? d->decode_capacity : 8ull * d->n_cu;
+  in.prefill_min_rows = d->tuning.prefill_min_rows;
+  in.decode_target_items = d->tuning.decode_target_items;
+  in.decode_min_tiles = d->tuning.decode_min_tiles;
+  in.prefill_workgroups = d->tuning.prefill_workgroups;
+  in.noalloc = d->noalloc != 0;
+  in.noalloc_bytes = NOALLOC_SCRATCH_BYTES;
+  fill_kernel_facts(in, d->kv_type, d->hd, d->hdv, d->n_head / d->n_kv);
+  PlanOut o;
+  if (n_rows > 0) plan_attend(in, o);
+  counts->n_items = o.items.size();
+  counts->n_merges = o.merges.size();
+  counts->n_units = o.pitems.size();
+  counts->item_words = sizeof(DecodeItem) / 4;
+  counts->merge_words = sizeof(MergeItem) / 4;
+  counts->unit_words = sizeof(PrefillItem) / 4;
+  counts->ng = o.ng;
+  counts->slots = o.slots;
+  counts->pf_wg = o.pf_wg;
+  counts->pf_per_wg = o.pf_per_wg;
+  counts->max_pages = o.max_pages;
+  counts->local = o.local ? 1u : 0u;
+  counts->layout = in.layout;
+  counts->chunk = o.chunk;
+  if (o.items.size() > items_cap || o.merges.size() > merges_cap || o.pitems.size() > units_cap)
+    return LMH_INVALID_ARGUMENT;   // the counts say how much room the lists need
+  if (!o.items.empty()) std::memcpy(items, o.items.data(), o.items.size() * sizeof(DecodeItem));
+  if (!o.merges.empty()) std::memcpy(merges, o.merges.data(), o.merges.size() * sizeof(MergeItem));
+  if (!o.pitems.empty()) std::memcpy(units, o.pitems.data(), o.pitems.size() * sizeof(PrefillItem));
   return LMH_OK;
 }
 

@@ -1,0 +1,56 @@
+// work.h — the per-call work lists lmh_attend's planner (plan.cpp, host only) builds and the
+// attention kernels read: plain structures, no device headers.
+#pragma once
+
+#include <stdint.h>
+
+namespace lmh {
+
+enum : uint32_t { KV_F16 = 0, KV_Q8 = 1, KV_F32 = 2, KV_BF16 = 3 };
+constexpr uint32_t LAYOUT_TILES = 0, LAYOUT_ROWS = 1;
+
+// One decode work item: row `row` (its sequence and position come from the row arrays), KV head
+// `kvh`, query heads kvh*group + h0 .. + n_heads, keys [p0, p1). `slot` is the partial-result slot
+// (split-K) or NO_SLOT when the item covers the row's whole key range and writes the output.
+struct DecodeItem {
+  uint32_t row;
+  uint32_t kvh;
+  uint32_t h0;
+  uint32_t p0, p1;
+  uint32_t slot;
+  uint32_t seq;   // the row's sequence (saves a dependent read of the row arrays)
+  uint32_t blk0;  // block id of the first tile p0 >> 4 (the first fetch skips the block-table read)
+};
+constexpr uint32_t NO_SLOT = 0xffffffffu;
+// A split item merged inside its workgroup (f32 decode of short rows): LOCAL_SLOT | (its index in
+// the row's group << 8) | the group's size; the group's items are consecutive waves of one
+// workgroup, and the first merges their partials from LDS, so the call needs no merge launch.
+constexpr uint32_t LOCAL_SLOT = 0x80000000u;
+constexpr uint32_t LOCAL_MERGE_MAX = 1024;   // heads x hdv of an item whose partials a wave keeps in LDS
+constexpr int LOCAL_WAVES = 8;               // waves per workgroup of a local-merge call (its largest group)
+
+// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..).
+struct MergeItem {
+  uint32_t row;
+  uint32_t kvh;
+  uint32_t h0;
+  uint32_t slot0;
+  uint32_t n_split;
+  uint32_t pad;
+};
+
+// One prefill work unit: KV head `kvh` of sequence `seq`, tokens at positions pos0 .. pos0+n_tok-1
+// which are stacked rows row0 .. row0+n_tok-1 (n_tok * group <= prefill_cols_per_unit()).
+// blk: the block ids of the unit's first 8 key pages (page i of its key range, clamped to the last
+// page), so the first K/V tiles are fetched without waiting for the block table.
+struct PrefillItem {
+  uint32_t seq;
+  uint32_t kvh;
+  uint32_t row0;
+  uint32_t pos0;
+  uint32_t n_tok;
+  uint32_t pad0, pad1, pad2;
+  uint32_t blk[8];
+};
+
+}  // namespace lmh

@@ -92,12 +92,20 @@ def test_noalloc_first_calls_on_a_fresh_handle(cuda):
     shape = (w.n_rows, w.layer.n_head, w.layer.hdv)
     b = torch.full(shape, float("nan"), device="cuda")
     a = torch.full(shape, float("nan"), device="cuda")
+    # earlier tests' handles are collected first, and not during the calls (their frees would
+    # raise the free memory the check reads)
+    import gc
+    gc.collect()
     torch.cuda.synchronize()
-    free0 = torch.cuda.mem_get_info()[0]
-    for _ in range(40):
-        hc.attend_noalloc(0, w.segments(), q, b, w.scale)
-    torch.cuda.synchronize()
-    free1 = torch.cuda.mem_get_info()[0]
+    gc.disable()
+    try:
+        free0 = torch.cuda.mem_get_info()[0]
+        for _ in range(40):
+            hc.attend_noalloc(0, w.segments(), q, b, w.scale)
+        torch.cuda.synchronize()
+        free1 = torch.cuda.mem_get_info()[0]
+    finally:
+        gc.enable()
     hc.attend(0, w.segments(), q, a, w.scale)
     torch.cuda.synchronize()
     print(f"device memory free before / after 40 noalloc calls: {free0} / {free1}")
