@@ -83,7 +83,6 @@ struct PrefillGeom {
   float scale_log2;  // scale * log2(e)
   uint32_t window;   // 0 = none
   uint32_t p_f16;    // 1: P rounded to f16 for P.V (Metal's prefill precision); 0: f16 hi + lo (q8_0: always hi + lo)
-  uint32_t q_bytes_32;   // 1: every Q row offset fits 32 bits (the next unit's Q may be prefetched)
 };
 
 // Fused per-row tail of attention_block (see lmh_qk_rope_store): flags as LMH_ROPE_*.

@@ -1496,7 +1496,6 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   pg.scale_log2 = r.scale_log2;
   pg.window = r.window;
   pg.p_f16 = kv->prefill_p_f16 ? 1u : 0u;
-  pg.q_bytes_32 = (uint64_t)n_rows * y.n_head * y.hd * 4 <= 0xffffffffull ? 1u : 0u;
   const MergeCopy mc{(const uint32_t*)(ex + items_pad), merge_dst,
                      kv->plan.merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
   // timing events are made on first use: not on the no-allocation path

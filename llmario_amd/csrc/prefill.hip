@@ -89,15 +89,6 @@ __device__ inline void lds_dma16(const uint8_t* sbase, uint32_t voff, uint32_t l
                : "memory", "m0");
 }
 
-// 4 bytes per lane into LDS (global_load_lds_dword, LDS address lds_dst + 4*L): used only to pull
-// lines into the caches ahead of use; the LDS destination is scratch nobody reads.
-__device__ inline void lds_dma4(const uint8_t* sbase, uint32_t voff, uint32_t lds_dst) {
-  const uint32_t l = __builtin_amdgcn_readfirstlane(lds_dst);
-  asm volatile("s_nop 4\n\ts_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2" ::"s"(l), "v"(voff),
-               "s"(sbase)
-               : "memory", "m0");
-}
-
 // bf16 pair (one uint32) -> f16 pair (one uint32), exact in the normal f16 range.
 __device__ inline uint32_t bf2_to_h2(uint32_t w) {
   typedef float f2 __attribute__((ext_vector_type(2)));
@@ -215,10 +206,19 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // (clamped to its last page) for the current 64-page chunk c, computed from the block-id list
   // once per 16 tiles, so a DMA costs two readlanes instead of an LDS read that waits for every
   // LDS operation in flight (the operand reads of the tile being computed among them).
+  // q8_0 keeps one lane-held block id instead of the four address words, the address then formed
+  // in scalar registers: its instance has no registers to spare, and the four words spilled to
+  // scratch memory were reloaded on every tile.
   const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
   uint32_t pk_lo = 0, pk_hi = 0, pv_lo = 0, pv_hi = 0, chunk = ~0u;
+  int blk_lane = 0;
   auto load_chunk = [&](uint32_t c) {
     const uint32_t p = min(c * 64 + lane, n_pages - 1);
+    if constexpr (Q8) {
+      blk_lane = blk_lds[p];
+      chunk = c;
+      return;
+    }
     const uint64_t b = (uint64_t)(uintptr_t)g.pool + (uint64_t)(uint32_t)blk_lds[p] * g.block_bytes;
     const uint32_t sub = (((page0 + p) << 4) & bt_mask) >> 4;
     const uint64_t kb = b + k_head + (uint64_t)sub * g.k_tile, vb = b + v_head + (uint64_t)sub * g.v_tile;
@@ -237,6 +237,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     }
     const uint32_t p = ti * 4 + tile;
     if ((p >> 6) != chunk) load_chunk(p >> 6);
+    if constexpr (Q8) {   // lane p % 64 holds the block id of page min(p, n_pages - 1)
+      const uint64_t blk = (uint32_t)__builtin_amdgcn_readlane(blk_lane, (int)(p & 63u));
+      const uint32_t sub = (((page0 + min(p, n_pages - 1)) << 4) & bt_mask) >> 4;
+      return g.pool + blk * g.block_bytes + (v_side ? v_head + (uint64_t)sub * g.v_tile : k_head + (uint64_t)sub * g.k_tile);
+    }
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane(v_side ? pv_lo : pk_lo, (int)(p & 63u));
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane(v_side ? pv_hi : pk_hi, (int)(p & 63u));
     return (const uint8_t*)(uintptr_t)(((uint64_t)hi << 32) | lo);
@@ -774,40 +779,6 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     }
   };
   auto sync = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
-  // q8_0: the next unit's Q rows pulled into the L2 while this unit's last tiles compute, so its
-  // prologue does not wait on HBM for them (c3 on q8_0 pages 472 -> 452 us; no gain on 16-bit
-  // pages, whose units are shorter, so only q8_0 units do it). PF DMAs of 4 bytes per lane, one per
-  // 128-byte line; their LDS destination is scratch nobody reads.
-  __shared__ uint32_t pf_junk[Q8 ? PW * 64 : 1];
-  constexpr int PF = HD / 64;   // lines per lane: 256 columns x HD*4 bytes / 128 / 512 lanes
-  const bool last_pass = !lo_any || pass == 1;
-  const bool pf_on = Q8 && last_pass && unit + 1 < per_wg && units[unit + 1].n_tok != 0 && n_tiles >= 3 &&
-                     pg.q_bytes_32;
-  auto prefetch_next_q = [&]() {
-    const PrefillItem nx = units[unit + 1];
-    const uint32_t lpc = HD / 32;                    // 128-byte lines per column (one head row)
-    const uint32_t n_col = nx.n_tok * G;
-    const uint32_t junk = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint32_t*)pf_junk + w * 256;
-#pragma unroll
-    for (int k = 0; k < PF; k++) {
-      const uint32_t line = min(k * NT + tid, n_col * lpc - 1);
-      const uint32_t c = line / lpc, j = line % lpc;
-      const uint32_t t = c / G, hh = c % G;
-      const uint32_t off = (((nx.row0 + t) * pg.n_head + nx.kvh * G + hh) * HD) * 4 + j * 128;
-      lds_dma4((const uint8_t*)q, off, junk);
-    }
-  };
-  auto wait_tile_pf = [&](uint32_t ti) {   // wait_tile when the prefetch DMAs follow tile ti+1's
-    constexpr int D = (Q8 ? QR + 1 : 2 * CPT) + PF;
-    if (ti + 1 < n_tiles) {
-      if constexpr (D == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-      else if constexpr (D == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-      else if constexpr (D == 5) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-      else asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
-    } else {
-      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    }
-  };
   f4 S0[2][NCB], S1[2][NCB];
   h8 Ph[NCB], Pl[NCB];
   KOps ko;
@@ -821,8 +792,6 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   }
   for (uint32_t ti = 0; ti < n_tiles; ti++) {
     if (ti + 2 < n_tiles) issue(ti + 2);
-    const bool pf_here = pf_on && ti + 3 == n_tiles;   // the iteration that issues the last tile
-    if (pf_here) prefetch_next_q();
     const uint8_t* kt = kv_lds + (ti % NSTAGE) * STAGE;
     const uint8_t* vt = kt + 4 * TILE;
     const uint32_t key0 = (page0 + ti * 4) * 16;
@@ -831,14 +800,14 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
       load_k(ko, kt, 1);
       load_v(vo, vt, 0);
       if (need_mask) mask(S0, key0);
-      if (pf_here) wait_tile_pf(ti + 1); else wait_tile(ti + 1);
+      wait_tile(ti + 1);
       settle(ti + 1);
       qk(S1, ko);
       softmax(S0, Ph, Pl, S1);
       pv(Ph, Pl, vo);
       if (need_mask) mask(S1, key0 + 32);
     } else {
-      if (pf_here) wait_tile_pf(ti + 1); else wait_tile(ti + 1);
+      wait_tile(ti + 1);
       settle(ti + 1);
     }
     if (ti + 1 < n_tiles) sync();
@@ -953,7 +922,7 @@ uint32_t prefill_cols_per_unit() { return PW * COLS; }
 
 uint32_t prefill_wg_per_cu() { return 1; }   // the LDS stages fill a CU
 
-size_t prefill_static_lds_bytes() { return 64 + PW * 64 * 4; }  // lo_flags[PW] rounded up; q8_0: pf_junk
+size_t prefill_static_lds_bytes() { return 64; }  // lo_flags[PW] rounded up
 
 size_t prefill_lds_bytes(uint32_t kv_type, uint32_t hd, uint32_t max_pages, uint32_t per_wg) {
   const size_t stage = 8 * (16 * (size_t)hd * 2) + (kv_type == KV_Q8 ? 8 * (size_t)hd : 0);   // + q8_0 scales
