@@ -275,7 +275,7 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
  *     the CPU path's f32 weights to within the 2e-3 bound even on rows whose output cancels).
  *     Applies to f16 / bf16 pages: q8_0 prompts always carry their scaled weights as bf16 hi + lo.
  *   prefill_min_rows: segments of at least this many rows go to the matrix-core prefill kernel
- *     (default 16; 1 .. 2^32).
+ *     (default 8, as Metal routes prompts of 8 tokens or more to its flash prefill; 1 .. 2^32).
  *   decode_target_items: split-K target of decode work items (default: half the items the device
  *     holds at once, from the occupancy query, for the matrix-core decode kernel; all of them for
  *     f32 and row-layout layers).

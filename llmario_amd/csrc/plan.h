@@ -60,8 +60,12 @@ struct PlanOut {
   bool local = false;                 // decode items merge inside their workgroups
 };
 
-// Segments of at least this many rows run on the matrix-core prefill kernel by default.
-constexpr uint64_t DEFAULT_PREFILL_MIN_ROWS = 16;
+// Segments of at least this many rows run on the matrix-core prefill kernel by default (Metal's
+// FA_MIN_TOKENS, metal/src/backend.rs:181). Measured on 8-row segments at contexts of 512..4096,
+// 32/8 heads, hd 128: the prefill kernel takes 89 us for 8 sequences (86 us as decode rows, each
+// re-reading its prefix) and 105 us for 32 (354 us as decode rows); at 4 rows the decode rows win
+// for 8 sequences (41 against 89 us).
+constexpr uint64_t DEFAULT_PREFILL_MIN_ROWS = 8;
 
 void plan_attend(const PlanIn& in, PlanOut& out);
 

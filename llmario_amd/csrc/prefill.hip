@@ -406,23 +406,25 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // needs no widening; qf then holds bf16 bits (split_q_bf16). Any other Q takes the two-pass f16
   // hi + lo path with K widened. q8_0 pages: the codes are widened to f16 either way; a Q exact in
   // f16 runs one pass.
+  // A value is exact in bf16 when the low 16 bits of its f32 encoding are zero: the test ORs the
+  // encodings and the bf16 values are their upper halves (one byte permute per pair); the values are
+  // only used when every one was exact (otherwise the unit takes the two-pass path).
   auto split_q_bf16 = [&](const float4 (&raw)[NC][2], h8 (&hi)[NC]) {
-    bool nz = false;
+    uint32_t low = 0;
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
       const float4 a = raw[ch][0], b = raw[ch][1];
-      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      const uint32_t u[8] = {__float_as_uint(a.x), __float_as_uint(a.y), __float_as_uint(a.z), __float_as_uint(a.w),
+                             __float_as_uint(b.x), __float_as_uint(b.y), __float_as_uint(b.z), __float_as_uint(b.w)};
       uint32_t wd[4];
 #pragma unroll
       for (int i = 0; i < 8; i += 2) {
-        const uint16_t h0 = dtile::bf16_rne(x[i]), h1 = dtile::bf16_rne(x[i + 1]);
-        nz |= __uint_as_float((uint32_t)h0 << 16) != x[i];
-        nz |= __uint_as_float((uint32_t)h1 << 16) != x[i + 1];
-        wd[i / 2] = (uint32_t)h0 | ((uint32_t)h1 << 16);
+        low |= u[i] | u[i + 1];
+        wd[i / 2] = __builtin_amdgcn_perm(u[i + 1], u[i], 0x07060302u);   // [hi16(u[i]), hi16(u[i+1])]
       }
       hi[ch] = __builtin_bit_cast(h8, make_uint4(wd[0], wd[1], wd[2], wd[3]));
     }
-    return nz;
+    return (low & 0xffffu) != 0;
   };
   h8 qf[2][NC];
   if (pass == 0) {
