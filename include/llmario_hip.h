@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define LMH_ABI_VERSION 2u
+#define LMH_ABI_VERSION 3u
 
 /* status codes */
 #define LMH_OK 0
@@ -281,6 +281,9 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
  *     f32 and row-layout layers).
  *   decode_min_tiles: smallest split-K chunk in 16-key tiles (default 8; 2 for f32 pages; 4 for
  *     row-layout layers; 1 .. 64).
+ *   prefill_whole_units: 1 = prefill units always run whole; 0 (default) = when whole units would
+ *     leave the device unbalanced (few, long units), their key ranges are cut into pieces spread over
+ *     the workgroups, whose partial results a merge launch combines (heads per KV group <= 16).
  * Out-of-range values fail with LMH_INVALID_ARGUMENT and change nothing. */
 typedef struct lmh_attend_tuning {
   uint32_t abi_version;        /* LMH_ABI_VERSION */
@@ -290,6 +293,8 @@ typedef struct lmh_attend_tuning {
   uint64_t decode_min_tiles;
   uint64_t prefill_workgroups;  /* cap on the prefill kernel's workgroups (0: every slot of the device);
                                    fewer workgroups run more units each */
+  uint32_t prefill_whole_units;
+  uint32_t reserved;            /* 0 */
 } lmh_attend_tuning;
 int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t);
 /* The options as set (0 = the default, which each call resolves). */

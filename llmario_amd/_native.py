@@ -18,7 +18,7 @@ STATUS_NAMES = {0: "OK", 1: "INVALID_ARGUMENT", 2: "KV_FULL", 3: "UNSUPPORTED", 
                 5: "OUT_OF_MEMORY"}
 KV_F16, KV_Q8_0, KV_F32, KV_BF16 = 0, 1, 2, 3
 KV_TYPES = {"f16": KV_F16, "q8_0": KV_Q8_0, "f32": KV_F32, "bf16": KV_BF16}
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 u32, u64, i32, P = C.c_uint32, C.c_uint64, C.c_int32, C.c_void_p
 
@@ -61,7 +61,8 @@ class RopeParams(C.Structure):
 
 class AttendTuning(C.Structure):
     _fields_ = [("abi_version", u32), ("prefill_p_f16", u32), ("prefill_min_rows", u64),
-                ("decode_target_items", u64), ("decode_min_tiles", u64), ("prefill_workgroups", u64)]
+                ("decode_target_items", u64), ("decode_min_tiles", u64), ("prefill_workgroups", u64),
+                ("prefill_whole_units", u32), ("reserved", u32)]
 
 
 class PlanDesc(C.Structure):

@@ -49,18 +49,90 @@ constexpr int waves_per_eu() {
   return (HD >= 256 || (HD >= 192 && HDV >= 192)) ? 1 : LMH_DECODE_WPE;
 }
 
-// Split-K merge (forward.rs:772-806), one wave per (task, query head), lanes over dims:
+// A prompt token's merge (MergeItem.nh != 0: the key pieces of a cut prefill unit), one wave per
+// item over its heads [h0, h0 + nh): row j of a chunk of heads is (head j / k, piece j % k) of the
+// item's k <= 64 partials (piece s in slot slot0 + s, head at position h). Lane j holds row j's
+// (m, l) and turns them into 2^(m - M_h) and 1 / L_h of its head; every lane then folds the
+// chunk's rows (16 loads in flight) into its NP dims, storing a head after its last piece. One
+// wave carries every head and piece of the token, so the few bytes of each merge are fetched in
+// one round trip instead of one per head.
+template <int NP>
+__device__ void merge_heads(const RowGeom& r, uint32_t hdv, const MergeItem& mi, const float* part, float* out,
+                            uint32_t lane) {
+  const uint32_t k = mi.n_split;
+  const size_t hstride = hdv + 4, stride = (size_t)r.ng * hstride;
+  const float* base = part + (size_t)mi.slot0 * stride;
+  const uint32_t hpc = 64u / k;   // heads per chunk
+  for (uint32_t hc = 0; hc < mi.nh; hc += hpc) {
+    const uint32_t nrow = (mi.nh - hc < hpc ? mi.nh - hc : hpc) * k;
+    const uint32_t jh = lane / k, first = jh * k;
+    float m = -INFINITY, l = 0.f;
+    if (lane < nrow) {
+      const float* pr = base + (size_t)(lane - first) * stride + (size_t)(hc + jh) * hstride + hdv;
+      m = pr[0];   // separate loads: (m, l) are 8-byte aligned only for even hdv
+      l = pr[1];
+    }
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < k; s++) M = fmaxf(M, __shfl(m, (int)(first + s)));
+    const float c = m == -INFINITY ? 0.f : exp2_fast(m - M);
+    const float cl = c * l;
+    float L = 0.f;
+    for (uint32_t s = 0; s < k; s++) L += __shfl(cl, (int)(first + s));
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    float acc[NP];
+#pragma unroll
+    for (int i = 0; i < NP; i++) acc[i] = 0.f;
+    for (uint32_t j0 = 0; j0 < nrow; j0 += 16) {
+      float pre[16][NP];
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        const uint32_t j = j0 + t;
+        const float* pp = base + (size_t)(j % k) * stride + (size_t)(hc + j / k) * hstride + lane * NP;
+#pragma unroll
+        for (int i = 0; i < NP; i++) pre[t][i] = j < nrow && lane * NP + i < hdv ? pp[i] : 0.f;
+      }
+#pragma unroll
+      for (int t = 0; t < 16; t++) {
+        const uint32_t j = j0 + t;
+        if (j < nrow) {
+          const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), (int)j));
+#pragma unroll
+          for (int i = 0; i < NP; i++) acc[i] += cj * pre[t][i];
+          if (j % k == k - 1) {
+            const float iv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), (int)j));
+            float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + hc + j / k) * hdv + lane * NP;
+#pragma unroll
+            for (int i = 0; i < NP; i++) {
+              if (lane * NP + i < hdv) op[i] = acc[i] * iv;
+              acc[i] = 0.f;
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// Split-K merge (forward.rs:772-806): the n_pf leading items are prompt tokens' merges (one wave
+// each, merge_heads); then one wave per (decode item, query head), lanes over dims:
 // m* = max m_s, out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m in the log2 domain.
 // A separate launch: the kernel boundary makes every split's partials visible across XCDs.
-// GROUPS: some item has more than 16 splits (rows past the first 16 are loaded in groups of 16;
-// without it the kernel keeps the lighter code that a call with at most 16 splits per item runs).
+// GROUPS: some decode item has more than 16 splits (rows past the first 16 are loaded in groups of
+// 16; without it the kernel keeps the lighter code that a call with at most 16 splits per item
+// runs).
 template <int NP, bool GROUPS>
 __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, uint32_t hdv, const MergeItem* items, uint32_t n_items,
-                                                    const float* part, float* out) {
+                                                    uint32_t n_pf, const float* part, float* out) {
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (wi >= n_items * r.ng) return;
-  const MergeItem mi = items[wi / r.ng];
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (wv < n_pf) {
+    const MergeItem mi = items[wv];
+    merge_heads<NP>(r, hdv, mi, part, out, lane);
+    return;
+  }
+  const uint32_t wi = wv - n_pf;
+  if (wi >= (n_items - n_pf) * r.ng) return;
+  const MergeItem mi = items[n_pf + wi / r.ng];
   const uint32_t h = wi % r.ng;
   if (mi.h0 + h >= r.group) return;
   // lane L folds dims L*NP .. L*NP+NP-1 (NP = ceil(hdv / 64); lanes past hdv idle)
@@ -730,18 +802,19 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev) {
+hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, uint32_t n_pf,
+                        const float* part, float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
-  if (hdv == 0 || hdv > ROWS_MAX_DIM) return hipErrorInvalidValue;
-  const uint32_t waves = n_items * r.ng;
-  const dim3 grid((waves + 3) / 4), block(256);
+  if (hdv == 0 || hdv > ROWS_MAX_DIM || n_pf > n_items) return hipErrorInvalidValue;
+  const uint64_t waves = n_pf + (uint64_t)(n_items - n_pf) * r.ng;
+  const dim3 grid((uint32_t)((waves + 3) / 4)), block(256);
   // dims per lane: ceil(hdv / 64) rounded up to a power of two
   const uint32_t np = hdv <= 64 ? 1 : hdv <= 128 ? 2 : hdv <= 256 ? 4 : 8;
 #define LMH_MERGE(NP)                                                                                              \
   if (np == NP) {                                                                                                  \
-    if (max_split > 16) LMH_LAUNCH(ev, (merge_kernel<NP, true>), grid, block, 0, s, r, hdv, items, n_items, part, out); \
-    else LMH_LAUNCH(ev, (merge_kernel<NP, false>), grid, block, 0, s, r, hdv, items, n_items, part, out);           \
+    if (max_split > 16)                                                                                            \
+      LMH_LAUNCH(ev, (merge_kernel<NP, true>), grid, block, 0, s, r, hdv, items, n_items, n_pf, part, out);        \
+    else LMH_LAUNCH(ev, (merge_kernel<NP, false>), grid, block, 0, s, r, hdv, items, n_items, n_pf, part, out);    \
     return hipGetLastError();                                                                                      \
   }
   LMH_MERGE(1) LMH_MERGE(2) LMH_MERGE(4) LMH_MERGE(8)

@@ -83,6 +83,8 @@ struct PrefillGeom {
   float scale_log2;  // scale * log2(e)
   uint32_t window;   // 0 = none
   uint32_t p_f16;    // 1: P rounded to f16 for P.V (Metal's prefill precision); 0: f16 hi + lo (q8_0: always hi + lo)
+  uint32_t ng;       // heads per partial slot (units that are key pieces write partials)
+  float* part;       // the call's partial slots
 };
 
 // Fused per-row tail of attention_block (see lmh_qk_rope_store): flags as LMH_ROPE_*.
@@ -147,9 +149,10 @@ struct MergeCopy {
 hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t n_items,
                          const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,
                          const LaunchEv& ev = {});
-// max_split: the largest n_split of the items (over 16: rows loaded in groups of 16)
-hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, const float* part,
-                        float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev = {});
+// items: n_pf prompt-token merges (nh != 0, n_split <= 64) first, then the decode merges;
+// max_split: the largest n_split of the decode merges (over 16: rows loaded in groups of 16)
+hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, uint32_t n_pf,
+                        const float* part, float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev = {});
 // The device scratch of lmh_attend_noalloc (split-K partials, then the merge list): its size, and
 // the address of `device`'s copy (call with that device current; resolved once per device).
 constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;
@@ -168,8 +171,8 @@ bool decode_local_merge_ok(uint32_t hd, uint32_t hdv, uint32_t group);
 // Prefill (multi-token segments on matrix cores): n_wg workgroups, workgroup b runs the units
 // items[b * per_wg ..] up to the first with n_tok == 0. `max_pages` bounds the key pages of any unit.
 hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
-                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s,
-                          const LaunchEv& ev = {});
+                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, const MergeCopy& mc,
+                          hipStream_t s, const LaunchEv& ev = {});
 bool prefill_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv, uint32_t group);
 // A call holding both prefill units and decode items, in one launch (any type and head size
 // prefill_supported accepts): pf_wg prefill workgroups, then the decode items eight per workgroup.

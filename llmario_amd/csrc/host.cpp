@@ -281,6 +281,7 @@ struct lmh_kv {
   bool prefill_p_f16 = false;
   uint64_t prefill_min_rows = 0, decode_target_items = 0, decode_min_tiles = 0;  // 0: defaults
   uint64_t prefill_workgroups = 0;                                                  // 0: every slot
+  bool prefill_whole_units = false;   // prefill units never cut into key pieces
   std::string err;
 
   ~lmh_kv() {
@@ -1435,6 +1436,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   pin.decode_target_items = kv->decode_target_items;
   pin.decode_min_tiles = kv->decode_min_tiles;
   pin.prefill_workgroups = kv->prefill_workgroups;
+  pin.prefill_no_split = kv->prefill_whole_units;
   pin.noalloc = noalloc;
   pin.noalloc_bytes = NOALLOC_SCRATCH_BYTES;
   fill_kernel_facts(pin, kv->kv_type, y.hd, y.hdv, group);
@@ -1496,6 +1498,8 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   pg.scale_log2 = r.scale_log2;
   pg.window = r.window;
   pg.p_f16 = kv->prefill_p_f16 ? 1u : 0u;
+  pg.ng = ng;
+  pg.part = part;
   const MergeCopy mc{(const uint32_t*)(ex + items_pad), merge_dst,
                      kv->plan.merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
   // timing events are made on first use: not on the no-allocation path
@@ -1516,11 +1520,10 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   if (!overlap && !kv->plan.pitems.empty()) {
     if ((e = time_launch(LMH_KERNEL_PREFILL, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_prefill(g, pg, (const PrefillItem*)(ex + items_pad + merges_pad), pf_wg, pf_per_wg, max_pages, q, out,
-                       st, ev);
+                       mc, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "prefill kernel");
   }
-  if (kv->plan.items.empty()) return kv->release_rows(slot, st);
-  if (!overlap) {
+  if (!overlap && !kv->plan.items.empty()) {
     if ((e = time_launch(LMH_KERNEL_DECODE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     e = launch_decode(g, r, (const DecodeItem*)ex, (uint32_t)kv->plan.items.size(), q, out, part, mc, st,
                       ev);
@@ -1528,9 +1531,18 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   }
   if (!kv->plan.merges.empty()) {
     if ((e = time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
-    uint32_t max_split = 0;
-    for (const MergeItem& m : kv->plan.merges) max_split = std::max(max_split, m.n_split);
-    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->plan.merges.size(),
+    // the planner lists the prompt tokens' merges (nh != 0) before the decode merges
+    uint32_t max_split = 0, n_pf = 0;
+    for (const MergeItem& m : kv->plan.merges) {
+      if (m.nh != 0) {
+        if (n_pf != (uint32_t)(&m - kv->plan.merges.data()) || m.n_split > PF_MAX_PIECES)
+          return kv->fail(LMH_UNSUPPORTED, "attend: the planner's prompt merges are out of order or too long");
+        n_pf++;
+      } else {
+        max_split = std::max(max_split, m.n_split);
+      }
+    }
+    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->plan.merges.size(), n_pf,
                      part, out, max_split, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
   }
@@ -1555,6 +1567,8 @@ static const char* tuning_error(const lmh_attend_tuning* t) {
   if (t->decode_min_tiles > 64) return "tuning: decode_min_tiles must be <= 64";
   if (t->decode_target_items > (1ull << 32)) return "tuning: decode_target_items out of range";
   if (t->prefill_workgroups > (1ull << 32)) return "tuning: prefill_workgroups out of range";
+  if (t->prefill_whole_units > 1) return "tuning: prefill_whole_units must be 0 or 1";
+  if (t->reserved != 0) return "tuning: reserved must be 0";
   return nullptr;
 }
 
@@ -1566,6 +1580,7 @@ int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {
   kv->prefill_min_rows = t->prefill_min_rows;
   kv->decode_target_items = t->decode_target_items;
   kv->decode_min_tiles = t->decode_min_tiles;
+  kv->prefill_whole_units = t->prefill_whole_units != 0;
   return LMH_OK;
 }
 
@@ -1577,6 +1592,8 @@ int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t) {
   t->decode_target_items = kv->decode_target_items;
   t->decode_min_tiles = kv->decode_min_tiles;
   t->prefill_workgroups = kv->prefill_workgroups;
+  t->prefill_whole_units = kv->prefill_whole_units ? 1u : 0u;
+  t->reserved = 0;
   return LMH_OK;
 }
 
@@ -1632,6 +1649,7 @@ int32_t lmh_plan_attend(const lmh_plan_desc* d, const lmh_seg* segs, uint64_t n_
   in.decode_target_items = d->tuning.decode_target_items;
   in.decode_min_tiles = d->tuning.decode_min_tiles;
   in.prefill_workgroups = d->tuning.prefill_workgroups;
+  in.prefill_no_split = d->tuning.prefill_whole_units != 0;
   in.noalloc = d->noalloc != 0;
   in.noalloc_bytes = NOALLOC_SCRATCH_BYTES;
   fill_kernel_facts(in, d->kv_type, d->hd, d->hdv, d->n_head / d->n_kv);

@@ -13,36 +13,58 @@ namespace {
 
 uint64_t key_lo(uint64_t pos, uint64_t window) { return (window > 0 && pos + 1 > window) ? pos + 1 - window : 0; }
 
-// Prefill units grouped per workgroup: prefill_wg_per_cu workgroups per CU, each running a list
-// of units. Longest-processing-time-first: units by decreasing key pages (plus a fixed cost for
-// the unit's Q load and output), each to the currently least loaded workgroup. Lists are padded
-// to the longest with empty units (n_tok = 0) at a fixed stride.
-void assign_prefill_units(std::vector<PrefillItem>& items, uint64_t window, uint32_t slots, uint32_t& n_wg,
-                          uint32_t& per_wg) {
-  n_wg = (uint32_t)std::min<uint64_t>(items.size(), std::max<uint32_t>(slots, 1));
-  per_wg = 0;
-  if (n_wg == 0) return;
-  auto work = [&](const PrefillItem& it) -> uint64_t {
-    const uint64_t last = (uint64_t)it.pos0 + it.n_tok - 1;
-    return last / 16 - key_lo(it.pos0, window) / 16 + 1 + 8;
-  };
-  std::stable_sort(items.begin(), items.end(),
-                   [&](const PrefillItem& a, const PrefillItem& b) { return work(a) > work(b); });
-  std::vector<std::vector<uint32_t>> lists(n_wg);
-  std::priority_queue<std::pair<uint64_t, uint32_t>, std::vector<std::pair<uint64_t, uint32_t>>,
-                      std::greater<std::pair<uint64_t, uint32_t>>> load;
-  for (uint32_t b = 0; b < n_wg; b++) load.push({0, b});
-  for (uint32_t i = 0; i < items.size(); i++) {
+// Prefill cost model, in units of one 64-key tile of a unit with all 256 columns: a tile of a unit
+// with fewer columns costs less (waves without columns only stage tiles), and every unit (or key
+// piece of one) pays a fixed cost for its Q loads and its output (measured on c3 / c5: a full tile
+// 2.2-2.4 us, the per-unit Q load, barrier and stores ~8 us).
+constexpr double PF_UNIT_COST = 3.5;
+double tile_cost(uint32_t n_col) { return 0.35 + 0.65 * std::min(8u, (n_col + 31) / 32) / 8.0; }
+// Key pieces are at least this many 64-key tiles (a unit is cut only when it has twice as many).
+constexpr uint32_t PF_MIN_PIECE = 8;
+// A decode row's 16-key tile for one KV head, in the same units (c2's decode kernel streams 36,864
+// such tiles in ~50 us on 256 CUs, 0.34 CU-us each, at a 2.2-us tile: 0.16; CUs that share HBM
+// with prefill work stream faster each).
+constexpr double DECODE_TILE_COST = 0.1;
+
+struct PfUnit {
+  PrefillItem it;   // page0 / n_pages: the whole unit's key pages
+  uint32_t tiles;
+  double cpt;
+  double cost() const { return tiles * cpt + PF_UNIT_COST; }
+};
+
+// The merge of cut units' pieces, in the same units per (token, query head, piece) partial read
+// (c5's 76,960 such partials of hdv 128 merge in 10.6 us more than its decode rows' merges alone,
+// at a 2.5-us tile), and the merge launch's own cost when no decode rows need one.
+constexpr double PF_MERGE_PARTIAL = 5.6e-5;
+constexpr double PF_MERGE_LAUNCH = 1.5;
+// Cut units only when that is estimated to finish at most this fraction of the whole units' time
+// (the walk's estimate was measured optimistic on c5: 7 tiles gained, 4.7 measured).
+constexpr double PF_CUT_GAIN = 0.9;
+
+// Whole units grouped per workgroup, longest-processing-time-first: units by decreasing cost,
+// each to the currently least loaded workgroup. Returns the largest workgroup load.
+double assign_whole_units(const std::vector<PfUnit>& units, uint32_t slots, std::vector<std::vector<PrefillItem>>& lists) {
+  const uint32_t n_wg = (uint32_t)std::min<uint64_t>(units.size(), std::max<uint32_t>(slots, 1));
+  lists.assign(n_wg, {});
+  std::vector<uint32_t> order(units.size());
+  for (uint32_t i = 0; i < order.size(); i++) order[i] = i;
+  std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return units[a].cost() > units[b].cost(); });
+  std::priority_queue<std::pair<double, uint32_t>, std::vector<std::pair<double, uint32_t>>,
+                      std::greater<std::pair<double, uint32_t>>> load;
+  for (uint32_t b = 0; b < n_wg; b++) load.push({0.0, b});
+  for (uint32_t i : order) {
     auto [l, b] = load.top();
     load.pop();
-    lists[b].push_back(i);
-    load.push({l + work(items[i]), b});
+    lists[b].push_back(units[i].it);
+    load.push({l + units[i].cost(), b});
   }
-  for (const auto& li : lists) per_wg = std::max<uint32_t>(per_wg, (uint32_t)li.size());
-  std::vector<PrefillItem> out((size_t)n_wg * per_wg, PrefillItem{});
-  for (uint32_t b = 0; b < n_wg; b++)
-    for (size_t j = 0; j < lists[b].size(); j++) out[(size_t)b * per_wg + j] = items[lists[b][j]];
-  items.swap(out);
+  double mx = 0.0;
+  while (!load.empty()) {
+    mx = std::max(mx, load.top().first);
+    load.pop();
+  }
+  return mx;
 }
 
 }  // namespace
@@ -64,38 +86,185 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
     return (uint32_t)in.table[seq * in.bps + (((p >> 4) << 4) >> in.bt_shift)];
   };
 
-  // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel
-  // in units of up to unit_cols / group tokens per KV head, balanced over prefill_wg_per_cu
-  // workgroups per CU.
+  // ---- prefill units: segments of at least `pf_min` rows go to the matrix-core prefill kernel.
+  // Per segment and KV head, the (token, query head) columns are packed token-major in units of
+  // unit_cols (a unit may start mid-token, so no unit is a remnant of a few columns); a unit's keys
+  // are the pages from its first token's range start to its last token.
   const uint64_t pf_min = in.prefill_min_rows ? in.prefill_min_rows : DEFAULT_PREFILL_MIN_ROWS;
   const bool pf_ok = in.scale > 0.f && in.layout == LAYOUT_TILES && in.prefill_supported;
   if (pf_ok) {
-    const uint32_t unit_tok = std::max<uint32_t>(in.unit_cols / group, 1);
+    std::vector<PfUnit> units;
     for (uint64_t i = 0; i < in.n_segs; i++) {
       const lmh_seg& sg = in.segs[i];
       if (sg.n < pf_min) continue;
-      for (uint64_t u = 0; u < sg.n; u += unit_tok) {
-        const uint32_t n_tok = (uint32_t)std::min<uint64_t>(unit_tok, sg.n - u);
-        const uint64_t pos0 = sg.pos0 + u, last = pos0 + n_tok - 1;
-        const uint64_t lo = key_lo(pos0, window);
-        o.max_pages = std::max<uint32_t>(o.max_pages, (uint32_t)(last / 16 - lo / 16 + 1));
-        PrefillItem it{(uint32_t)sg.seq, 0, (uint32_t)(sg.start + u), (uint32_t)pos0, n_tok, 0, 0, 0, {}};
-        const uint64_t page0 = lo / 16, n_pages = last / 16 - lo / 16 + 1;
-        for (uint64_t b = 0; b < 8; b++) it.blk[b] = blk_at(sg.seq, (page0 + std::min<uint64_t>(b, n_pages - 1)) << 4);
+      const uint64_t total = sg.n * group;
+      for (uint64_t c0 = 0; c0 < total; c0 += in.unit_cols) {
+        const uint32_t n_col = (uint32_t)std::min<uint64_t>(in.unit_cols, total - c0);
+        const uint64_t t0 = c0 / group, t1 = (c0 + n_col - 1) / group;
+        const uint64_t pos0 = sg.pos0 + t0, last = sg.pos0 + t1;
+        const uint64_t page_lo = key_lo(pos0, window) / 16, n_pages = last / 16 - page_lo + 1;
+        PfUnit u{};
+        u.it.seq = (uint32_t)sg.seq;
+        u.it.row0 = (uint32_t)(sg.start + t0);
+        u.it.pos0 = (uint32_t)pos0;
+        u.it.n_tok = (uint32_t)(t1 - t0 + 1);
+        u.it.c_off = (uint32_t)(c0 % group);
+        u.it.n_col = n_col;
+        u.it.page0 = (uint32_t)page_lo;
+        u.it.n_pages = (uint32_t)n_pages;
+        u.it.slot = NO_SLOT;
+        u.tiles = (uint32_t)((n_pages + 3) / 4);
+        u.cpt = tile_cost(n_col);
         for (uint32_t kvh = 0; kvh < in.n_kv; kvh++) {
-          it.kvh = kvh;
-          o.pitems.push_back(it);
+          u.it.kvh = kvh;
+          units.push_back(u);
         }
       }
       for (uint64_t j = 0; j < sg.n; j++) o.decode_row[sg.start + j] = 0;
     }
-    const uint32_t slots = in.n_cu * in.prefill_wg_per_cu;
-    assign_prefill_units(o.pitems, window,
-                         in.prefill_workgroups ? (uint32_t)std::min<uint64_t>(in.prefill_workgroups, slots) : slots,
-                         o.pf_wg, o.pf_per_wg);
+    // Workgroups for the prefill units. With decode rows in the same launch, the CUs are shared in
+    // proportion to the two kinds' estimated cost (the decode workgroups take the others).
+    uint32_t slots = in.n_cu * in.prefill_wg_per_cu;
+    double w_pf = 0.0;
+    uint32_t max_tiles = 0;
+    double max_cost = 0.0;
+    for (const PfUnit& u : units) {
+      w_pf += u.cost();
+      max_tiles = std::max(max_tiles, u.tiles);
+      max_cost = std::max(max_cost, u.cost());
+    }
+    uint64_t decode_tiles = 0;
+    for (uint64_t t = 0; t < n_rows; t++) {
+      if (!o.decode_row[t]) continue;
+      const uint64_t pos = (uint64_t)in.row_pos[t];
+      decode_tiles += pos / 16 - key_lo(pos, window) / 16 + 1;
+    }
+    if (decode_tiles > 0 && !units.empty() && slots > 1) {
+      const double w_dec = (double)decode_tiles * in.n_kv * head_blocks * DECODE_TILE_COST;
+      const double share = w_pf / (w_pf + w_dec);
+      slots = std::min<uint32_t>(slots - 1, std::max<uint32_t>(1, (uint32_t)(slots * share + 0.5)));
+    }
+    if (in.prefill_workgroups) slots = (uint32_t)std::min<uint64_t>(in.prefill_workgroups, slots);
+    std::vector<std::vector<PrefillItem>> lists;
+    // Whole units (longest first, each to the least loaded workgroup), unless cutting is estimated
+    // to finish well ahead: then the concatenated tiles of all units are cut into one stretch per
+    // workgroup (stream-K), a unit spanning several workgroups running as key pieces that each leave
+    // partials (O, m, l) per column for the merge launch (attend_split's merge,
+    // forward.rs:772-806). A piece's partial slot per token holds the unit's heads of that token:
+    // groups of up to 16 heads, as the decode items'. The cut plan is kept when its largest load
+    // plus the merge's estimate is below PF_CUT_GAIN of the whole units' largest load; a first
+    // bound on its load is the tiles shared evenly with about one more piece per workgroup.
+    const double whole = assign_whole_units(units, slots, lists);
+    double w_cut = 0.0;
+    for (const PfUnit& u : units) w_cut += u.tiles * u.cpt;
+    const double cap = (w_cut + PF_UNIT_COST * ((double)units.size() + slots)) / std::max<uint32_t>(slots, 1);
+    const bool try_cut = !in.prefill_no_split && group <= 16 && !units.empty() && max_tiles >= 2 * PF_MIN_PIECE &&
+                         cap < PF_CUT_GAIN * whole;
+    // a unit's pieces (workgroup, first tile) into the lists; a unit of several pieces gets a
+    // partial slot per (token, piece) and a merge per token
+    auto emit_pieces = [&](const PfUnit& u, const std::vector<std::pair<uint32_t, uint32_t>>& pieces,
+                           std::vector<std::vector<PrefillItem>>& lists) {
+      const uint32_t k = (uint32_t)pieces.size();
+      const uint32_t base = o.slots;
+      if (k > 1) {
+        // merges per token of the unit, over the unit's heads of that token
+        const uint64_t c_abs = u.it.c_off;   // the unit's first column, counted from its first token
+        for (uint32_t i = 0; i < u.it.n_tok; i++) {
+          const uint64_t h_lo = i == 0 ? c_abs : 0;
+          const uint64_t h_hi = std::min<uint64_t>(group, c_abs + u.it.n_col - (uint64_t)i * group);
+          o.merges.push_back(MergeItem{u.it.row0 + i, u.it.kvh, (uint32_t)h_lo, base + i * k, k, (uint32_t)(h_hi - h_lo)});
+        }
+        o.slots += u.it.n_tok * k;
+      }
+      for (uint32_t s = 0; s < k; s++) {
+        const uint32_t a = pieces[s].second, b = s + 1 < k ? pieces[s + 1].second : u.tiles;
+        PrefillItem it = u.it;
+        it.page0 = u.it.page0 + 4 * a;
+        it.n_pages = std::min(u.it.n_pages, 4 * b) - 4 * a;
+        it.slot = k > 1 ? base + s : NO_SLOT;
+        it.slot_stride = k > 1 ? k : 0;
+        lists[pieces[s].first].push_back(it);
+      }
+    };
+    if (try_cut) {
+      // Walk the units' tiles with a capacity per workgroup: a piece fills the current workgroup
+      // (at least PF_MIN_PIECE tiles, and no remainder under PF_MIN_PIECE left behind), the next
+      // piece starts on the next workgroup. The capacity is the smallest (to 1%) whose walk fits
+      // the workgroups with at most PF_MAX_PIECES pieces per unit.
+      std::vector<std::vector<std::pair<uint32_t, uint32_t>>> cuts(units.size());   // (workgroup, first tile)
+      auto walk = [&](double c) -> uint32_t {   // workgroups used (UINT32_MAX: a unit over PF_MAX_PIECES)
+        uint32_t wg = 0;
+        double load = 0.0;
+        for (size_t ui = 0; ui < units.size(); ui++) {
+          const PfUnit& u = units[ui];
+          cuts[ui].clear();
+          uint32_t t = 0;
+          while (t < u.tiles) {
+            if (cuts[ui].size() == PF_MAX_PIECES) return UINT32_MAX;
+            const double avail = c - load - PF_UNIT_COST;
+            if (avail < PF_MIN_PIECE * u.cpt && load > 0.0) {
+              wg++;
+              load = 0.0;
+              continue;
+            }
+            uint32_t take = (uint32_t)std::max<double>(PF_MIN_PIECE, avail / u.cpt);
+            if (take >= u.tiles - t || u.tiles - t - take < PF_MIN_PIECE) take = u.tiles - t;
+            cuts[ui].push_back({wg, t});
+            t += take;
+            load += PF_UNIT_COST + take * u.cpt;
+            if (load >= c - PF_MIN_PIECE * u.cpt) {
+              wg++;
+              load = 0.0;
+            }
+          }
+        }
+        return load > 0.0 ? wg + 1 : wg;
+      };
+      double lo_c = cap, hi_c = std::max(cap, max_cost) * 2.0;
+      while (walk(hi_c) > slots) hi_c *= 2.0;
+      for (int i = 0; i < 30 && hi_c > lo_c * 1.01; i++) {
+        const double mid = 0.5 * (lo_c + hi_c);
+        if (walk(mid) <= slots) hi_c = mid;
+        else lo_c = mid;
+      }
+      const uint32_t n_wg = walk(hi_c);
+      // the cut plan's largest load and its merge estimate
+      std::vector<double> load(n_wg, 0.0);
+      double partials = 0.0;
+      for (size_t ui = 0; ui < units.size(); ui++) {
+        const PfUnit& u = units[ui];
+        const auto& pieces = cuts[ui];
+        for (size_t s = 0; s < pieces.size(); s++) {
+          const uint32_t b = s + 1 < pieces.size() ? pieces[s + 1].second : u.tiles;
+          load[pieces[s].first] += PF_UNIT_COST + (b - pieces[s].second) * u.cpt;
+        }
+        if (pieces.size() > 1) partials += (double)u.it.n_col * pieces.size();
+      }
+      const double merge = partials * PF_MERGE_PARTIAL * (in.hdv + 4) / 132.0 +
+                           (decode_tiles == 0 && partials > 0 ? PF_MERGE_LAUNCH : 0.0);
+      const double cut_load = *std::max_element(load.begin(), load.end()) + merge;
+      if (cut_load < PF_CUT_GAIN * whole) {
+        lists.assign(n_wg, {});
+        for (size_t ui = 0; ui < units.size(); ui++) emit_pieces(units[ui], cuts[ui], lists);
+        while (!lists.empty() && lists.back().empty()) lists.pop_back();
+      }
+    }
+    o.pf_wg = (uint32_t)lists.size();
+    for (const auto& li : lists) o.pf_per_wg = std::max<uint32_t>(o.pf_per_wg, (uint32_t)li.size());
+    o.pitems.assign((size_t)o.pf_wg * o.pf_per_wg, PrefillItem{});
+    for (uint32_t b = 0; b < o.pf_wg; b++) {
+      for (size_t j = 0; j < lists[b].size(); j++) {
+        PrefillItem it = lists[b][j];
+        for (uint32_t i = 0; i < 8; i++) it.blk[i] = blk_at(it.seq, (uint64_t)(it.page0 + std::min(i, it.n_pages - 1)) << 4);
+        o.max_pages = std::max(o.max_pages, it.n_pages);
+        o.pitems[(size_t)b * o.pf_per_wg + j] = it;
+      }
+    }
     if (in.prefill_lds_fixed + (size_t)o.pf_per_wg * sizeof(PrefillItem) + (size_t)o.max_pages * 4 > in.lds_limit) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
       o.pitems.clear();
+      o.merges.clear();
+      o.slots = 0;
       std::fill(o.decode_row.begin(), o.decode_row.end(), 1);
       o.max_pages = 0;
       o.pf_wg = o.pf_per_wg = 0;
@@ -190,7 +359,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
           o.items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, seq, blk_at(seq, lo)});
           continue;
         }
-        o.merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, o.slots, (uint32_t)n_split, 0});
+        o.merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, o.slots, (uint32_t)n_split, 0});   // nh 0: ng heads
         for (uint64_t s = 0; s < n_split; s++) {
           const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
           const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);

@@ -35,6 +35,7 @@ struct PlanIn {
   uint64_t decode_capacity = 1;     // decode items the layer's decode kernel holds at once
   // lmh_attend_tuning (0: the default)
   uint64_t prefill_min_rows = 0, decode_target_items = 0, decode_min_tiles = 0, prefill_workgroups = 0;
+  bool prefill_no_split = false;    // units are never cut into key pieces
   // lmh_attend_noalloc: split slots and merges bounded by the scratch
   bool noalloc = false;
   size_t noalloc_bytes = 0;

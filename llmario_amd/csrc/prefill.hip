@@ -138,7 +138,8 @@ __device__ inline uint4 i8x8_to_bf8(uint32_t a, uint32_t b) {
 // to f16, the precision of the Metal sibling's prefill.
 template <int KVT, int HD, bool PLO>
 __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items,
-                                           uint32_t per_wg, const float* q, float* out, uint32_t wg) {
+                                           uint32_t per_wg, const float* q, float* out, uint32_t wg,
+                                           const MergeCopy& mc) {
   constexpr int NC = HD / 32;                 // Q.K chunks of 32 dims
   constexpr int NJ = HD / 16;                 // O^T blocks of 16 dims
   constexpr int TILE = 16 * HD * 2;           // bytes of one 16-token page tile (K or V) in LDS
@@ -153,6 +154,9 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   PrefillItem* units = (PrefillItem*)(smem + NSTAGE * STAGE);      // this workgroup's unit list
   int* blk_lds = (int*)(units + per_wg);                           // block id of each key page in range
 
+  // The first workgroup copies the call's merge list (units that are key pieces of a longer range
+  // leave partials for the merge launch that follows).
+  dtile::copy_merges(mc, wg == 0);
   // The workgroup's units (the host's balanced assignment, per_wg slots, an empty unit ends the
   // list): fetched once, so each unit starts without a memory round trip for its descriptor.
   {
@@ -171,9 +175,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   const uint32_t hq = lane & 15u, grp = lane >> 4;
   const uint32_t G = pg.group;
   const uint32_t pos_last = it.pos0 + it.n_tok - 1;
-  const uint32_t lo_first = (pg.window > 0 && it.pos0 + 1 > pg.window) ? it.pos0 + 1 - pg.window : 0;
-  const uint32_t page0 = lo_first >> 4, page1 = pos_last >> 4;
-  const uint32_t n_pages = page1 - page0 + 1;
+  const uint32_t page0 = it.page0, n_pages = it.n_pages;   // the unit's key pages
+  const uint32_t c_off = it.c_off, n_col = it.n_col;
 
   // ---- K/V staging. Tile i covers keys (page0 + 4i)*16 .. +64: 4 K and 4 V page tiles, each
   // R rows of 1 KiB (one wave-wide DMA per row). Every wave issues 2*CPT DMAs per tile, so its
@@ -375,8 +378,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // second column block's registers holding the first's lo part (same registers, same products
   // per pass, twice the passes).
   auto load_q = [&](uint32_t c, float4 (&raw)[NC][2]) {
-    const uint32_t t = c / G, hh = c % G;
-    const bool valid = t < it.n_tok;
+    const uint32_t t = (c + c_off) / G, hh = (c + c_off) % G;
+    const bool valid = c < n_col;
     const float* qp = q + ((size_t)(it.row0 + (valid ? t : 0)) * pg.n_head + it.kvh * G + hh) * HD;
 #pragma unroll
     for (int ch = 0; ch < NC; ch++) {
@@ -477,8 +480,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
   for (int x = 0; x < NX; x++) {
     const uint32_t c = w * COLS + (LO ? pb : x) * 16 + hq;
-    const uint32_t t = c / G;
-    cval[x] = t < it.n_tok;
+    const uint32_t t = (c + c_off) / G;
+    cval[x] = c < n_col;
     cpos[x] = it.pos0 + (cval[x] ? t : 0);
     clo[x] = (pg.window > 0 && cpos[x] + 1 > pg.window) ? cpos[x] + 1 - pg.window : 0;
   }
@@ -504,12 +507,12 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   }
   // this wave's lowest/highest column positions in the pass (mask-free tiles)
   const uint32_t c_first = w * COLS + (LO ? pb * 16 : 0), c_span = LO ? 16 : COLS;
-  const bool wave_active = c_first / G < it.n_tok;
+  const bool wave_active = c_first < n_col;
   uint32_t wpos_min, wpos_max;
   {
-    const uint32_t t0 = c_first / G, tl = (c_first + c_span - 1) / G;
-    const uint32_t t1 = tl < it.n_tok ? tl : it.n_tok - 1;
-    wpos_min = it.pos0 + (t0 < it.n_tok ? t0 : t1);
+    const uint32_t c_last = min(c_first + c_span, n_col) - 1;   // n_col >= 1
+    const uint32_t t1 = (c_last + c_off) / G;
+    wpos_min = it.pos0 + min((c_first + c_off) / G, t1);
     wpos_max = it.pos0 + t1;
   }
   const uint32_t wlo_max = (pg.window > 0 && wpos_max + 1 > pg.window) ? wpos_max + 1 - pg.window : 0;
@@ -825,13 +828,25 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     }
   }
 
-  // ---- epilogue: per column, out = O / l (l summed over the lane groups)
+  // ---- epilogue: per column, out = O / l (l summed over the lane groups); a key piece of a longer
+  // range leaves its partial (O, m, l) instead, m as the log2-domain reference its weights were
+  // taken against (c2 (s - m_raw) + PUP = c2 s - (c2 m_raw - PUP)), -inf if no key was visible
 #pragma unroll
   for (int x = 0; x < NX; x++) {
     const float lt = sum_over_groups(l[x]);
     if (!cval[x]) continue;
     const uint32_t col = w * COLS + (LO ? pb : x) * 16 + hq;
-    const uint32_t t = col / G, hh = col % G;
+    const uint32_t t = (col + c_off) / G, hh = (col + c_off) % G;
+    if (it.slot != NO_SLOT) {
+      float* pp = pg.part + ((size_t)(it.slot + t * it.slot_stride) * pg.ng + (hh - (t == 0 ? c_off : 0))) * (HD + 4);
+#pragma unroll
+      for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][x][0], O[j][x][1], O[j][x][2], O[j][x][3]);
+      if (grp == 0) {
+        pp[HD] = thr[x] == -INFINITY ? -INFINITY : -nm[x] * c2 - PUP;
+        pp[HD + 1] = lt;
+      }
+      continue;
+    }
     const float inv = lt > 0.f ? 1.0f / lt : 0.f;
     float* op = out + ((size_t)(it.row0 + t) * pg.n_head + it.kvh * G + hh) * HD;
 #pragma unroll
@@ -858,8 +873,8 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 template <int KVT, int HD, bool PLO>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32_t per_wg, const float* q,
-                    float* out) {
-  prefill_wg<KVT, HD, PLO>(g, pg, items, per_wg, q, out, blockIdx.x);
+                    float* out, MergeCopy mc) {
+  prefill_wg<KVT, HD, PLO>(g, pg, items, per_wg, q, out, blockIdx.x, mc);
 }
 
 // A mixed batch (prefill units and decode items) in one launch: workgroups 0 .. pf_wg-1 run the
@@ -873,8 +888,8 @@ template <int KVT, int HD, bool PLO>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_t per_wg, uint32_t pf_wg, RowGeom r,
                   const DecodeItem* items, uint32_t n_items, const float* q, float* out, float* part, MergeCopy mc) {
-  if (blockIdx.x < pf_wg) {
-    prefill_wg<KVT, HD, PLO>(g, pg, pitems, per_wg, q, out, blockIdx.x);
+  if (blockIdx.x < pf_wg) {   // the decode workgroups copy the merge list
+    prefill_wg<KVT, HD, PLO>(g, pg, pitems, per_wg, q, out, blockIdx.x, MergeCopy{nullptr, nullptr, 0});
     return;
   }
   const uint32_t b = blockIdx.x - pf_wg;
@@ -885,17 +900,18 @@ void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_
 
 template <int KVT, int HD>
 hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
-                    uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s, const LaunchEv& ev) {
+                    uint32_t per_wg, uint32_t max_pages, const float* q, float* out, const MergeCopy& mc, hipStream_t s,
+                    const LaunchEv& ev) {
   const uint32_t lds = (uint32_t)prefill_lds_bytes(KVT, HD, max_pages, per_wg);
   // q8_0 has one instance: its scaled weights are always carried as hi + lo (prefill_p_f16 applies to
   // 16-bit pages)
   if constexpr (KVT != KV_Q8) {
     if (pg.p_f16) {
-      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
       return hipGetLastError();
     }
   }
-  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out);
+  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
   return hipGetLastError();
 }
 
@@ -951,18 +967,18 @@ hipError_t launch_mixed(const PageGeom& g, const PrefillGeom& pg, const PrefillI
 }
 
 hipError_t launch_prefill(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items, uint32_t n_wg,
-                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, hipStream_t s,
-                          const LaunchEv& ev) {
+                          uint32_t per_wg, uint32_t max_pages, const float* q, float* out, const MergeCopy& mc,
+                          hipStream_t s, const LaunchEv& ev) {
   if (n_wg == 0 || per_wg == 0) return hipSuccess;
   if (g.kv_type == KV_BF16) {
-    if (g.hd == 128) return launch_t<KV_BF16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
-    if (g.hd == 64) return launch_t<KV_BF16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+    if (g.hd == 128) return launch_t<KV_BF16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, mc, s, ev);
+    if (g.hd == 64) return launch_t<KV_BF16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, mc, s, ev);
   } else if (g.kv_type == KV_F16) {
-    if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
-    if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+    if (g.hd == 128) return launch_t<KV_F16, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, mc, s, ev);
+    if (g.hd == 64) return launch_t<KV_F16, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, mc, s, ev);
   } else if (g.kv_type == KV_Q8) {
-    if (g.hd == 128) return launch_t<KV_Q8, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
-    if (g.hd == 64) return launch_t<KV_Q8, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, s, ev);
+    if (g.hd == 128) return launch_t<KV_Q8, 128>(g, pg, items, n_wg, per_wg, max_pages, q, out, mc, s, ev);
+    if (g.hd == 64) return launch_t<KV_Q8, 64>(g, pg, items, n_wg, per_wg, max_pages, q, out, mc, s, ev);
   }
   return hipErrorInvalidValue;
 }

@@ -29,27 +29,41 @@ constexpr uint32_t LOCAL_SLOT = 0x80000000u;
 constexpr uint32_t LOCAL_MERGE_MAX = 1024;   // heads x hdv of an item whose partials a wave keeps in LDS
 constexpr int LOCAL_WAVES = 8;               // waves per workgroup of a local-merge call (its largest group)
 
-// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, h0..).
+// Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, heads h0 ..
+// h0 + nh - 1; nh = 0: up to the item's head count ng). Head h0 + i sits at position i of a slot.
 struct MergeItem {
   uint32_t row;
   uint32_t kvh;
   uint32_t h0;
   uint32_t slot0;
   uint32_t n_split;
-  uint32_t pad;
+  uint32_t nh;
 };
+// A prompt token's merge (nh != 0) combines at most this many key pieces (the merge folds each
+// head's pieces within one wave); such merges precede the decode merges in a call's list.
+constexpr uint32_t PF_MAX_PIECES = 64;
 
-// One prefill work unit: KV head `kvh` of sequence `seq`, tokens at positions pos0 .. pos0+n_tok-1
-// which are stacked rows row0 .. row0+n_tok-1 (n_tok * group <= prefill_cols_per_unit()).
-// blk: the block ids of the unit's first 8 key pages (page i of its key range, clamped to the last
-// page), so the first K/V tiles are fetched without waiting for the block table.
+// One prefill work unit: KV head `kvh` of sequence `seq`. Its columns are the (token, query head)
+// pairs of the stacked rows row0, row0 + 1, .. (positions pos0, pos0 + 1, ..) flattened
+// token-major from head c_off of the first token: column c < n_col is token (c + c_off) / group,
+// head (c + c_off) % group (n_col <= prefill_cols_per_unit(); n_tok = the tokens the columns
+// touch). Its keys are pages page0 .. page0 + n_pages - 1 of the sequence (16 positions each),
+// within each column's own range (causal, window). slot = NO_SLOT: those pages are the columns'
+// whole ranges and the unit writes the output. Otherwise the unit is one key piece of a longer
+// range: column (t, h)'s partial (o, m, l) goes to slot `slot + t * slot_stride`, at position
+// h - (t == 0 ? c_off : 0), and a merge launch combines the pieces.
+// blk: the block ids of pages page0 .. page0 + 7 (clamped to the last page), so the first K/V
+// tiles are fetched without waiting for the block table.
 struct PrefillItem {
   uint32_t seq;
   uint32_t kvh;
   uint32_t row0;
   uint32_t pos0;
   uint32_t n_tok;
-  uint32_t pad0, pad1, pad2;
+  uint32_t c_off, n_col;
+  uint32_t page0, n_pages;
+  uint32_t slot, slot_stride;
+  uint32_t pad;
   uint32_t blk[8];
 };
 

@@ -16,6 +16,7 @@ from llmario_amd import harness
 from llmario_amd.kv import HipKvCache, KvFull, Layer
 from llmario_amd.workloads import Generator, config, small
 from golden_io import load as load_golden, names as golden_names
+from test_plan import SPLIT
 
 pytestmark = pytest.mark.gpu
 
@@ -250,6 +251,27 @@ def test_prefill_units_stream_through_few_workgroups(cuda, kv, layer, prior, new
     err = row_rel_err(got, ref)
     print(f"{kv} {layer} prior={prior} new={new} window={window} bt={bt} q={q_kind} wgs={wgs}: {err:.3e}")
     assert err <= TOL[kv], err
+
+
+# Long prompt units cut into key pieces across workgroups (their partials merged per token), in
+# the geometries the planner's CPU test shows cut: checked against the oracle, with the same call
+# planned as whole units beside it.
+@pytest.mark.parametrize("kv,geo,prior,new,window,bt", SPLIT)
+@pytest.mark.parametrize("q_kind", ["rounded", "f32"])
+def test_prefill_key_pieces(cuda, kv, geo, prior, new, window, bt, q_kind):
+    w = small("k", kv, Layer(*geo), prior, new, window=window, seed=53, block_tokens=bt)
+    hc, oc, q = pair(w)
+    if q_kind == "f32":   # bits below f16 / bf16: the two-pass path
+        q = np.random.default_rng(9).standard_normal(q.shape).astype(np.float32)
+    got = run_gpu(hc, w, q)
+    hc.set_tuning(prefill_whole_units=True)
+    whole = run_gpu(hc, w, q)
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    assert np.isfinite(got).all() and np.isfinite(whole).all()
+    err, err_w = row_rel_err(got, ref), row_rel_err(whole, ref)
+    print(f"{kv} {geo} prior={prior} new={new} window={window} bt={bt} q={q_kind}: pieces {err:.3e}, "
+          f"whole units {err_w:.3e}")
+    assert err <= TOL[kv] and err_w <= TOL[kv], (err, err_w)
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c4"])

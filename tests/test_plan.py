@@ -26,7 +26,7 @@ def plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window=0, scale=0.1, n_cu=2
     tab = np.ascontiguousarray(table, dtype=np.int32)
     t = N.AttendTuning(N.ABI_VERSION, int(tuning.get("prefill_p_f16", 0)), int(tuning.get("prefill_min_rows", 0)),
                        int(tuning.get("decode_target_items", 0)), int(tuning.get("decode_min_tiles", 0)),
-                       int(tuning.get("prefill_workgroups", 0)))
+                       int(tuning.get("prefill_workgroups", 0)), int(tuning.get("prefill_whole_units", 0)), 0)
     d = N.PlanDesc(N.ABI_VERSION, KV[kv], n_head, n_kv, hd, hdv, bt, n_cu, capacity, n_seqs, bps,
                    tab.ctypes.data_as(C.c_void_p), window, scale, 1 if noalloc else 0, t)
     arr = (N.Seg * max(len(segs), 1))(*[N.Seg(*s) for s in segs])
@@ -107,12 +107,15 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
                 idx, n = (slot >> 8) & 0x7F, slot & 0xFF
                 first = i - idx
                 assert first // 8 == (first + n - 1) // 8
+    dec_merges = set()
     for m in merges:
-        row, kvh, h0, slot0, n_split = (int(x) for x in m[:5])
-        parts = by_key[(row, kvh, h0)]
-        assert n_split == len(parts) > 1
-        assert sorted(p[2] for p in parts) == list(range(slot0, slot0 + n_split))
-    assert len(merges) == sum(1 for p in by_key.values() if len(p) > 1) or c.local
+        row, kvh, h0, slot0, n_split, nh = (int(x) for x in m[:6])
+        if (row, kvh, h0) in by_key and nh == 0:   # a decode row's merge
+            parts = by_key[(row, kvh, h0)]
+            assert n_split == len(parts) > 1
+            assert sorted(p[2] for p in parts) == list(range(slot0, slot0 + n_split))
+            dec_merges.add((row, kvh, h0))
+    assert len(dec_merges) == sum(1 for p in by_key.values() if len(p) > 1) or c.local
     if noalloc and c.slots:
         # the split target is capped to what the no-allocation scratch holds; a call whose rows
         # still need more (chunks at their 64-tile maximum) is refused by lmh_attend_noalloc
@@ -125,19 +128,50 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
         lst = units[wgi * c.pf_per_wg:(wgi + 1) * c.pf_per_wg]
         live = [int(u[4]) != 0 for u in lst]
         assert live == sorted(live, reverse=True) and live[0]
+    # each unit (or key piece of one): packed columns, its pages, block ids; a column's pieces
+    # partition its unit's key pages on 64-key tile boundaries and write distinct partial slots of
+    # the column's merge
+    pieces = {}
     for u in units:
-        seq, kvh, row0, pos0, n_tok = (int(x) for x in u[:5])
+        seq, kvh, row0, pos0, n_tok, c_off, n_col, page0, n_pages, slot, stride = (int(x) for x in u[:11])
         if n_tok == 0:
             continue
-        assert kvh < n_kv and n_tok * group <= unit_cols
-        for i in range(n_tok):
-            assert rows[row0 + i] == (seq, pos0 + i)
-            covered[row0 + i, kvh * group:(kvh + 1) * group] += 1
-        lo, last = key_lo(pos0, window), pos0 + n_tok - 1
-        page0, n_pages = lo // 16, last // 16 - lo // 16 + 1
+        assert kvh < n_kv and 0 < n_col <= unit_cols and c_off < group and n_pages >= 1
+        assert (c_off + n_col - 1) // group == n_tok - 1
         assert n_pages <= c.max_pages
         for b in range(8):
-            assert int(u[8 + b]) == blk(seq, (page0 + min(b, n_pages - 1)) * 16)
+            assert int(u[12 + b]) == blk(seq, (page0 + min(b, n_pages - 1)) * 16)
+        for col in range(n_col):
+            t, h = (col + c_off) // group, (col + c_off) % group
+            assert rows[row0 + t] == (seq, pos0 + t)
+            key = (row0 + t, kvh * group + h)
+            ps = pieces.setdefault(key, [])
+            ps.append((page0, n_pages, slot if slot == NO_SLOT else slot + t * stride, h - (c_off if t == 0 else 0)))
+    # prompt-token merges (nh != 0) come first, each over at most 64 pieces
+    nh_col = [int(m[5]) for m in merges]
+    n_pf = sum(1 for x in nh_col if x)
+    assert all(nh_col[:n_pf]) and not any(nh_col[n_pf:])
+    assert all(int(m[4]) <= 64 for m in merges[:n_pf])
+    merge_of = {}
+    for m in merges:
+        row, kvh, h0, slot0, n_split, nh = (int(x) for x in m[:6])
+        if nh:
+            for h in range(h0, h0 + nh):
+                merge_of[(row, kvh * group + h)] = (slot0, n_split, h0)
+    for (row, head), ps in pieces.items():
+        s_, pos = rows[row]
+        ps.sort()
+        lo, last = key_lo(pos, window), pos
+        assert ps[0][0] * 16 <= lo and (ps[-1][0] + ps[-1][1]) * 16 > last
+        for x, y in zip(ps, ps[1:]):
+            assert x[0] + x[1] == y[0] and (y[0] - ps[0][0]) % 4 == 0
+        if len(ps) == 1:
+            assert ps[0][2] == NO_SLOT and (row, head) not in merge_of
+        else:
+            slot0, n_split, h0 = merge_of[(row, head)]
+            assert n_split == len(ps) and sorted(p[2] for p in ps) == list(range(slot0, slot0 + n_split))
+            assert all(p[3] == head % group - h0 for p in ps)
+        covered[row, head] += 1
     assert (covered == 1).all(), np.argwhere(covered != 1)[:5]
 
 
@@ -212,6 +246,50 @@ def test_configuration_shapes():
             assert len(items) > 0 and live_units > 0
         if name == "c2":
             assert live_units == 0 and len(merges) > 0
+
+
+# Few long prompt units on many CUs: their key ranges are cut into pieces (stream-K), whose
+# partials the merge kernel combines per token. Geometries: a prefix with decode rows beside,
+# bf16 on 32-token blocks, q8_0, a window (ranges past page 0), group 1, group 16, and a prompt
+# without a prefix (pieces past a token's diagonal are fully masked for it).
+SPLIT = [
+    ("f16", (40, 8, 128, 128), [4095, 300, 2000], [64, 1, 1], 0, 16),
+    ("bf16", (32, 8, 128, 128), [3000], [40], 0, 32),
+    ("q8_0", (32, 8, 128, 128), [2500, 100], [48, 1], 0, 16),
+    ("f16", (16, 2, 64, 64), [5000], [100], 1500, 16),
+    ("bf16", (8, 8, 128, 128), [2000], [30], 0, 64),
+    ("f16", (64, 4, 128, 128), [1800], [20], 0, 16),
+    ("bf16", (8, 8, 128, 128), [0], [2000], 0, 16),
+    ("q8_0", (8, 2, 64, 64), [3000, 50], [9, 1], 0, 64),
+]
+
+
+def contiguous_table(totals, bt):
+    bps = max((t + bt - 1) // bt for t in totals)
+    table = np.full((len(totals), bps), -1, np.int64)
+    k = 0
+    for s, t in enumerate(totals):
+        nb = (t + bt - 1) // bt
+        table[s, :nb] = np.arange(k, k + nb)
+        k += nb
+    return table
+
+
+@pytest.mark.parametrize("kv,geo,prior,new,window,bt", SPLIT)
+def test_long_units_are_cut_into_key_pieces(kv, geo, prior, new, window, bt):
+    n_head, n_kv, hd, hdv = geo
+    segs, start = [], 0
+    for s, (p, n) in enumerate(zip(prior, new)):
+        segs.append((s, start, n, p))
+        start += n
+    table = contiguous_table([p + n for p, n in zip(prior, new)], bt)
+    items, merges, units, c = plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window=window)
+    check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges, units, c)
+    live = units[units[:, 4] != 0]
+    assert (live[:, 9] != NO_SLOT).any()                  # some units were cut
+    _, _, units_w, c_w = plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window=window, prefill_whole_units=1)
+    live_w = units_w[units_w[:, 4] != 0]
+    assert (live_w[:, 9] == NO_SLOT).all() and len(live) > len(live_w)
 
 
 def test_invalid_calls_are_refused():
