@@ -17,7 +17,8 @@ headline line still prints): every other configuration's throughput and its laun
 parts of a mixed launch), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), c3's
 prompts on q8_0 pages (`c3_q8`; `c3_q8_rows`: the same with every row sent to the decode kernels), c3
 with Q keeping all f32 bits (`c3_q_f32`: the prefill's two-pass path; every other leg's Q is rounded
-to the cache's 16-bit type), the
+to the cache's 16-bit type), a 64-token prompt chunk on a 32k prefix with its prefill units cut into
+key pieces across the device (`chunk32k`) and kept whole (`chunk32k_whole`), the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
 of a c4 sequence (`snapshot_c4`), a scheduler-driven serving loop on c5's mix (`sched_c5`), c5w
 with its layer in the sliding-window pool (`window_c5w`), and the CPU baseline (the C++
@@ -540,8 +541,8 @@ def main():
     # ~0.2 s of c2 steps: the clock needs tens of milliseconds of load to settle (10 warm-up steps
     # left the cold decode kernel at 52.7 us against 50.3 us settled)
     ap.add_argument("--warmup", type=int, default=3000)
-    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c5,c5w,rope_c3,snapshot_c4,"
-                                       "sched_c5,window_c5w",
+    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c5,c5w,chunk32k,chunk32k_whole,"
+                                       "rope_c3,snapshot_c4,sched_c5,window_c5w",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline budget (c2 on all threads and on 1, c1 on both)")
@@ -551,7 +552,7 @@ def main():
                     help="minimum warm-up time of the headline and of each extra configuration (clock ramp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-config", default="",
-                    help="only time this one config (c1..c5, c5w) and print its result dict: the "
+                    help="only time this one config (c1..c5, c5w, chunk32k; suffixes _q_f32, _p_f16, _rows, _whole) and print its result dict: the "
                          "command the rocprofv3 summaries under profiles/ were taken with")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (20 launches): the known-size "
@@ -596,6 +597,8 @@ def main():
             name, tuning = name[:-len("_p_f16")], {"prefill_p_f16": True}
         elif name.endswith("_rows"):
             name, tuning = name[:-len("_rows")], {"prefill_min_rows": 1 << 32}
+        elif name.endswith("_whole"):
+            name, tuning = name[:-len("_whole")], {"prefill_whole_units": True}
         q_f32 = name.endswith("_q_f32")
         name = name[:-len("_q_f32")] if q_f32 else name
         res = time_config(name, args.steps, args.warmup, warmup_s=args.extra_warmup_s, n_layers=layers,
@@ -626,6 +629,10 @@ def main():
         # c3_q8 on the matrix-core prefill
         "c3_q8_rows": lambda: time_config("c3_q8", max(3, short // 4), 1, warmup_s=args.extra_warmup_s,
                                           tuning={"prefill_min_rows": 1 << 32}, label="c3_q8_rows"),
+        # the long-prefix chunk with its units kept whole (one workgroup per unit), beside chunk32k
+        # (units cut into key pieces across the device, partials merged)
+        "chunk32k_whole": lambda: time_config("chunk32k", short, 3, warmup_s=args.extra_warmup_s,
+                                              tuning={"prefill_whole_units": True}, label="chunk32k_whole"),
         # c3 with Q keeping all f32 bits (the prefill's two passes: Q as f16 hi + lo)
         "c3_q_f32": lambda: time_config("c3", short, 3, warmup_s=args.extra_warmup_s, q_f32=True,
                                         label="c3_q_f32"),

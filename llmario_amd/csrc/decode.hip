@@ -50,25 +50,24 @@ constexpr int waves_per_eu() {
 }
 
 // A prompt token's merge (MergeItem.nh != 0: the key pieces of a cut prefill unit), one wave per
-// item over its heads [h0, h0 + nh): row j of a chunk of heads is (head j / k, piece j % k) of the
-// item's k <= 64 partials (piece s in slot slot0 + s, head at position h). Lane j holds row j's
-// (m, l) and turns them into 2^(m - M_h) and 1 / L_h of its head; every lane then folds the
-// chunk's rows (16 loads in flight) into its NP dims, storing a head after its last piece. One
-// wave carries every head and piece of the token, so the few bytes of each merge are fetched in
-// one round trip instead of one per head.
+// item: heads h0 .. h0 + nh - 1 of its KV group, each the merge of the n_split = k piece partials
+// in slots slot0 .. slot0 + k - 1 (head h at position h of a slot). Row j = (head j / k, piece
+// j % k) of the item's nh * k <= 64 rows: lane j holds row j's (m, l) and turns them into
+// 2^(m - M_h) and 1 / L_h of its head; every lane then folds the rows, PF_MERGE_ROWS loads in
+// flight at once (the planner keeps nh * k within that, or nh = 1), into its NP dims, storing a head
+// after its last piece. Prompt merges exist only for hdv <= 128 (NP <= 2).
 template <int NP>
 __device__ void merge_heads(const RowGeom& r, uint32_t hdv, const MergeItem& mi, const float* part, float* out,
                             uint32_t lane) {
-  const uint32_t k = mi.n_split;
-  const size_t hstride = hdv + 4, stride = (size_t)r.ng * hstride;
-  const float* base = part + (size_t)mi.slot0 * stride;
-  const uint32_t hpc = 64u / k;   // heads per chunk
-  for (uint32_t hc = 0; hc < mi.nh; hc += hpc) {
-    const uint32_t nrow = (mi.nh - hc < hpc ? mi.nh - hc : hpc) * k;
+  if constexpr (NP <= 2) {
+    constexpr int RB = (int)PF_MERGE_ROWS;
+    const uint32_t k = mi.n_split, nrow = mi.nh * k;
+    const size_t hstride = hdv + 4, stride = (size_t)r.ng * hstride;
+    const float* base = part + (size_t)mi.slot0 * stride + (size_t)mi.h0 * hstride;
     const uint32_t jh = lane / k, first = jh * k;
     float m = -INFINITY, l = 0.f;
     if (lane < nrow) {
-      const float* pr = base + (size_t)(lane - first) * stride + (size_t)(hc + jh) * hstride + hdv;
+      const float* pr = base + (size_t)(lane - first) * stride + (size_t)jh * hstride + hdv;
       m = pr[0];   // separate loads: (m, l) are 8-byte aligned only for even hdv
       l = pr[1];
     }
@@ -82,30 +81,38 @@ __device__ void merge_heads(const RowGeom& r, uint32_t hdv, const MergeItem& mi,
     float acc[NP];
 #pragma unroll
     for (int i = 0; i < NP; i++) acc[i] = 0.f;
-    for (uint32_t j0 = 0; j0 < nrow; j0 += 16) {
-      float pre[16][NP];
+    // (head, piece) of row j0 + t, advanced row by row (scalar: no division in the loops)
+    uint32_t h_at = 0, s_at = 0;
+    for (uint32_t j0 = 0; j0 < nrow; j0 += RB) {
+      float pre[RB][NP];
+      uint32_t h = h_at, sp = s_at;
 #pragma unroll
-      for (int t = 0; t < 16; t++) {
-        const uint32_t j = j0 + t;
-        const float* pp = base + (size_t)(j % k) * stride + (size_t)(hc + j / k) * hstride + lane * NP;
+      for (int t = 0; t < RB; t++) {
+        const float* pp = base + (size_t)sp * stride + (size_t)h * hstride + lane * NP;
 #pragma unroll
-        for (int i = 0; i < NP; i++) pre[t][i] = j < nrow && lane * NP + i < hdv ? pp[i] : 0.f;
+        for (int i = 0; i < NP; i++) pre[t][i] = j0 + t < nrow && lane * NP + i < hdv ? pp[i] : 0.f;
+        if (++sp == k) {
+          sp = 0;
+          h++;
+        }
       }
 #pragma unroll
-      for (int t = 0; t < 16; t++) {
+      for (int t = 0; t < RB; t++) {
         const uint32_t j = j0 + t;
         if (j < nrow) {
           const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), (int)j));
 #pragma unroll
           for (int i = 0; i < NP; i++) acc[i] += cj * pre[t][i];
-          if (j % k == k - 1) {
+          if (++s_at == k) {
             const float iv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), (int)j));
-            float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + hc + j / k) * hdv + lane * NP;
+            float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h_at) * hdv + lane * NP;
 #pragma unroll
             for (int i = 0; i < NP; i++) {
               if (lane * NP + i < hdv) op[i] = acc[i] * iv;
               acc[i] = 0.f;
             }
+            s_at = 0;
+            h_at++;
           }
         }
       }
@@ -222,7 +229,7 @@ __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(wave
 void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q, float* out,
                         float* part, MergeCopy mc) {
   const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
-  copy_merges(mc, blockIdx.x == 0);
+  copy_merges(mc, blockIdx.x, gridDim.x);
   if (wi < n_items) decode_item<KVT, HD, HDV>(g, r, items, wi, q, out, part);
 }
 
@@ -249,7 +256,7 @@ __global__ __launch_bounds__(64 * W) void decode_f32_kernel(PageGeom g, RowGeom 
   __shared__ float lp[W][LPN];   // local merge: each wave's partials
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t wi = blockIdx.x * W + w;
-  copy_merges(mc, blockIdx.x == 0);
+  copy_merges(mc, blockIdx.x, gridDim.x);
   const bool active = wi < n_items;
   // local merge: every wave reaches the workgroup barrier before the merge, active or not
   const bool local = LPN > 1 && r.local_merge != 0;
@@ -473,7 +480,7 @@ __global__ __launch_bounds__(64 * WAVES) void decode_rows_kernel(PageGeom g, Row
   __shared__ float ps[WAVES][RNG][64];
   const uint32_t lane = threadIdx.x & 63u, w = threadIdx.x >> 6;
   const uint32_t wi = blockIdx.x * WAVES + w;
-  copy_merges(mc, blockIdx.x == 0);
+  copy_merges(mc, blockIdx.x, gridDim.x);
   if (wi >= n_items) return;   // no block-wide barrier below: each wave works alone
   const DecodeItem it = items[wi];
   const uint32_t hd = g.hd, hdv = g.hdv;

@@ -150,12 +150,15 @@ __device__ inline float scale_at(const uint4* s, int r, int c) {
   return h_to_f((uint16_t)((idx & 1) ? (w >> 16) : (w & 0xffff)));
 }
 
-// The first workgroup of a decode launch copies the call's merge list from the staged (host-mapped)
-// work list into device memory, beside its own work: the merge kernel that follows then starts
-// from device memory instead of a round trip over the bus.
-__device__ inline void copy_merges(const MergeCopy& mc, bool first_block) {
-  if (!first_block) return;
-  for (uint32_t i = threadIdx.x; i < mc.n_words; i += blockDim.x) mc.dst[i] = mc.src[i];
+// The workgroups of a decode, prefill or mixed launch copy the call's merge list from the staged
+// (host-mapped) work list into device memory beside their own work, a slice each (a word per
+// thread for up to block x grid words): the merge kernel that follows then starts from device
+// memory instead of a round trip over the bus, and no workgroup spends more than one bus round
+// trip on it (a list of thousands of prompt merges copied by one workgroup held that workgroup
+// back by tens of microseconds).
+__device__ inline void copy_merges(const MergeCopy& mc, uint32_t block, uint32_t n_blocks) {
+  const uint32_t stride = n_blocks * blockDim.x;
+  for (uint32_t i = block * blockDim.x + threadIdx.x; i < mc.n_words; i += stride) mc.dst[i] = mc.src[i];
 }
 
 // One decode work item, items[wi], computed by the calling wave: the partial (o, m, l) to

@@ -1535,7 +1535,8 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
     uint32_t max_split = 0, n_pf = 0;
     for (const MergeItem& m : kv->plan.merges) {
       if (m.nh != 0) {
-        if (n_pf != (uint32_t)(&m - kv->plan.merges.data()) || m.n_split > PF_MAX_PIECES)
+        if (n_pf != (uint32_t)(&m - kv->plan.merges.data()) || m.n_split > PF_MAX_PIECES ||
+            (m.nh > 1 && m.nh * m.n_split > PF_MERGE_ROWS) || y.hdv > 128)
           return kv->fail(LMH_UNSUPPORTED, "attend: the planner's prompt merges are out of order or too long");
         n_pf++;
       } else {

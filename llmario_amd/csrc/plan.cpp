@@ -20,7 +20,10 @@ uint64_t key_lo(uint64_t pos, uint64_t window) { return (window > 0 && pos + 1 >
 constexpr double PF_UNIT_COST = 3.5;
 double tile_cost(uint32_t n_col) { return 0.35 + 0.65 * std::min(8u, (n_col + 31) / 32) / 8.0; }
 // Key pieces are at least this many 64-key tiles (a unit is cut only when it has twice as many).
-constexpr uint32_t PF_MIN_PIECE = 8;
+#ifndef LMH_PF_MIN_PIECE
+#define LMH_PF_MIN_PIECE 8
+#endif
+constexpr uint32_t PF_MIN_PIECE = LMH_PF_MIN_PIECE;
 // A decode row's 16-key tile for one KV head, in the same units (c2's decode kernel streams 36,864
 // such tiles in ~50 us on 256 CUs, 0.34 CU-us each, at a 2.2-us tile: 0.16; CUs that share HBM
 // with prefill work stream faster each).
@@ -40,7 +43,10 @@ constexpr double PF_MERGE_PARTIAL = 5.6e-5;
 constexpr double PF_MERGE_LAUNCH = 1.5;
 // Cut units only when that is estimated to finish at most this fraction of the whole units' time
 // (the walk's estimate was measured optimistic on c5: 7 tiles gained, 4.7 measured).
-constexpr double PF_CUT_GAIN = 0.9;
+#ifndef LMH_PF_CUT_GAIN
+#define LMH_PF_CUT_GAIN 0.9
+#endif
+constexpr double PF_CUT_GAIN = LMH_PF_CUT_GAIN;
 
 // Whole units grouped per workgroup, longest-processing-time-first: units by decreasing cost,
 // each to the currently least loaded workgroup. Returns the largest workgroup load.
@@ -167,12 +173,16 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
       const uint32_t k = (uint32_t)pieces.size();
       const uint32_t base = o.slots;
       if (k > 1) {
-        // merges per token of the unit, over the unit's heads of that token
+        // merges per token of the unit over the unit's heads of that token, in groups of heads
+        // whose partial rows (heads x pieces) one merge wave loads at once
+        const uint32_t hpm = std::max<uint32_t>(1, PF_MERGE_ROWS / k);
         const uint64_t c_abs = u.it.c_off;   // the unit's first column, counted from its first token
         for (uint32_t i = 0; i < u.it.n_tok; i++) {
           const uint64_t h_lo = i == 0 ? c_abs : 0;
           const uint64_t h_hi = std::min<uint64_t>(group, c_abs + u.it.n_col - (uint64_t)i * group);
-          o.merges.push_back(MergeItem{u.it.row0 + i, u.it.kvh, (uint32_t)h_lo, base + i * k, k, (uint32_t)(h_hi - h_lo)});
+          for (uint64_t h = h_lo; h < h_hi; h += hpm)
+            o.merges.push_back(MergeItem{u.it.row0 + i, u.it.kvh, (uint32_t)h, base + i * k, k,
+                                         (uint32_t)std::min<uint64_t>(hpm, h_hi - h)});
         }
         o.slots += u.it.n_tok * k;
       }

@@ -154,9 +154,9 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   PrefillItem* units = (PrefillItem*)(smem + NSTAGE * STAGE);      // this workgroup's unit list
   int* blk_lds = (int*)(units + per_wg);                           // block id of each key page in range
 
-  // The first workgroup copies the call's merge list (units that are key pieces of a longer range
-  // leave partials for the merge launch that follows).
-  dtile::copy_merges(mc, wg == 0);
+  // The workgroups copy the call's merge list, a slice each (units that are key pieces of a longer
+  // range leave partials for the merge launch that follows).
+  dtile::copy_merges(mc, wg, gridDim.x);
   // The workgroup's units (the host's balanced assignment, per_wg slots, an empty unit ends the
   // list): fetched once, so each unit starts without a memory round trip for its descriptor.
   {
@@ -838,7 +838,7 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     const uint32_t col = w * COLS + (LO ? pb : x) * 16 + hq;
     const uint32_t t = (col + c_off) / G, hh = (col + c_off) % G;
     if (it.slot != NO_SLOT) {
-      float* pp = pg.part + ((size_t)(it.slot + t * it.slot_stride) * pg.ng + (hh - (t == 0 ? c_off : 0))) * (HD + 4);
+      float* pp = pg.part + ((size_t)(it.slot + t * it.slot_stride) * pg.ng + hh) * (HD + 4);
 #pragma unroll
       for (int j = 0; j < NJ; j++) *(float4*)(pp + 16 * j + 4 * grp) = make_float4(O[j][x][0], O[j][x][1], O[j][x][2], O[j][x][3]);
       if (grp == 0) {
@@ -888,12 +888,12 @@ template <int KVT, int HD, bool PLO>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_t per_wg, uint32_t pf_wg, RowGeom r,
                   const DecodeItem* items, uint32_t n_items, const float* q, float* out, float* part, MergeCopy mc) {
-  if (blockIdx.x < pf_wg) {   // the decode workgroups copy the merge list
+  dtile::copy_merges(mc, blockIdx.x, gridDim.x);   // every workgroup copies a slice of the merge list
+  if (blockIdx.x < pf_wg) {
     prefill_wg<KVT, HD, PLO>(g, pg, pitems, per_wg, q, out, blockIdx.x, MergeCopy{nullptr, nullptr, 0});
     return;
   }
   const uint32_t b = blockIdx.x - pf_wg;
-  dtile::copy_merges(mc, b == 0);
   const uint32_t wi = b * PW + (threadIdx.x >> 6);
   if (wi < n_items) dtile::decode_item<KVT, HD, HD>(g, r, items, wi, q, out, part);
 }

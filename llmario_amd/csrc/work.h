@@ -30,7 +30,9 @@ constexpr uint32_t LOCAL_MERGE_MAX = 1024;   // heads x hdv of an item whose par
 constexpr int LOCAL_WAVES = 8;               // waves per workgroup of a local-merge call (its largest group)
 
 // Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, heads h0 ..
-// h0 + nh - 1; nh = 0: up to the item's head count ng). Head h0 + i sits at position i of a slot.
+// h0 + nh - 1). nh = 0 (a decode row's merge): up to the item's head count ng, head h0 + i at
+// position i of a slot. nh != 0 (a prompt token's merge over the key pieces of its unit): head h
+// at position h of a slot (the slot holds the whole KV group: group <= 16 = ng).
 struct MergeItem {
   uint32_t row;
   uint32_t kvh;
@@ -39,9 +41,11 @@ struct MergeItem {
   uint32_t n_split;
   uint32_t nh;
 };
-// A prompt token's merge (nh != 0) combines at most this many key pieces (the merge folds each
-// head's pieces within one wave); such merges precede the decode merges in a call's list.
+// A prompt token's merge (nh != 0) combines at most this many key pieces, and nh * n_split <=
+// PF_MERGE_ROWS unless nh = 1 (the merge folds an item's partial rows within one wave, loading up
+// to PF_MERGE_ROWS rows at once); such merges precede the decode merges in a call's list.
 constexpr uint32_t PF_MAX_PIECES = 64;
+constexpr uint32_t PF_MERGE_ROWS = 32;
 
 // One prefill work unit: KV head `kvh` of sequence `seq`. Its columns are the (token, query head)
 // pairs of the stacked rows row0, row0 + 1, .. (positions pos0, pos0 + 1, ..) flattened
@@ -50,8 +54,8 @@ constexpr uint32_t PF_MAX_PIECES = 64;
 // touch). Its keys are pages page0 .. page0 + n_pages - 1 of the sequence (16 positions each),
 // within each column's own range (causal, window). slot = NO_SLOT: those pages are the columns'
 // whole ranges and the unit writes the output. Otherwise the unit is one key piece of a longer
-// range: column (t, h)'s partial (o, m, l) goes to slot `slot + t * slot_stride`, at position
-// h - (t == 0 ? c_off : 0), and a merge launch combines the pieces.
+// range: column (t, h)'s partial (o, m, l) goes to slot `slot + t * slot_stride`, at position h,
+// and a merge launch combines the pieces.
 // blk: the block ids of pages page0 .. page0 + 7 (clamped to the last page), so the first K/V
 // tiles are fetched without waiting for the block table.
 struct PrefillItem {

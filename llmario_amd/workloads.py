@@ -116,7 +116,8 @@ class Workload:
 
 
 def config(name: str) -> Workload:
-    """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096); c3_q8 is c3 on q8_0 pages."""
+    """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096); c3_q8 is c3 on q8_0 pages;
+    chunk32k is a long-prefix prompt chunk (few, long prefill units: the key-piece case)."""
     if name == "c1":
         return Workload("c1", "f32", Layer(8, 8, 64, 64), prior=[255], new=[1], seed=1)
     if name == "c2":
@@ -137,6 +138,9 @@ def config(name: str) -> Workload:
         new = [1] * 16 + [512, 512]
         return Workload(name, "f16", Layer(40, 8, 128, 128), prior=prior, new=new, seed=5,
                         window=4096 if name == "c5w" else 0)
+    if name == "chunk32k":   # one 64-token prompt chunk on a 32,704-token prefix (chunked prefill of a
+        # long prompt): 8 prefill units of 256 columns, each with 512 key tiles, on a 256-CU device
+        return Workload("chunk32k", "f16", Layer(32, 8, 128, 128), prior=[32704], new=[64], seed=6)
     raise KeyError(name)
 
 

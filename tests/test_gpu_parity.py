@@ -285,7 +285,7 @@ def test_attend_config_all_rows(cuda, name):
     assert err <= TOL[w.kv_type], err
 
 
-@pytest.mark.parametrize("name", ["c3", "c3_q8", "c5", "c5w"])
+@pytest.mark.parametrize("name", ["c3", "c3_q8", "c5", "c5w", "chunk32k"])
 def test_attend_config_sampled_rows(cuda, name):
     w = config(name)
     hc, oc, q = pair(w)

@@ -146,7 +146,7 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
             assert rows[row0 + t] == (seq, pos0 + t)
             key = (row0 + t, kvh * group + h)
             ps = pieces.setdefault(key, [])
-            ps.append((page0, n_pages, slot if slot == NO_SLOT else slot + t * stride, h - (c_off if t == 0 else 0)))
+            ps.append((page0, n_pages, slot if slot == NO_SLOT else slot + t * stride, h))
     # prompt-token merges (nh != 0) come first, each over at most 64 pieces
     nh_col = [int(m[5]) for m in merges]
     n_pf = sum(1 for x in nh_col if x)
@@ -156,7 +156,9 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
     for m in merges:
         row, kvh, h0, slot0, n_split, nh = (int(x) for x in m[:6])
         if nh:
+            assert nh == 1 or nh * n_split <= 32
             for h in range(h0, h0 + nh):
+                assert (row, kvh * group + h) not in merge_of
                 merge_of[(row, kvh * group + h)] = (slot0, n_split, h0)
     for (row, head), ps in pieces.items():
         s_, pos = rows[row]
@@ -170,7 +172,7 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
         else:
             slot0, n_split, h0 = merge_of[(row, head)]
             assert n_split == len(ps) and sorted(p[2] for p in ps) == list(range(slot0, slot0 + n_split))
-            assert all(p[3] == head % group - h0 for p in ps)
+            assert all(p[3] == head % group for p in ps)   # a partial sits at its head's position
         covered[row, head] += 1
     assert (covered == 1).all(), np.argwhere(covered != 1)[:5]
 
@@ -223,9 +225,10 @@ def test_random_calls_plan_a_partition_of_the_work(seed):
 
 def test_configuration_shapes():
     """The benchmark configurations' calls plan as intended: c2's rows split into items of whole
-    tiles with merges; c3's prompts become prefill units only; c5 holds both kinds."""
+    tiles with merges; c3's prompts become prefill units only; c5 holds both kinds; chunk32k's eight
+    long units are cut into key pieces."""
     from llmario_amd.workloads import Generator, config
-    for name in ["c1", "c2", "c3", "c4", "c5", "c5w"]:
+    for name in ["c1", "c2", "c3", "c4", "c5", "c5w", "chunk32k"]:
         w = config(name)
         gen = Generator(w)
         bps = max(len(t) for t in gen.tables)
@@ -246,6 +249,10 @@ def test_configuration_shapes():
             assert len(items) > 0 and live_units > 0
         if name == "c2":
             assert live_units == 0 and len(merges) > 0
+        cut = bool(len(units)) and bool((units[units[:, 4] != 0][:, 9] != NO_SLOT).any())
+        # only the long-prefix chunk's few units are cut into key pieces (c5's are whole: cutting them
+        # measured slower)
+        assert cut == (name == "chunk32k"), name
 
 
 # Few long prompt units on many CUs: their key ranges are cut into pieces (stream-K), whose
