@@ -166,24 +166,34 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
     const double cap = (w_cut + PF_UNIT_COST * ((double)units.size() + slots)) / std::max<uint32_t>(slots, 1);
     const bool try_cut = !in.prefill_no_split && group <= 16 && !units.empty() && max_tiles >= 2 * PF_MIN_PIECE &&
                          cap < PF_CUT_GAIN * whole;
+    // A cut unit's merges: per token over the unit's heads of that token, in groups of heads whose
+    // partial rows (heads x pieces) one merge wave loads at once. for_each_merge(u, k, f) calls
+    // f(token, first head, heads) for each.
+    auto for_each_merge = [&](const PfUnit& u, uint32_t k, auto&& f) {
+      const uint32_t hpm = std::max<uint32_t>(1, PF_MERGE_ROWS / k);
+      const uint64_t c_abs = u.it.c_off;   // the unit's first column, counted from its first token
+      for (uint32_t i = 0; i < u.it.n_tok; i++) {
+        const uint64_t h_lo = i == 0 ? c_abs : 0;
+        const uint64_t h_hi = std::min<uint64_t>(group, c_abs + u.it.n_col - (uint64_t)i * group);
+        for (uint64_t h = h_lo; h < h_hi; h += hpm) f(i, (uint32_t)h, (uint32_t)std::min<uint64_t>(hpm, h_hi - h));
+      }
+    };
+    auto piece_merges = [&](const PfUnit& u, uint32_t k) {
+      uint64_t n = 0;
+      for_each_merge(u, k, [&](uint32_t, uint32_t, uint32_t) { n++; });
+      return n;
+    };
+    const size_t pf_slot_bytes = (size_t)ng * (in.hdv + 4) * 4;   // a slot holds the group's heads (ng = group)
     // a unit's pieces (workgroup, first tile) into the lists; a unit of several pieces gets a
-    // partial slot per (token, piece) and a merge per token
+    // partial slot per (token, piece) and its merges
     auto emit_pieces = [&](const PfUnit& u, const std::vector<std::pair<uint32_t, uint32_t>>& pieces,
                            std::vector<std::vector<PrefillItem>>& lists) {
       const uint32_t k = (uint32_t)pieces.size();
       const uint32_t base = o.slots;
       if (k > 1) {
-        // merges per token of the unit over the unit's heads of that token, in groups of heads
-        // whose partial rows (heads x pieces) one merge wave loads at once
-        const uint32_t hpm = std::max<uint32_t>(1, PF_MERGE_ROWS / k);
-        const uint64_t c_abs = u.it.c_off;   // the unit's first column, counted from its first token
-        for (uint32_t i = 0; i < u.it.n_tok; i++) {
-          const uint64_t h_lo = i == 0 ? c_abs : 0;
-          const uint64_t h_hi = std::min<uint64_t>(group, c_abs + u.it.n_col - (uint64_t)i * group);
-          for (uint64_t h = h_lo; h < h_hi; h += hpm)
-            o.merges.push_back(MergeItem{u.it.row0 + i, u.it.kvh, (uint32_t)h, base + i * k, k,
-                                         (uint32_t)std::min<uint64_t>(hpm, h_hi - h)});
-        }
+        for_each_merge(u, k, [&](uint32_t i, uint32_t h, uint32_t nh) {
+          o.merges.push_back(MergeItem{u.it.row0 + i, u.it.kvh, h, base + i * k, k, nh});
+        });
         o.slots += u.it.n_tok * k;
       }
       for (uint32_t s = 0; s < k; s++) {
@@ -230,14 +240,41 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
         }
         return load > 0.0 ? wg + 1 : wg;
       };
-      double lo_c = cap, hi_c = std::max(cap, max_cost) * 2.0;
-      while (walk(hi_c) > slots) hi_c *= 2.0;
-      for (int i = 0; i < 30 && hi_c > lo_c * 1.01; i++) {
-        const double mid = 0.5 * (lo_c + hi_c);
-        if (walk(mid) <= slots) hi_c = mid;
-        else lo_c = mid;
+      // the walk over at most n workgroups: the workgroups it uses
+      auto walk_fit = [&](uint32_t n) -> uint32_t {
+        const double lo0 = (w_cut + PF_UNIT_COST * ((double)units.size() + n)) / n;
+        double lo_c = lo0, hi_c = std::max(lo0, max_cost) * 2.0;
+        while (walk(hi_c) > n) hi_c *= 2.0;
+        for (int i = 0; i < 30 && hi_c > lo_c * 1.01; i++) {
+          const double mid = 0.5 * (lo_c + hi_c);
+          if (walk(mid) <= n) hi_c = mid;
+          else lo_c = mid;
+        }
+        return walk(hi_c);
+      };
+      // No-allocation calls: the pieces' partial slots and merges must fit their share of the
+      // scratch (half of it beside decode rows, whose splits take the rest; all of it otherwise),
+      // so the walk takes half the workgroups until they do.
+      auto pf_scratch = [&]() -> size_t {
+        uint64_t n_slots = 0, n_merges = 0;
+        for (size_t ui = 0; ui < units.size(); ui++) {
+          const uint64_t k = cuts[ui].size();
+          if (k > 1) {
+            n_slots += units[ui].it.n_tok * k;
+            n_merges += piece_merges(units[ui], (uint32_t)k);
+          }
+        }
+        return (n_slots * pf_slot_bytes + 255) / 256 * 256 + n_merges * sizeof(MergeItem);
+      };
+      const size_t pf_budget = decode_tiles > 0 ? in.noalloc_bytes / 2 : in.noalloc_bytes - 256;
+      uint32_t n_cap = slots;
+      uint32_t n_wg = walk_fit(n_cap);
+      bool fits = !in.noalloc || pf_scratch() <= pf_budget;
+      while (!fits && n_cap > 1) {
+        n_cap /= 2;
+        n_wg = walk_fit(n_cap);
+        fits = pf_scratch() <= pf_budget;
       }
-      const uint32_t n_wg = walk(hi_c);
       // the cut plan's largest load and its merge estimate
       std::vector<double> load(n_wg, 0.0);
       double partials = 0.0;
@@ -253,7 +290,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
       const double merge = partials * PF_MERGE_PARTIAL * (in.hdv + 4) / 132.0 +
                            (decode_tiles == 0 && partials > 0 ? PF_MERGE_LAUNCH : 0.0);
       const double cut_load = *std::max_element(load.begin(), load.end()) + merge;
-      if (cut_load < PF_CUT_GAIN * whole) {
+      if (fits && cut_load < PF_CUT_GAIN * whole) {
         lists.assign(n_wg, {});
         for (size_t ui = 0; ui < units.size(); ui++) emit_pieces(units[ui], cuts[ui], lists);
         while (!lists.empty() && lists.back().empty()) lists.pop_back();
@@ -303,8 +340,12 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   uint64_t target = std::max<uint64_t>(in.decode_target_items ? in.decode_target_items : cap_target, 1);
   // no-allocation calls: at most as many split slots (and merges) as the scratch holds
   const size_t slot_bytes = (size_t)ng * (in.hdv + 4) * 4;
-  if (in.noalloc)
-    target = std::max<uint64_t>(1, std::min<uint64_t>(target, in.noalloc_bytes / (slot_bytes + sizeof(MergeItem))));
+  if (in.noalloc) {
+    // what the prompt pieces' partials and merges left of the scratch (each region 256-aligned)
+    const size_t used = ((size_t)o.slots * slot_bytes + 255) / 256 * 256 + o.merges.size() * sizeof(MergeItem) + 256;
+    const size_t left = in.noalloc_bytes > used ? in.noalloc_bytes - used : 0;
+    target = std::max<uint64_t>(1, std::min<uint64_t>(target, left / (slot_bytes + sizeof(MergeItem))));
+  }
   // Smallest chunk: 8 tiles for the matrix-core kernels (enough work per wave to stream at full
   // rate); 2 tiles for f32 rows, whose VALU kernel walks keys with dependent loads (latency-bound:
   // more, shorter items hide it better); 4 for the row layout.

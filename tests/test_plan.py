@@ -299,6 +299,30 @@ def test_long_units_are_cut_into_key_pieces(kv, geo, prior, new, window, bt):
     assert (live_w[:, 9] == NO_SLOT).all() and len(live) > len(live_w)
 
 
+def test_noalloc_pieces_fit_the_scratch():
+    """A no-allocation call's key pieces keep their partials and merges within the scratch (half of
+    it beside decode rows): a long-prefix chunk whose full cut would need 33 MB runs on fewer,
+    longer pieces instead of whole units."""
+    n_head, n_kv, hd, hdv = 32, 8, 128, 128
+    for prior, new in [([32704], [64]), ([32704, 5000], [64, 1])]:
+        segs, start = [], 0
+        for s, (p, n) in enumerate(zip(prior, new)):
+            segs.append((s, start, n, p))
+            start += n
+        table = contiguous_table([p + n for p, n in zip(prior, new)], 16)
+        full = plan("f16", n_head, n_kv, hd, hdv, 16, table, segs)
+        items, merges, units, c = plan("f16", n_head, n_kv, hd, hdv, 16, table, segs, noalloc=True)
+        check_plan("f16", n_head, n_kv, hd, hdv, 16, table, segs, 0, items, merges, units, c, noalloc=True)
+        live = units[units[:, 4] != 0]
+        n_pf = int(sum(1 for m in merges if int(m[5])))
+        pf_slots = sum(int(u[4]) for u in live if int(u[9]) != NO_SLOT)   # a piece: a slot per token
+        pf_bytes = (pf_slots * c.ng * (hdv + 4) * 4 + 255) // 256 * 256 + n_pf * 24
+        budget = (32 << 20) // 2 if len(items) else (32 << 20) - 256
+        assert (live[:, 9] != NO_SLOT).any()                 # still cut
+        assert pf_bytes <= budget, (pf_bytes, budget)
+        assert len(live) < int((full[2][:, 4] != 0).sum())   # into fewer pieces than without the limit
+
+
 def test_invalid_calls_are_refused():
     table = np.arange(8, dtype=np.int64).reshape(1, 8)
     segs = [(0, 0, 1, 200)]                      # position 200 needs block 12 of 16-token blocks

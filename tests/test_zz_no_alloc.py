@@ -57,6 +57,25 @@ def test_noalloc_mixed_call_matches(cuda, kv):
     assert err <= TOL[kv] and np.array_equal(a, b)
 
 
+@pytest.mark.parametrize("prior", [4000, 32704])
+def test_noalloc_prompt_key_pieces(cuda, prior):
+    """A prompt chunk whose units are cut into key pieces (partials and merges in the scratch): at a
+    4,000-key prefix the no-allocation plan is lmh_attend's (the same bits); at 32,704 keys the
+    full cut would overflow the scratch, so the no-allocation call runs fewer, longer pieces and
+    matches within the tolerance."""
+    w = small("nak", "f16", Layer(32, 8, 128, 128), prior=[prior], new=[64], seed=6)
+    gen = Generator(w)
+    hc = harness.load(w, gen)
+    q = gen.q()
+    a, b = both(hc, w, q)
+    assert np.isfinite(b).all()
+    err = row_rel_err(b, a)
+    print(f"prompt pieces at {prior}: noalloc vs attend {err:.3e}, identical={np.array_equal(a, b)}")
+    assert err <= TOL["f16"], err
+    if prior == 4000:
+        assert np.array_equal(a, b)
+
+
 def test_noalloc_refuses_a_call_beyond_its_scratch(cuda):
     import torch
     # group 16 (16 heads per item) and 32 rows x 8 KV heads x 16 splits of 1024 keys: 4096 split
