@@ -51,47 +51,50 @@ constexpr int waves_per_eu() {
 
 // A prompt token's merge (MergeItem.nh != 0: the key pieces of a cut prefill unit), one wave per
 // item: heads h0 .. h0 + nh - 1 of its KV group, each the merge of the n_split = k piece partials
-// in slots slot0 .. slot0 + k - 1 (head h at position h of a slot). Row j = (head j / k, piece
-// j % k) of the item's nh * k <= 64 rows: lane j holds row j's (m, l) and turns them into
-// 2^(m - M_h) and 1 / L_h of its head; every lane then folds the rows, PF_MERGE_ROWS loads in
-// flight at once (the planner keeps nh * k within that, or nh = 1), into its NP dims, storing a head
-// after its last piece. Prompt merges exist only for hdv <= 128 (NP <= 2).
-template <int NP>
+// in slots slot0 .. slot0 + k - 1 (head h at position h of a slot). Lane h * K + s (K: k rounded up
+// to a power of two) holds (m, l) of head h's piece s and turns them into 2^(m - M_h) and 1 / L_h,
+// the max and sum taken by butterflies within each aligned group of K lanes (log2 K exchange
+// steps, not k dependent ones); every lane then folds the item's nh * k partial rows, up to
+// PF_MERGE_ROWS loads in flight (the planner keeps nh * k within that, or nh = 1; nh * K
+// <= 64 follows), into its NP dims, storing a head after its last piece, RB rows at a time (16
+// when no item has more: the lighter kernel runs more waves per SIMD). Prompt merges exist only
+// for hdv = 64 or 128 (the prefill's widths), i.e. hdv = 64 * NP.
+template <int NP, int RB>
 __device__ void merge_heads(const RowGeom& r, uint32_t hdv, const MergeItem& mi, const float* part, float* out,
                             uint32_t lane) {
-  if constexpr (NP <= 2) {
-    constexpr int RB = (int)PF_MERGE_ROWS;
+  {
     const uint32_t k = mi.n_split, nrow = mi.nh * k;
+    const uint32_t lk = k > 1 ? 32u - (uint32_t)__builtin_clz(k - 1) : 0u;   // K = 2^lk >= k
     const size_t hstride = hdv + 4, stride = (size_t)r.ng * hstride;
     const float* base = part + (size_t)mi.slot0 * stride + (size_t)mi.h0 * hstride;
-    const uint32_t jh = lane / k, first = jh * k;
+    const uint32_t jh = lane >> lk, js = lane & ((1u << lk) - 1u);
     float m = -INFINITY, l = 0.f;
-    if (lane < nrow) {
-      const float* pr = base + (size_t)(lane - first) * stride + (size_t)jh * hstride + hdv;
+    if (jh < mi.nh && js < k) {
+      const float* pr = base + (size_t)js * stride + (size_t)jh * hstride + hdv;
       m = pr[0];   // separate loads: (m, l) are 8-byte aligned only for even hdv
       l = pr[1];
     }
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < k; s++) M = fmaxf(M, __shfl(m, (int)(first + s)));
+    float M = m;
+    for (uint32_t x = 1; x < (1u << lk); x <<= 1) M = fmaxf(M, __shfl_xor(M, (int)x));
     const float c = m == -INFINITY ? 0.f : exp2_fast(m - M);
-    const float cl = c * l;
-    float L = 0.f;
-    for (uint32_t s = 0; s < k; s++) L += __shfl(cl, (int)(first + s));
+    float L = c * l;
+    for (uint32_t x = 1; x < (1u << lk); x <<= 1) L += __shfl_xor(L, (int)x);
     const float inv = L > 0.f ? 1.0f / L : 0.f;
     float acc[NP];
 #pragma unroll
     for (int i = 0; i < NP; i++) acc[i] = 0.f;
-    // (head, piece) of row j0 + t, advanced row by row (scalar: no division in the loops)
+    // (head, piece) of row j0 + t, advanced row by row (scalar: no division in the loops). hdv is
+    // 64 * NP here, so every lane loads its NP dims of a row as one vector; rows past the item's
+    // last re-read that row (in bounds, no branch between the loads) and are not folded.
+    typedef float fv __attribute__((ext_vector_type(NP)));
     uint32_t h_at = 0, s_at = 0;
     for (uint32_t j0 = 0; j0 < nrow; j0 += RB) {
-      float pre[RB][NP];
+      fv pre[RB];
       uint32_t h = h_at, sp = s_at;
 #pragma unroll
       for (int t = 0; t < RB; t++) {
-        const float* pp = base + (size_t)sp * stride + (size_t)h * hstride + lane * NP;
-#pragma unroll
-        for (int i = 0; i < NP; i++) pre[t][i] = j0 + t < nrow && lane * NP + i < hdv ? pp[i] : 0.f;
-        if (++sp == k) {
+        pre[t] = *(const fv*)(base + (size_t)sp * stride + (size_t)h * hstride + lane * NP);
+        if (j0 + t + 1 < nrow && ++sp == k) {
           sp = 0;
           h++;
         }
@@ -100,17 +103,18 @@ __device__ void merge_heads(const RowGeom& r, uint32_t hdv, const MergeItem& mi,
       for (int t = 0; t < RB; t++) {
         const uint32_t j = j0 + t;
         if (j < nrow) {
-          const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), (int)j));
+          const float cj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(c), (int)((h_at << lk) + s_at)));
 #pragma unroll
           for (int i = 0; i < NP; i++) acc[i] += cj * pre[t][i];
           if (++s_at == k) {
-            const float iv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), (int)j));
-            float* op = out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h_at) * hdv + lane * NP;
+            const float iv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(inv), (int)(h_at << lk)));
+            fv o;
 #pragma unroll
             for (int i = 0; i < NP; i++) {
-              if (lane * NP + i < hdv) op[i] = acc[i] * iv;
+              o[i] = acc[i] * iv;
               acc[i] = 0.f;
             }
+            *(fv*)(out + ((size_t)mi.row * r.n_head + mi.kvh * r.group + mi.h0 + h_at) * hdv + lane * NP) = o;
             s_at = 0;
             h_at++;
           }
@@ -120,26 +124,28 @@ __device__ void merge_heads(const RowGeom& r, uint32_t hdv, const MergeItem& mi,
   }
 }
 
-// Split-K merge (forward.rs:772-806): the n_pf leading items are prompt tokens' merges (one wave
-// each, merge_heads); then one wave per (decode item, query head), lanes over dims:
+// Split-K merge (forward.rs:772-806): merge_prompt_kernel runs the prompt tokens' merges (one wave
+// each, merge_heads), merge_kernel the decode rows' merges, one wave per (item, query head), lanes
+// over dims:
 // m* = max m_s, out = sum 2^(m_s - m*) o_s / sum 2^(m_s - m*) l_s, with m in the log2 domain.
 // A separate launch: the kernel boundary makes every split's partials visible across XCDs.
 // GROUPS: some decode item has more than 16 splits (rows past the first 16 are loaded in groups of
 // 16; without it the kernel keeps the lighter code that a call with at most 16 splits per item
 // runs).
+template <int NP, int RB>
+__global__ __launch_bounds__(256) void merge_prompt_kernel(RowGeom r, uint32_t hdv, const MergeItem* items,
+                                                           uint32_t n_items, const float* part, float* out) {
+  const uint32_t wv = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
+  if (wv < n_items) merge_heads<NP, RB>(r, hdv, items[wv], part, out, threadIdx.x & 63u);
+}
+
 template <int NP, bool GROUPS>
 __global__ __launch_bounds__(256) void merge_kernel(RowGeom r, uint32_t hdv, const MergeItem* items, uint32_t n_items,
-                                                    uint32_t n_pf, const float* part, float* out) {
+                                                    const float* part, float* out) {
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wv = __builtin_amdgcn_readfirstlane(blockIdx.x * 4 + (threadIdx.x >> 6));
-  if (wv < n_pf) {
-    const MergeItem mi = items[wv];
-    merge_heads<NP>(r, hdv, mi, part, out, lane);
-    return;
-  }
-  const uint32_t wi = wv - n_pf;
-  if (wi >= (n_items - n_pf) * r.ng) return;
-  const MergeItem mi = items[n_pf + wi / r.ng];
+  const uint32_t wi = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wi >= n_items * r.ng) return;
+  const MergeItem mi = items[wi / r.ng];
   const uint32_t h = wi % r.ng;
   if (mi.h0 + h >= r.group) return;
   // lane L folds dims L*NP .. L*NP+NP-1 (NP = ceil(hdv / 64); lanes past hdv idle)
@@ -810,18 +816,36 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
 }
 
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, uint32_t n_pf,
-                        const float* part, float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev) {
+                        uint32_t max_pf_rows, const float* part, float* out, uint32_t max_split, hipStream_t s,
+                        const LaunchEv& ev) {
   if (n_items == 0) return hipSuccess;
-  if (hdv == 0 || hdv > ROWS_MAX_DIM || n_pf > n_items) return hipErrorInvalidValue;
-  const uint64_t waves = n_pf + (uint64_t)(n_items - n_pf) * r.ng;
+  if (hdv == 0 || hdv > ROWS_MAX_DIM || n_pf > n_items || (n_pf > 0 && hdv != 64 && hdv != 128))
+    return hipErrorInvalidValue;
+  // the prompt tokens' merges and the decode merges as two launches when the call has both (the
+  // timing events then bracket the pair)
+  const uint32_t n_dec = n_items - n_pf;
+  const LaunchEv ev_pf{ev.start, n_dec ? nullptr : ev.stop}, ev_dec{n_pf ? nullptr : ev.start, ev.stop};
+  if (n_pf > 0) {
+    const dim3 grid((n_pf + 3) / 4), block(256);
+    if (max_pf_rows > 64) return hipErrorInvalidValue;   // nh * k <= PF_MERGE_ROWS, or nh = 1 and k <= 64
+    const bool light = max_pf_rows <= 16;
+    if (hdv == 64 && light) LMH_LAUNCH(ev_pf, (merge_prompt_kernel<1, 16>), grid, block, 0, s, r, hdv, items, n_pf, part, out);
+    else if (hdv == 64) LMH_LAUNCH(ev_pf, (merge_prompt_kernel<1, PF_MERGE_ROWS>), grid, block, 0, s, r, hdv, items, n_pf, part, out);
+    else if (light) LMH_LAUNCH(ev_pf, (merge_prompt_kernel<2, 16>), grid, block, 0, s, r, hdv, items, n_pf, part, out);
+    else LMH_LAUNCH(ev_pf, (merge_prompt_kernel<2, PF_MERGE_ROWS>), grid, block, 0, s, r, hdv, items, n_pf, part, out);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess || n_dec == 0) return e;
+  }
+  items += n_pf;
+  const uint64_t waves = (uint64_t)n_dec * r.ng;
   const dim3 grid((uint32_t)((waves + 3) / 4)), block(256);
   // dims per lane: ceil(hdv / 64) rounded up to a power of two
   const uint32_t np = hdv <= 64 ? 1 : hdv <= 128 ? 2 : hdv <= 256 ? 4 : 8;
 #define LMH_MERGE(NP)                                                                                              \
   if (np == NP) {                                                                                                  \
     if (max_split > 16)                                                                                            \
-      LMH_LAUNCH(ev, (merge_kernel<NP, true>), grid, block, 0, s, r, hdv, items, n_items, n_pf, part, out);        \
-    else LMH_LAUNCH(ev, (merge_kernel<NP, false>), grid, block, 0, s, r, hdv, items, n_items, n_pf, part, out);    \
+      LMH_LAUNCH(ev_dec, (merge_kernel<NP, true>), grid, block, 0, s, r, hdv, items, n_dec, part, out);           \
+    else LMH_LAUNCH(ev_dec, (merge_kernel<NP, false>), grid, block, 0, s, r, hdv, items, n_dec, part, out);       \
     return hipGetLastError();                                                                                      \
   }
   LMH_MERGE(1) LMH_MERGE(2) LMH_MERGE(4) LMH_MERGE(8)

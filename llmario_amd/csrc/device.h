@@ -150,9 +150,11 @@ hipError_t launch_decode(const PageGeom& g, const RowGeom& r, const DecodeItem* 
                          const float* q, float* out, float* part, const MergeCopy& mc, hipStream_t s,
                          const LaunchEv& ev = {});
 // items: n_pf prompt-token merges (nh != 0, n_split <= 64) first, then the decode merges;
-// max_split: the largest n_split of the decode merges (over 16: rows loaded in groups of 16)
+// max_pf_rows: the largest nh * n_split of the prompt merges; max_split: the largest n_split of the
+// decode merges (over 16: rows loaded in groups of 16)
 hipError_t launch_merge(const RowGeom& r, uint32_t hdv, const MergeItem* items, uint32_t n_items, uint32_t n_pf,
-                        const float* part, float* out, uint32_t max_split, hipStream_t s, const LaunchEv& ev = {});
+                        uint32_t max_pf_rows, const float* part, float* out, uint32_t max_split, hipStream_t s,
+                        const LaunchEv& ev = {});
 // The device scratch of lmh_attend_noalloc (split-K partials, then the merge list): its size, and
 // the address of `device`'s copy (call with that device current; resolved once per device).
 constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(32) << 20;

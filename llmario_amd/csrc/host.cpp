@@ -1532,18 +1532,19 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   if (!kv->plan.merges.empty()) {
     if ((e = time_launch(LMH_KERNEL_MERGE, ev)) != hipSuccess) return kv->hip_fail(e, "event");
     // the planner lists the prompt tokens' merges (nh != 0) before the decode merges
-    uint32_t max_split = 0, n_pf = 0;
+    uint32_t max_split = 0, n_pf = 0, max_pf_rows = 0;
     for (const MergeItem& m : kv->plan.merges) {
       if (m.nh != 0) {
+        max_pf_rows = std::max(max_pf_rows, m.nh * m.n_split);
         if (n_pf != (uint32_t)(&m - kv->plan.merges.data()) || m.n_split > PF_MAX_PIECES ||
-            (m.nh > 1 && m.nh * m.n_split > PF_MERGE_ROWS) || y.hdv > 128)
+            (m.nh > 1 && m.nh * m.n_split > PF_MERGE_ROWS) || (y.hdv != 64 && y.hdv != 128))
           return kv->fail(LMH_UNSUPPORTED, "attend: the planner's prompt merges are out of order or too long");
         n_pf++;
       } else {
         max_split = std::max(max_split, m.n_split);
       }
     }
-    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->plan.merges.size(), n_pf,
+    e = launch_merge(r, y.hdv, (const MergeItem*)merge_dst, (uint32_t)kv->plan.merges.size(), n_pf, max_pf_rows,
                      part, out, max_split, st, ev);
     if (e != hipSuccess) return kv->hip_fail(e, "merge kernel");
   }
