@@ -413,7 +413,7 @@ __global__ __launch_bounds__(256) void qk_rope_store_reg_kernel(PageGeom g, Rope
         }
       }
       if (is_q) {
-        *(fv*)(q_out + ((size_t)row * r.n_head + it) * HD + lane * VPL) = x;
+        __builtin_nontemporal_store(x, (fv*)(q_out + ((size_t)row * r.n_head + it) * HD + lane * VPL));
       } else {
         float xa[VPL];
 #pragma unroll
@@ -664,7 +664,7 @@ __device__ void rope_tokens(const PageGeom& g, const RopeGeom& r, float2 (*cs)[R
       }
       if (is_q) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) *(fv*)(q_out + ((size_t)(row0 + t) * r.n_head + it) * HD + lane * VPL) = x[t];
+        for (int t = 0; t < NT; t++) __builtin_nontemporal_store(x[t], (fv*)(q_out + ((size_t)(row0 + t) * r.n_head + it) * HD + lane * VPL));
       } else if (!is_v || NT == 1) {
 #pragma unroll
         for (int t = 0; t < NT; t++) {
@@ -891,7 +891,13 @@ __device__ void rope_quad_slots(const PageGeom& g, const RopeGeom& r, float2 (*c
 #pragma unroll
         for (uint32_t hb = 0; hb < 2; hb++)
 #pragma unroll
-          for (uint32_t f = 0; f < NF; f++) *(float4*)(dst + hb * H2 + 4 * (sub + 8 * f)) = x[hb][f];
+          for (uint32_t f = 0; f < NF; f++) {
+            // Q is stored non-temporally (rope_c3: kernel 75 -> 60 us); the K/V pages stay
+            // cacheable for the attention call that reads them next (non-temporal there: no gain)
+            typedef float f4 __attribute__((ext_vector_type(4)));
+            const f4 v = {x[hb][f].x, x[hb][f].y, x[hb][f].z, x[hb][f].w};
+            __builtin_nontemporal_store(v, (f4*)(dst + hb * H2 + 4 * (sub + 8 * f)));
+          }
       } else {
         uint8_t* head = sl0.base + g.k_off + hh * g.k_head + sl0.tile * g.k_tile;
 #pragma unroll
