@@ -90,10 +90,11 @@ struct DirtyRows {  // the rows [lo, hi) of a host-side table that differ from t
 // one event covers every use enqueued before it: an event is recorded every EVERY uses (and when
 // the stream changes) instead of after each call, since each event record on the stream costs the
 // GPU ~3 us between a call's last kernel and the next call's first (c2's step 59.4 -> 57.0 us,
-// c1's 14.0 -> 10.9 us).
+// c1's 14.0 -> 10.9 us, one event per 4 uses; per 8 uses, c2 54.8-55.4 -> 54.4-54.7 us and c4
+// 99.5-100.4 -> 98.2-98.5 us on one box).
 struct Uploader {
   static constexpr int N = 16;      // slots (N > EVERY: a slot comes round after its use is covered)
-  static constexpr int EVERY = 4;   // uses per completion event
+  static constexpr int EVERY = 8;   // uses per completion event
   uint8_t* host[N] = {};
   uint8_t* dev[N] = {};  // the device address of host[i]
   size_t cap[N] = {};
