@@ -284,6 +284,12 @@ int32_t lmh_attend_noalloc(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
  *   prefill_whole_units: 1 = prefill units always run whole; 0 (default) = when whole units would
  *     leave the device unbalanced (few, long units), their key ranges are cut into pieces spread over
  *     the workgroups, whose partial results a merge launch combines (heads per KV group <= 16).
+ *   prefill_q_split: how the f16 / bf16 prefill launch takes a Q with bits below the page type
+ *     (Q as f16 hi + lo parts either way, results within the same bound): 1 = the launch for
+ *     exact Q, whose units with such bits run two passes of half their columns; 2 = the launch
+ *     whose every unit runs one pass with the hi + lo products (a Q exact in the page type runs
+ *     slower there); 0 (default) = the second when the handle's previous prefill launch found
+ *     such bits (each launch records it), else the first. q8_0 pages always take the first.
  * Out-of-range values fail with LMH_INVALID_ARGUMENT and change nothing. */
 typedef struct lmh_attend_tuning {
   uint32_t abi_version;        /* LMH_ABI_VERSION */
@@ -294,7 +300,7 @@ typedef struct lmh_attend_tuning {
   uint64_t prefill_workgroups;  /* cap on the prefill kernel's workgroups (0: every slot of the device);
                                    fewer workgroups run more units each */
   uint32_t prefill_whole_units;
-  uint32_t reserved;            /* 0 */
+  uint32_t prefill_q_split;     /* 0 (default), 1 or 2 */
 } lmh_attend_tuning;
 int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t);
 /* The options as set (0 = the default, which each call resolves). */

@@ -62,7 +62,7 @@ class RopeParams(C.Structure):
 class AttendTuning(C.Structure):
     _fields_ = [("abi_version", u32), ("prefill_p_f16", u32), ("prefill_min_rows", u64),
                 ("decode_target_items", u64), ("decode_min_tiles", u64), ("prefill_workgroups", u64),
-                ("prefill_whole_units", u32), ("reserved", u32)]
+                ("prefill_whole_units", u32), ("prefill_q_split", u32)]
 
 
 class PlanDesc(C.Structure):

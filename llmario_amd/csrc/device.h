@@ -84,7 +84,9 @@ struct PrefillGeom {
   uint32_t window;   // 0 = none
   uint32_t p_f16;    // 1: P rounded to f16 for P.V (Metal's prefill precision); 0: f16 hi + lo (q8_0: always hi + lo)
   uint32_t ng;       // heads per partial slot (units that are key pieces write partials)
+  uint32_t q_split;  // 1: f16 / bf16 pages run every unit as one pass of Q hi + lo products
   float* part;       // the call's partial slots
+  uint32_t* q_flag;  // workgroup 0 records whether its first unit's Q has bits below the page type
 };
 
 // Fused per-row tail of attention_block (see lmh_qk_rope_store): flags as LMH_ROPE_*.

@@ -283,6 +283,11 @@ struct lmh_kv {
   uint64_t prefill_min_rows = 0, decode_target_items = 0, decode_min_tiles = 0;  // 0: defaults
   uint64_t prefill_workgroups = 0;                                                  // 0: every slot
   bool prefill_whole_units = false;   // prefill units never cut into key pieces
+  uint32_t prefill_q_split = 0;       // 0: from q_flag; 1: exact-Q launch; 2: hi + lo launch
+  // Written by each prefill launch (workgroup 0): whether its first unit's Q has bits below the
+  // page type. Pinned and device-mapped, read without waiting: the next call's launch choice.
+  volatile uint32_t* q_flag = nullptr;
+  uint32_t* q_flag_dev = nullptr;
   std::string err;
 
   ~lmh_kv() {
@@ -291,6 +296,7 @@ struct lmh_kv {
     if (d_table) (void)hipFree(d_table);
     if (d_wpool) (void)hipFree(d_wpool);
     if (d_wtable) (void)hipFree(d_wtable);
+    if (q_flag) (void)hipHostFree((void*)q_flag);
     for (auto& p : evs) {
       (void)hipEventDestroy(p.first);
       (void)hipEventDestroy(p.second);
@@ -866,6 +872,15 @@ int32_t lmh_kv_create(const lmh_kv_options* o, lmh_kv** out) {
   if (e == hipSuccess) e = kv->up.reserve(std::max<size_t>(1 << 20, kv->bps * 4 * 16));
   // this device's copy of lmh_attend_noalloc's scratch (resolved once per device)
   if (e == hipSuccess) e = noalloc_scratch(o->device, &kv->scratch);
+  if (e == hipSuccess) {
+    void* f = nullptr;
+    e = hipHostMalloc(&f, 256, hipHostMallocMapped | hipHostMallocCoherent);
+    if (e == hipSuccess) {
+      kv->q_flag = (volatile uint32_t*)f;
+      *kv->q_flag = 0;
+      e = hipHostGetDevicePointer((void**)&kv->q_flag_dev, f, 0);
+    }
+  }
   if (e != hipSuccess) {
     g_create_error = std::string("device allocation failed: ") + hipGetErrorString(e);
     delete kv;
@@ -1501,6 +1516,10 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   pg.p_f16 = kv->prefill_p_f16 ? 1u : 0u;
   pg.ng = ng;
   pg.part = part;
+  pg.q_flag = kv->q_flag_dev;
+  // the launch for a Q with bits below the page type (one pass of hi + lo products), when asked
+  // for or when the handle's previous prefill launch found such bits
+  pg.q_split = kv->prefill_q_split == 2 || (kv->prefill_q_split == 0 && *kv->q_flag != 0) ? 1u : 0u;
   const MergeCopy mc{(const uint32_t*)(ex + items_pad), merge_dst,
                      kv->plan.merges.empty() ? 0u : (uint32_t)(merges_bytes / 4)};
   // timing events are made on first use: not on the no-allocation path
@@ -1571,7 +1590,7 @@ static const char* tuning_error(const lmh_attend_tuning* t) {
   if (t->decode_target_items > (1ull << 32)) return "tuning: decode_target_items out of range";
   if (t->prefill_workgroups > (1ull << 32)) return "tuning: prefill_workgroups out of range";
   if (t->prefill_whole_units > 1) return "tuning: prefill_whole_units must be 0 or 1";
-  if (t->reserved != 0) return "tuning: reserved must be 0";
+  if (t->prefill_q_split > 2) return "tuning: prefill_q_split must be 0, 1 or 2";
   return nullptr;
 }
 
@@ -1584,6 +1603,7 @@ int32_t lmh_kv_set_tuning(lmh_kv* kv, const lmh_attend_tuning* t) {
   kv->decode_target_items = t->decode_target_items;
   kv->decode_min_tiles = t->decode_min_tiles;
   kv->prefill_whole_units = t->prefill_whole_units != 0;
+  kv->prefill_q_split = t->prefill_q_split;
   return LMH_OK;
 }
 
@@ -1596,7 +1616,7 @@ int32_t lmh_kv_get_tuning(const lmh_kv* kv, lmh_attend_tuning* t) {
   t->decode_min_tiles = kv->decode_min_tiles;
   t->prefill_workgroups = kv->prefill_workgroups;
   t->prefill_whole_units = kv->prefill_whole_units ? 1u : 0u;
-  t->reserved = 0;
+  t->prefill_q_split = kv->prefill_q_split;
   return LMH_OK;
 }
 

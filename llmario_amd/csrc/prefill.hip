@@ -136,7 +136,7 @@ __device__ inline uint4 i8x8_to_bf8(uint32_t a, uint32_t b) {
 // Workgroup `wg` of a prefill launch: its list of units, items[wg * per_wg ..]. PLO: P carried
 // past f16 as hi + lo halves (two P.V products on the same V operand); without it P is rounded
 // to f16, the precision of the Metal sibling's prefill.
-template <int KVT, int HD, bool PLO>
+template <int KVT, int HD, bool PLO, bool QS>
 __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom& pg, const PrefillItem* items,
                                            uint32_t per_wg, const float* q, float* out, uint32_t wg,
                                            const MergeCopy& mc) {
@@ -460,19 +460,37 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
     for (int i = 0; i < PW; i++) lo_or |= lo_flags[i];
     lo_any = lo_or != 0;
+    // the handle's record for its next call's launch choice (workgroup 0's first unit)
+    if (wg == 0 && unit == 0 && tid == 0 && pg.q_flag) *pg.q_flag = lo_any ? 1u : 0u;
   }
-  widen_k = KVT != KV_BF16 || lo_any;
-  if (lo_any) {   // column block `pass` of each wave: its Q as hi (qf[0]) + lo (qf[1])
+  // QS: every unit of a 16-bit page launch runs one pass with Q as hi + lo parts
+  constexpr bool SPLIT_ALL = QS && !Q8;
+  widen_k = KVT != KV_BF16 || lo_any || SPLIT_ALL;
+  // Q as f16 hi + lo parts: the QS launch of 16-bit pages runs every unit as one pass of both
+  // column blocks, Q as hi (qf) + lo (ql); otherwise a Q with bits below the page type runs two
+  // passes of one column block, its Q as hi (qf[0]) + lo (qf[1]).
+  h8 ql[NCB][NC];
+  if constexpr (SPLIT_ALL) {
+#pragma unroll
+    for (int x = 0; x < NCB; x++) {
+      float4 raw[NC][2];
+      load_q(w * COLS + x * 16 + hq, raw);
+      split_q(raw, qf[x], ql[x]);
+    }
+  } else if (lo_any) {
     float4 raw[NC][2];
     load_q(w * COLS + pass * 16 + hq, raw);
     split_q(raw, qf[0], qf[1]);
   }
 
-  // One pass over the unit's key tiles for this wave's column blocks: LO = false, both blocks
-  // (columns 32w .. 32w+31) with Q in f16; LO = true, block `pb` (columns 32w + 16pb ..) with
+  // One pass over the unit's key tiles for this wave's column blocks: MODE 0, both blocks
+  // (columns 32w .. 32w+31) with Q in f16 (or bf16); MODE 2, both blocks with Q as f16 hi (qf) +
+  // lo (ql) parts, the two products of each summed in one accumulator; MODE 1 (LO), block `pb`
+  // (columns 32w + 16pb ..) with
   // its Q as hi (qf[0]) + lo (qf[1]).
-  auto run = [&](auto lo_tag, uint32_t pb) {
-  constexpr bool LO = decltype(lo_tag)::value;
+  auto run = [&](auto mode_tag, uint32_t pb) {
+  constexpr int MODE = decltype(mode_tag)::value;
+  constexpr bool LO = MODE == 1, LO2 = MODE == 2;
   constexpr int NX = LO ? 1 : NCB;            // column blocks of the pass
   const float c2 = pg.scale_log2;             // scale * log2(e): raw score -> log2 domain
   uint32_t cpos[NCB], clo[NCB];
@@ -599,7 +617,13 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
 #pragma unroll
       for (int kk = 0; kk < 2; kk++) {
         const h8 a = __builtin_bit_cast(h8, ko.a[ch][kk]);
-        if constexpr (LO) {
+        if constexpr (LO2) {
+#pragma unroll
+          for (int cb = 0; cb < NCB; cb++) {
+            const f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[cb][ch], ch == 0 ? nmv[cb] : S[kk][cb], 0, 0, 0);
+            S[kk][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, ql[cb][ch], acc, 0, 0, 0);
+          }
+        } else if constexpr (LO) {
           S[kk][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[0][ch], ch == 0 ? nmv[0] : S[kk][0], 0, 0, 0);
           S[kk][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qf[1][ch], ch == 0 ? f4{0.f, 0.f, 0.f, 0.f} : S[kk][1],
                                                             0, 0, 0);
@@ -803,11 +827,14 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     const bool need_mask = key0 + BK - 1 > wpos_min || key0 < wlo_max || key0 + BK - 1 > pos_last;
     if (wave_active) {
       load_k(ko, kt, 1);
-      load_v(vo, vt, 0);
+      // MODE 2 (twice the Q registers): V's operands are read once the K operands are consumed,
+      // during the exponentials, so the two sets are not held at once
+      if constexpr (!LO2) load_v(vo, vt, 0);
       if (need_mask) mask(S0, key0);
       wait_tile(ti + 1);
       settle(ti + 1);
       qk(S1, ko);
+      if constexpr (LO2) load_v(vo, vt, 0);
       softmax(S0, Ph, Pl, S1);
       pv(Ph, Pl, vo);
       if (need_mask) mask(S1, key0 + 32);
@@ -817,12 +844,13 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     }
     if (ti + 1 < n_tiles) sync();
     if (wave_active) {
-      load_v(vo, vt, 1);
+      if constexpr (!LO2) load_v(vo, vt, 1);
       // first half of the next tile (after the last tile: a stale stage, never used), issued
       // before this half's exponentials so its products overlap them and are complete when the
       // next iteration reads S0
       load_k(ko, kv_lds + ((ti + 1) % NSTAGE) * STAGE, 0);
       qk(S0, ko);
+      if constexpr (LO2) load_v(vo, vt, 1);
       softmax(S1, Ph, Pl, S0);
       pv(Ph, Pl, vo);
     }
@@ -862,22 +890,27 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   __syncthreads();
   };
 
-  if (!lo_any) {
-    run(std::false_type{}, 0);
+  if constexpr (SPLIT_ALL) {
+    run(std::integral_constant<int, 2>{}, 0);
     unit++;
   } else {
-    run(std::true_type{}, pass);
-    pass ^= 1u;
-    if (pass == 0) unit++;
+    if (!lo_any) {
+      run(std::integral_constant<int, 0>{}, 0);
+      unit++;
+    } else {
+      run(std::integral_constant<int, 1>{}, pass);
+      pass ^= 1u;
+      if (pass == 0) unit++;
+    }
   }
   }
 }
 
-template <int KVT, int HD, bool PLO>
+template <int KVT, int HD, bool PLO, bool QS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32_t per_wg, const float* q,
                     float* out, MergeCopy mc) {
-  prefill_wg<KVT, HD, PLO>(g, pg, items, per_wg, q, out, blockIdx.x, mc);
+  prefill_wg<KVT, HD, PLO, QS>(g, pg, items, per_wg, q, out, blockIdx.x, mc);
 }
 
 // A mixed batch (prefill units and decode items) in one launch: workgroups 0 .. pf_wg-1 run the
@@ -887,13 +920,13 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
 // workgroup carries the prefill LDS allocation, so a CU holds one workgroup of either kind: the
 // same eight waves per CU the decode kernel runs at. One launch instead of a decode launch on a
 // second stream saves the two cross-stream waits and their idle gaps.
-template <int KVT, int HD, bool PLO>
+template <int KVT, int HD, bool PLO, bool QS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_t per_wg, uint32_t pf_wg, RowGeom r,
                   const DecodeItem* items, uint32_t n_items, const float* q, float* out, float* part, MergeCopy mc) {
   dtile::copy_merges(mc, blockIdx.x, gridDim.x);   // every workgroup copies a slice of the merge list
   if (blockIdx.x < pf_wg) {
-    prefill_wg<KVT, HD, PLO>(g, pg, pitems, per_wg, q, out, blockIdx.x, MergeCopy{nullptr, nullptr, 0});
+    prefill_wg<KVT, HD, PLO, QS>(g, pg, pitems, per_wg, q, out, blockIdx.x, MergeCopy{nullptr, nullptr, 0});
     return;
   }
   const uint32_t b = blockIdx.x - pf_wg;
@@ -907,14 +940,19 @@ hipError_t launch_t(const PageGeom& g, const PrefillGeom& pg, const PrefillItem*
                     const LaunchEv& ev) {
   const uint32_t lds = (uint32_t)prefill_lds_bytes(KVT, HD, max_pages, per_wg);
   // q8_0 has one instance: its scaled weights are always carried as hi + lo (prefill_p_f16 applies to
-  // 16-bit pages)
+  // 16-bit pages) and its Q with lo parts runs two passes; 16-bit pages have an instance per Q form
   if constexpr (KVT != KV_Q8) {
-    if (pg.p_f16) {
-      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
-      return hipGetLastError();
-    }
+    if (pg.p_f16 && pg.q_split)
+      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
+    else if (pg.p_f16)
+      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, false, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
+    else if (pg.q_split)
+      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
+    else
+      LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
+    return hipGetLastError();
   }
-  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
+  LMH_LAUNCH(ev, (prefill_kernel<KVT, HD, true, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, items, per_wg, q, out, mc);
   return hipGetLastError();
 }
 
@@ -925,15 +963,18 @@ hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const Prefil
                           hipStream_t s, const LaunchEv& ev) {
   const uint32_t lds = (uint32_t)prefill_lds_bytes(KVT, HD, max_pages, per_wg);
   const uint32_t n_wg = pf_wg + (n_items + PW - 1) / PW;
+#define LMH_MIXED_LAUNCH(P, S)                                                                               \
+  LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, P, S>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r, items, \
+             n_items, q, out, part, mc)
   if constexpr (KVT != KV_Q8) {
-    if (pg.p_f16) {
-      LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, false>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
-                 items, n_items, q, out, part, mc);
-      return hipGetLastError();
-    }
+    if (pg.p_f16 && pg.q_split) LMH_MIXED_LAUNCH(false, true);
+    else if (pg.p_f16) LMH_MIXED_LAUNCH(false, false);
+    else if (pg.q_split) LMH_MIXED_LAUNCH(true, true);
+    else LMH_MIXED_LAUNCH(true, false);
+    return hipGetLastError();
   }
-  LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, true>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r,
-             items, n_items, q, out, part, mc);
+  LMH_MIXED_LAUNCH(true, false);
+#undef LMH_MIXED_LAUNCH
   return hipGetLastError();
 }
 

@@ -281,7 +281,8 @@ class HipKvCache:
 
     def set_tuning(self, *, prefill_p_f16: bool | None = None, prefill_min_rows: int | None = None,
                    decode_target_items: int | None = None, decode_min_tiles: int | None = None,
-                   prefill_workgroups: int | None = None, prefill_whole_units: bool | None = None):
+                   prefill_workgroups: int | None = None, prefill_whole_units: bool | None = None,
+                   prefill_q_split: int | None = None):
         """lmh_kv_set_tuning: change the given options, keep the others (0 = the default)."""
         t = N.AttendTuning()
         self._check(N.lib().lmh_kv_get_tuning(self.h, C.byref(t)))
@@ -297,12 +298,14 @@ class HipKvCache:
             t.prefill_workgroups = int(prefill_workgroups)
         if prefill_whole_units is not None:
             t.prefill_whole_units = 1 if prefill_whole_units else 0
+        if prefill_q_split is not None:
+            t.prefill_q_split = int(prefill_q_split)
         self._check(N.lib().lmh_kv_set_tuning(self.h, C.byref(t)))
 
     def tuning(self) -> dict:
         t = N.AttendTuning()
         self._check(N.lib().lmh_kv_get_tuning(self.h, C.byref(t)))
-        return {f: getattr(t, f) for f, _ in N.AttendTuning._fields_ if f not in ("abi_version", "reserved")}
+        return {f: getattr(t, f) for f, _ in N.AttendTuning._fields_ if f != "abi_version"}
 
     def set_timing(self, on: bool):
         self._check(N.lib().lmh_kv_set_timing(self.h, 1 if on else 0))

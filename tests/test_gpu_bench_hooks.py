@@ -59,10 +59,12 @@ def test_tuning_read_back_changes_nothing(cuda):
     oc = O.empty_cache_for(w)
     hc = harness.load(w, gen, on_rows=lambda s, t, k, v: O.fill(oc, t, s, k, v, w.prior[s]))
     assert hc.tuning() == {"prefill_p_f16": 0, "prefill_min_rows": 0, "decode_target_items": 0,
-                           "decode_min_tiles": 0, "prefill_workgroups": 0, "prefill_whole_units": 0}
+                           "decode_min_tiles": 0, "prefill_workgroups": 0, "prefill_whole_units": 0,
+                           "prefill_q_split": 0}
     hc.set_tuning(prefill_workgroups=3)
     assert hc.tuning() == {"prefill_p_f16": 0, "prefill_min_rows": 0, "decode_target_items": 0,
-                           "decode_min_tiles": 0, "prefill_workgroups": 3, "prefill_whole_units": 0}
+                           "decode_min_tiles": 0, "prefill_workgroups": 3, "prefill_whole_units": 0,
+                           "prefill_q_split": 0}
     q = gen.q()
     qd = torch.from_numpy(q).cuda()
     out = torch.empty((w.n_rows, w.layer.n_head, w.layer.hdv), device="cuda")

@@ -9,7 +9,9 @@ The head geometries are c2's (decode rows, f16), c3's (causal prefill, bf16; als
 (decode rows and a prefill chunk in one launch, f16; also with a window, and q8_0), each with Q
 carrying bits below f16 (the prefill kernel's two-pass path with hi + lo Q parts) and with Q held
 in the cache's 16-bit type (its one-pass path; q8_0 prompts always take the two-pass path), and
-with automatic and forced split-K.
+with automatic and forced split-K. The `_split` forms force the prefill launch whose units all run
+one pass of Q hi + lo products (prefill_q_split = 2; the default picks it after a launch whose Q
+had bits below the page type), on a Q with such bits and on one without.
 """
 
 import os
@@ -93,7 +95,7 @@ def build(kv, L, prior, new, seed, v_scale=None):
 
 
 @pytest.mark.parametrize("name,kv,layer,prior,new,window", CASES, ids=[c[0] for c in CASES])
-@pytest.mark.parametrize("q_kind", ["f32", "rounded"])
+@pytest.mark.parametrize("q_kind", ["f32", "rounded", "f32_split", "rounded_split"])
 @pytest.mark.parametrize("split", ["auto", "forced"])
 def test_cancelling_rows(cuda, name, kv, layer, prior, new, window, q_kind, split):
     import torch
@@ -101,8 +103,10 @@ def test_cancelling_rows(cuda, name, kv, layer, prior, new, window, q_kind, spli
     hc, oc, segs, n_rows, rng = build(kv, layer, prior, new, seed=zlib.crc32(f"{name}/{q_kind}".encode()) % 1000)
     if split == "forced":
         hc.set_tuning(decode_min_tiles=1, decode_target_items=100000)
+    if q_kind.endswith("_split"):
+        hc.set_tuning(prefill_q_split=2)
     q = rng.standard_normal((n_rows, layer.n_head, layer.hd)).astype(np.float32)
-    if q_kind == "rounded":
+    if q_kind.startswith("rounded"):
         q = to_type(q, kv)
     scale = layer.hd ** -0.5
     out = torch.full((n_rows, layer.n_head, layer.hdv), float("nan"), device="cuda")

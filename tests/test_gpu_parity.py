@@ -236,13 +236,15 @@ STREAM = [
 
 
 @pytest.mark.parametrize("kv,layer,prior,new,window,bt", STREAM)
-@pytest.mark.parametrize("q_kind", ["rounded", "f32"])
+@pytest.mark.parametrize("q_kind", ["rounded", "f32", "f32_split"])
 @pytest.mark.parametrize("wgs", [1, 3])
 def test_prefill_units_stream_through_few_workgroups(cuda, kv, layer, prior, new, window, bt, q_kind, wgs):
     w = small("s", kv, layer, prior, new, window=window, seed=47, block_tokens=bt)
     hc, oc, q = pair(w)
-    if q_kind == "f32":   # bits below f16 / bf16: the two-pass path
+    if q_kind != "rounded":   # bits below f16 / bf16: two passes, or (_split) one of hi + lo products
         q = np.random.default_rng(5).standard_normal(q.shape).astype(np.float32)
+    if q_kind == "f32_split":
+        hc.set_tuning(prefill_q_split=2)
     hc.set_tuning(prefill_workgroups=wgs)
     assert hc.tuning()["prefill_workgroups"] == wgs
     got = run_gpu(hc, w, q)
@@ -253,16 +255,40 @@ def test_prefill_units_stream_through_few_workgroups(cuda, kv, layer, prior, new
     assert err <= TOL[kv], err
 
 
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_prefill_q_form_follows_previous_launch(cuda, kv):
+    """By default (prefill_q_split = 0) a call's prefill launch is chosen by the Q its previous
+    launch saw: calls alternating between a Q exact in the page type and one with bits below it
+    run every pairing of Q form and launch (each change of form meets the launch chosen for the
+    other), all within the bound and equal to the same call with the launch forced."""
+    w = small("qs", kv, Layer(32, 8, 128, 128), prior=[0, 300], new=[300, 200], seed=11)
+    hc, oc, q = pair(w)
+    qf = np.random.default_rng(3).standard_normal(q.shape).astype(np.float32)
+    refs = {id(x): oc.attend(0, w.segments(), x, w.scale, w.window, THREADS) for x in (q, qf)}
+    for x in (q, qf, qf, q, q, qf):
+        got = run_gpu(hc, w, x)
+        err = row_rel_err(got, refs[id(x)])
+        print(f"{kv} q={'f32' if x is qf else 'rounded'}: {err:.3e}")
+        assert err <= TOL[kv], err
+    for forced in (1, 2):
+        hc.set_tuning(prefill_q_split=forced)
+        assert hc.tuning()["prefill_q_split"] == forced
+        for x in (q, qf):
+            assert row_rel_err(run_gpu(hc, w, x), refs[id(x)]) <= TOL[kv]
+
+
 # Long prompt units cut into key pieces across workgroups (their partials merged per token), in
 # the geometries the planner's CPU test shows cut: checked against the oracle, with the same call
 # planned as whole units beside it.
 @pytest.mark.parametrize("kv,geo,prior,new,window,bt", SPLIT)
-@pytest.mark.parametrize("q_kind", ["rounded", "f32"])
+@pytest.mark.parametrize("q_kind", ["rounded", "f32", "f32_split"])
 def test_prefill_key_pieces(cuda, kv, geo, prior, new, window, bt, q_kind):
     w = small("k", kv, Layer(*geo), prior, new, window=window, seed=53, block_tokens=bt)
     hc, oc, q = pair(w)
-    if q_kind == "f32":   # bits below f16 / bf16: the two-pass path
+    if q_kind != "rounded":   # bits below f16 / bf16: two passes, or (_split) one of hi + lo products
         q = np.random.default_rng(9).standard_normal(q.shape).astype(np.float32)
+    if q_kind == "f32_split":
+        hc.set_tuning(prefill_q_split=2)
     got = run_gpu(hc, w, q)
     hc.set_tuning(prefill_whole_units=True)
     whole = run_gpu(hc, w, q)

@@ -50,6 +50,10 @@ def draw(seed):
     elif r < 0.5:
         tuning = {"prefill_whole_units": True}
     q_f32 = rng.random() < 0.3
+    # the prefill launch for Q forms (drawn last, so the earlier draws stay those of the seed)
+    q_split = int(rng.integers(0, 3))
+    if q_split:
+        tuning = dict(tuning, prefill_q_split=q_split)
     return kv, geo, bt, window, prior, new, tuning, q_f32
 
 
