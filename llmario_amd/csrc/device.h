@@ -103,13 +103,14 @@ constexpr uint32_t ROPE_MAX_DIM = 512;  // largest hd / hdv the fused kernel sta
 
 // Benchmark timing: a launch may carry a start / stop event pair that its own dispatch records
 // (hipExtLaunchKernel), so the measured interval is the kernel alone, without event packets queued
-// around it. Null events: an ordinary launch.
+// around it. Null events: an ordinary launch. A pair of launches bracketed by one pair of events
+// passes the start to the first launch and the stop to the second (either may be null alone).
 struct LaunchEv {
   hipEvent_t start = nullptr, stop = nullptr;
 };
 #define LMH_LAUNCH(ev, kernel, grid, block, lds, stream, ...)                                             \
   do {                                                                                                    \
-    if ((ev).start)                                                                                       \
+    if ((ev).start || (ev).stop)                                                                          \
       hipExtLaunchKernelGGL(kernel, grid, block, lds, stream, (ev).start, (ev).stop, 0u, __VA_ARGS__);     \
     else                                                                                                  \
       hipLaunchKernelGGL(kernel, grid, block, lds, stream, __VA_ARGS__);                                  \

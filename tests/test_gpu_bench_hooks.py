@@ -77,3 +77,28 @@ def test_tuning_read_back_changes_nothing(cuda):
     assert kt["decode"][1] == 1 and kt["merge"][1] == 0, kt
     ref = oc.attend(0, w.segments(), q, w.scale, 0, 4)
     assert row_rel_err(out.cpu().numpy(), ref) <= TOL["f32"]
+
+
+def test_kernel_time_brackets_both_merge_launches(cuda):
+    """A call whose prompt units are cut into key pieces beside split decode rows merges in two
+    launches (prompt tokens, then decode rows) timed as one interval: the start event goes with
+    the first launch and the stop event with the second, so the interval can be read."""
+    import torch
+
+    from conftest import TOL, row_rel_err
+    from llmario_amd.kv import Layer
+    from llmario_amd.workloads import small
+    from test_gpu_parity import pair, run_gpu
+    import oracle as O
+
+    w = small("m2", "f16", Layer(40, 8, 128, 128), prior=[4095, 300, 2000], new=[64, 1, 1], seed=5)
+    hc, oc, q = pair(w)
+    hc.set_tuning(decode_min_tiles=1, decode_target_items=100000)   # every decode row split
+    hc.kernel_times()
+    hc.set_timing(True)
+    got = run_gpu(hc, w, q)
+    kt = hc.kernel_times()
+    hc.set_timing(False)
+    assert kt["mixed"][1] == 1 and kt["merge"][1] == 1 and kt["merge"][0] > 0, kt
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, 4)
+    assert row_rel_err(got, ref) <= TOL["f16"]
