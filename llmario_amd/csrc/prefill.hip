@@ -19,7 +19,10 @@
 // in the page layout, which already holds each 16-token tile in MFMA operand order. bf16 V is
 // widened to f16 in LDS once per tile by the thread that loaded it (exact for |x| in
 // [2^-14, 65504]); bf16 K too when Q is not exact in bf16 (Q then runs as f16 hi + lo parts), while
-// a Q exact in bf16 multiplies bf16 K as it is. Q stays unscaled; each column's reference max
+// a Q exact in bf16 multiplies bf16 K as it is. A Q with bits below the page type runs, in the
+// launch for exact Q, as two passes of 16 columns per wave; the QS launch (chosen per call from
+// the previous launch's Q) runs every unit as one pass whose Q.K products are the hi part then the
+// lo part into one accumulator. Q stays unscaled; each column's reference max
 // enters (negated) as the initial accumulator of Q.K, so a product is s - m and its weight one fma
 // and one exp2 away. The reference max moves lazily (a lane's weight sum past a bound sends the
 // wave to a rare path that reduces the column max), so the O accumulators are almost never
@@ -373,10 +376,11 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
   // unscaled: a Q held in f16 or bf16 values (activations already rounded to the cache's 16-bit
   // type) is then exact in f16, and the products are exact against exactly represented K; the
   // scale multiplies the accumulator in the exponent. A Q with bits below f16 splits into
-  // hi + lo f16 parts (~22 bits) whose products sum in one accumulator: when any lane of the
-  // workgroup has a nonzero lo part, the unit runs in two passes of 16 columns per wave, the
-  // second column block's registers holding the first's lo part (same registers, same products
-  // per pass, twice the passes).
+  // hi + lo f16 parts (~22 bits) whose products sum in one accumulator: in the launch for exact Q,
+  // when any lane of the workgroup has a nonzero lo part, the unit runs in two passes of 16
+  // columns per wave, the second column block's registers holding the first's lo part (same
+  // registers, same products per pass, twice the passes); the QS launch holds both blocks' lo
+  // parts too (ql) and runs one pass.
   auto load_q = [&](uint32_t c, float4 (&raw)[NC][2]) {
     const uint32_t t = (c + c_off) / G, hh = (c + c_off) % G;
     const bool valid = c < n_col;
@@ -406,9 +410,9 @@ __device__ __forceinline__ void prefill_wg(const PageGeom& g, const PrefillGeom&
     return nz;
   };
   // bf16 pages: a Q held in bf16 values multiplies bf16 K exactly on the bf16 matrix cores, so K
-  // needs no widening; qf then holds bf16 bits (split_q_bf16). Any other Q takes the two-pass f16
-  // hi + lo path with K widened. q8_0 pages: the codes are widened to f16 either way; a Q exact in
-  // f16 runs one pass.
+  // needs no widening; qf then holds bf16 bits (split_q_bf16). Any other Q takes the f16 hi + lo
+  // path with K widened (two passes, or one in the QS launch). q8_0 pages: the codes are widened
+  // to f16 either way; a Q exact in f16 runs one pass.
   // A value is exact in bf16 when the low 16 bits of its f32 encoding are zero: the test ORs the
   // encodings and the bf16 values are their upper halves (one byte permute per pair); the values are
   // only used when every one was exact (otherwise the unit takes the two-pass path).
