@@ -48,28 +48,54 @@ constexpr double PF_MERGE_LAUNCH = 1.5;
 #endif
 constexpr double PF_CUT_GAIN = LMH_PF_CUT_GAIN;
 
-// Whole units grouped per workgroup, longest-processing-time-first: units by decreasing cost,
-// each to the currently least loaded workgroup. Returns the largest workgroup load.
-double assign_whole_units(const std::vector<PfUnit>& units, uint32_t slots, std::vector<std::vector<PrefillItem>>& lists) {
+// Prefill items per workgroup in the order they were added, as (workgroup, item) pairs appended to
+// two flat arrays: a call lists ~1,000 units over ~256 workgroups, and one vector per workgroup
+// cost more host time in allocations than the planning itself.
+struct WgLists {
+  uint32_t n_wg = 0;
+  std::vector<uint32_t> wg;
+  std::vector<PrefillItem> it;
+  void reset(uint32_t n, size_t cap) {
+    n_wg = n;
+    wg.clear();
+    it.clear();
+    wg.reserve(cap);
+    it.reserve(cap);
+  }
+  void push(uint32_t b, const PrefillItem& x) {
+    wg.push_back(b);
+    it.push_back(x);
+  }
+};
+
+// Whole units grouped per workgroup, longest-processing-time-first: units by decreasing cost (ties
+// in list order), each to the currently least loaded workgroup (ties to the lower index). Returns
+// the largest workgroup load. The loads live in a binary min-heap of (load, workgroup) whose top
+// is updated in place; the pairs are distinct, so the least one, and with it the plan, does not
+// depend on how the heap orders equal loads.
+double assign_whole_units(const std::vector<PfUnit>& units, uint32_t slots, WgLists& lists) {
   const uint32_t n_wg = (uint32_t)std::min<uint64_t>(units.size(), std::max<uint32_t>(slots, 1));
-  lists.assign(n_wg, {});
-  std::vector<uint32_t> order(units.size());
-  for (uint32_t i = 0; i < order.size(); i++) order[i] = i;
-  std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) { return units[a].cost() > units[b].cost(); });
-  std::priority_queue<std::pair<double, uint32_t>, std::vector<std::pair<double, uint32_t>>,
-                      std::greater<std::pair<double, uint32_t>>> load;
-  for (uint32_t b = 0; b < n_wg; b++) load.push({0.0, b});
-  for (uint32_t i : order) {
-    auto [l, b] = load.top();
-    load.pop();
-    lists[b].push_back(units[i].it);
-    load.push({l + units[i].cost(), b});
+  lists.reset(n_wg, units.size());
+  std::vector<std::pair<double, uint32_t>> order(units.size());
+  for (uint32_t i = 0; i < order.size(); i++) order[i] = {-units[i].cost(), i};
+  std::sort(order.begin(), order.end());
+  std::vector<std::pair<double, uint32_t>> heap(n_wg);
+  for (uint32_t b = 0; b < n_wg; b++) heap[b] = {0.0, b};   // ascending: already a heap
+  for (const auto& oi : order) {
+    const PfUnit& u = units[oi.second];
+    lists.push(heap[0].second, u.it);
+    heap[0].first += u.cost();
+    for (size_t j = 0;;) {   // sift the grown top down
+      const size_t c = 2 * j + 1;
+      if (c >= heap.size()) break;
+      const size_t m = c + 1 < heap.size() && heap[c + 1] < heap[c] ? c + 1 : c;
+      if (!(heap[m] < heap[j])) break;
+      std::swap(heap[m], heap[j]);
+      j = m;
+    }
   }
   double mx = 0.0;
-  while (!load.empty()) {
-    mx = std::max(mx, load.top().first);
-    load.pop();
-  }
+  for (const auto& h : heap) mx = std::max(mx, h.first);
   return mx;
 }
 
@@ -100,6 +126,10 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   const bool pf_ok = in.scale > 0.f && in.layout == LAYOUT_TILES && in.prefill_supported;
   if (pf_ok) {
     std::vector<PfUnit> units;
+    uint64_t n_units = 0;
+    for (uint64_t i = 0; i < in.n_segs; i++)
+      if (in.segs[i].n >= pf_min) n_units += (in.segs[i].n * group + in.unit_cols - 1) / in.unit_cols * in.n_kv;
+    units.reserve(n_units);
     for (uint64_t i = 0; i < in.n_segs; i++) {
       const lmh_seg& sg = in.segs[i];
       if (sg.n < pf_min) continue;
@@ -151,7 +181,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
       slots = std::min<uint32_t>(slots - 1, std::max<uint32_t>(1, (uint32_t)(slots * share + 0.5)));
     }
     if (in.prefill_workgroups) slots = (uint32_t)std::min<uint64_t>(in.prefill_workgroups, slots);
-    std::vector<std::vector<PrefillItem>> lists;
+    WgLists lists;
     // Whole units (longest first, each to the least loaded workgroup), unless cutting is estimated
     // to finish well ahead: then the concatenated tiles of all units are cut into one stretch per
     // workgroup (stream-K), a unit spanning several workgroups running as key pieces that each leave
@@ -186,8 +216,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
     const size_t pf_slot_bytes = (size_t)ng * (in.hdv + 4) * 4;   // a slot holds the group's heads (ng = group)
     // a unit's pieces (workgroup, first tile) into the lists; a unit of several pieces gets a
     // partial slot per (token, piece) and its merges
-    auto emit_pieces = [&](const PfUnit& u, const std::vector<std::pair<uint32_t, uint32_t>>& pieces,
-                           std::vector<std::vector<PrefillItem>>& lists) {
+    auto emit_pieces = [&](const PfUnit& u, const std::vector<std::pair<uint32_t, uint32_t>>& pieces) {
       const uint32_t k = (uint32_t)pieces.size();
       const uint32_t base = o.slots;
       if (k > 1) {
@@ -203,7 +232,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
         it.n_pages = std::min(u.it.n_pages, 4 * b) - 4 * a;
         it.slot = k > 1 ? base + s : NO_SLOT;
         it.slot_stride = k > 1 ? k : 0;
-        lists[pieces[s].first].push_back(it);
+        lists.push(pieces[s].first, it);
       }
     };
     if (try_cut) {
@@ -291,21 +320,24 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
                            (decode_tiles == 0 && partials > 0 ? PF_MERGE_LAUNCH : 0.0);
       const double cut_load = *std::max_element(load.begin(), load.end()) + merge;
       if (fits && cut_load < PF_CUT_GAIN * whole) {
-        lists.assign(n_wg, {});
-        for (size_t ui = 0; ui < units.size(); ui++) emit_pieces(units[ui], cuts[ui], lists);
-        while (!lists.empty() && lists.back().empty()) lists.pop_back();
+        lists.reset(n_wg, units.size() + n_wg);
+        for (size_t ui = 0; ui < units.size(); ui++) emit_pieces(units[ui], cuts[ui]);
+        lists.n_wg = 0;   // workgroups past the last one given a piece stay unlaunched
+        for (uint32_t b : lists.wg) lists.n_wg = std::max(lists.n_wg, b + 1);
       }
     }
-    o.pf_wg = (uint32_t)lists.size();
-    for (const auto& li : lists) o.pf_per_wg = std::max<uint32_t>(o.pf_per_wg, (uint32_t)li.size());
+    // pf_wg lists of pf_per_wg items, each workgroup's items in the order they were added
+    o.pf_wg = lists.n_wg;
+    std::vector<uint32_t> fill(o.pf_wg, 0);
+    for (uint32_t b : lists.wg) o.pf_per_wg = std::max(o.pf_per_wg, ++fill[b]);
     o.pitems.assign((size_t)o.pf_wg * o.pf_per_wg, PrefillItem{});
-    for (uint32_t b = 0; b < o.pf_wg; b++) {
-      for (size_t j = 0; j < lists[b].size(); j++) {
-        PrefillItem it = lists[b][j];
-        for (uint32_t i = 0; i < 8; i++) it.blk[i] = blk_at(it.seq, (uint64_t)(it.page0 + std::min(i, it.n_pages - 1)) << 4);
-        o.max_pages = std::max(o.max_pages, it.n_pages);
-        o.pitems[(size_t)b * o.pf_per_wg + j] = it;
-      }
+    std::fill(fill.begin(), fill.end(), 0u);
+    for (size_t k = 0; k < lists.wg.size(); k++) {
+      const uint32_t b = lists.wg[k];
+      PrefillItem it = lists.it[k];
+      for (uint32_t i = 0; i < 8; i++) it.blk[i] = blk_at(it.seq, (uint64_t)(it.page0 + std::min(i, it.n_pages - 1)) << 4);
+      o.max_pages = std::max(o.max_pages, it.n_pages);
+      o.pitems[(size_t)b * o.pf_per_wg + fill[b]++] = it;
     }
     if (in.prefill_lds_fixed + (size_t)o.pf_per_wg * sizeof(PrefillItem) + (size_t)o.max_pages * 4 > in.lds_limit) {
       // key ranges too long to list in LDS: those segments go through the decode kernel
