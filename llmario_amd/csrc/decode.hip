@@ -239,6 +239,63 @@ void decode_mfma_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t
   if (wi < n_items) decode_item<KVT, HD, HDV>(g, r, items, wi, q, out, part);
 }
 
+// Matrix-core decode whose split rows merge inside their workgroup: a row's items (1, 2 or 4) are
+// consecutive waves of one workgroup (the planner never lets a group cross one). Each split wave
+// leaves its partial in LDS; after the barrier, wave s of a group of n folds the group's partials
+// (forward.rs:772-806's log-sum-exp merge) for the O blocks j = s, s + n, .. and writes them. No
+// partials go to HBM and the call needs no merge launch. Instances: decode_mfma_local_ok.
+static_assert(WAVES == MFMA_LOCAL_WAVES, "the planner's local groups fill the decode kernel's workgroups");
+template <int KVT, int HD, int HDV>
+constexpr bool mfma_local_ok() {
+  return KVT != KV_F32 && HD == HDV && (HD == 64 || HD == 128);
+}
+
+template <int KVT, int HD, int HDV>
+__global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD, HDV>(), waves_per_eu<HD, HDV>())))
+void decode_mfma_local_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q,
+                              float* out, float* part, MergeCopy mc) {
+  constexpr int NJ = HDV / 16, LF = local_partial_floats<HDV>();
+  __shared__ __align__(16) float lp[WAVES * LF];
+  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const uint32_t wi = blockIdx.x * WAVES + w;
+  copy_merges(mc, blockIdx.x, gridDim.x);
+  if (wi < n_items) decode_item<KVT, HD, HDV, true>(g, r, items, wi, q, out, part, lp);
+  __syncthreads();   // every wave of the workgroup, with an item or not
+  if (wi >= n_items) return;
+  const uint32_t slot = __builtin_amdgcn_readfirstlane(items[wi].slot);
+  if (slot == NO_SLOT || (slot & LOCAL_SLOT) == 0) return;
+  const uint32_t row = __builtin_amdgcn_readfirstlane(items[wi].row);
+  const uint32_t kvh = __builtin_amdgcn_readfirstlane(items[wi].kvh);
+  const uint32_t h0 = __builtin_amdgcn_readfirstlane(items[wi].h0);
+  const uint32_t s = (slot >> 8) & 0x7fu, n = slot & 0xffu;
+  if (s >= n || s > w || w - s + n > (uint32_t)WAVES) return;   // a group inside the workgroup (the planner's)
+  const float* grp0 = lp + (w - s) * LF;   // the group's first wave
+  const uint32_t hq = lane & 15u, grp = lane >> 4;
+  float M = -INFINITY;
+  for (uint32_t k = 0; k < n; k++) M = fmaxf(M, grp0[k * LF + NJ * 256 + hq]);
+  float c[WAVES], L = 0.f;
+#pragma unroll
+  for (int k = 0; k < WAVES; k++) {
+    c[k] = 0.f;
+    if ((uint32_t)k < n) {
+      const float ms = grp0[k * LF + NJ * 256 + hq];
+      c[k] = ms == -INFINITY ? 0.f : exp2_fast(ms - M);
+      L = fmaf(c[k], grp0[k * LF + NJ * 256 + 16 + hq], L);
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  if (hq >= r.ng || h0 + hq >= r.group) return;
+  float* op = out + ((size_t)row * r.n_head + kvh * r.group + h0 + hq) * HDV + 4 * grp;
+  for (uint32_t j = s; j < (uint32_t)NJ; j += n) {
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < WAVES; k++)
+      if ((uint32_t)k < n) acc += c[k] * *(const f4*)(grp0 + k * LF + (j * 64 + lane) * 4);
+    acc *= inv;
+    *(float4*)(op + 16 * j) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
 // ---- f32 pages: VALU path ----------------------------------------------------------------------
 // NG: query heads per item (the launch's ng when the group is 1, 2, 4 or 8; 16 otherwise, with a
 // run-time guard for a last head block shorter than 16), so the per-head loops carry no guards
@@ -636,6 +693,14 @@ hipError_t launch_one(const PageGeom& g, const RowGeom& r, const DecodeItem* ite
       case 8: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 8>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
       default: LMH_LAUNCH(ev, (decode_f32_kernel<HD, HDV, 16>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc); break;
     }
+  } else if (r.local_merge) {   // the planner's groups of at most MFMA_LOCAL_WAVES (= WAVES) items
+    if constexpr (mfma_local_ok<KVT, HD, HDV>()) {
+      if (r.local_merge != (uint32_t)WAVES) return hipErrorInvalidValue;
+      LMH_LAUNCH(ev, (decode_mfma_local_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part,
+                 mc);
+    } else {
+      return hipErrorInvalidValue;
+    }
   } else {
     LMH_LAUNCH(ev, (decode_mfma_kernel<KVT, HD, HDV>), grid, block, 0, s, g, r, items, n_items, q, out, part, mc);
   }
@@ -790,6 +855,14 @@ bool decode_local_merge_ok(uint32_t hd, uint32_t hdv, uint32_t group) {
            : n == 8 ? f32_local_ok<H, H, 8>() : f32_local_ok<H, H, 16>();
   LMH_LOK(64) LMH_LOK(128) LMH_LOK(256)
 #undef LMH_LOK
+  return false;
+}
+
+bool decode_mfma_local_ok(uint32_t kv_type, uint32_t hd, uint32_t hdv) {
+#define LMH_MLOK(T)                                                                                       \
+  if (kv_type == T) return (hd == 64 && hdv == 64) ? mfma_local_ok<T, 64, 64>() : (hd == 128 && hdv == 128) ? mfma_local_ok<T, 128, 128>() : false;
+  LMH_MLOK(KV_F16) LMH_MLOK(KV_BF16) LMH_MLOK(KV_Q8)
+#undef LMH_MLOK
   return false;
 }
 

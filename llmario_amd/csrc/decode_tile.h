@@ -161,11 +161,21 @@ __device__ inline void copy_merges(const MergeCopy& mc, uint32_t block, uint32_t
   for (uint32_t i = block * blockDim.x + threadIdx.x; i < mc.n_words; i += stride) mc.dst[i] = mc.src[i];
 }
 
+// Floats of a wave's partial in LDS when a row's split items merge inside their workgroup: the
+// O^T blocks lane-major (a float4 per lane and 16-dim block, as the accumulators hold them), then
+// m and l of the 16 heads.
+template <int HDV>
+constexpr int local_partial_floats() {
+  return (HDV / 16) * 256 + 32;
+}
+
 // One decode work item, items[wi], computed by the calling wave: the partial (o, m, l) to
-// `part` for a split item, else the normalised output row to `out`.
-template <int KVT, int HD, int HDV>
+// `part` for a split item, else the normalised output row to `out`. LOCAL: an item whose slot is
+// LOCAL_SLOT | ... leaves its partial in the wave's share of `lds` (local_partial_floats floats
+// per wave) for the workgroup's merge instead.
+template <int KVT, int HD, int HDV, bool LOCAL = false>
 __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r, const DecodeItem* items, uint32_t wi,
-                                            const float* q, float* out, float* part) {
+                                            const float* q, float* out, float* part, float* lds = nullptr) {
   constexpr int NC = HD / 32;    // Q.K chunks of 32 dims
   constexpr int NJ = HDV / 16;   // O^T blocks of 16 dims
   constexpr bool Q8 = KVT == KV_Q8;
@@ -409,6 +419,18 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   }
   lsum = xsum_groups(lsum);
 
+  if constexpr (LOCAL) {
+    if (it.slot != NO_SLOT && (it.slot & LOCAL_SLOT) != 0) {
+      float* lw = lds + (threadIdx.x >> 6) * local_partial_floats<HDV>();
+#pragma unroll
+      for (int j = 0; j < NJ; j++) *(f4*)(lw + (j * 64 + lane) * 4) = O[j];
+      if (grp == 0) {
+        lw[NJ * 256 + hq] = m - pup;   // the reference the weights were taken against
+        lw[NJ * 256 + 16 + hq] = lsum;
+      }
+      return;
+    }
+  }
   if (it.slot == NO_SLOT) {
     if (!hv) return;
     const float inv = 1.0f / lsum;

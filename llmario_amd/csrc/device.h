@@ -75,7 +75,7 @@ struct RowGeom {
   uint32_t ng;             // heads per item = min(group, 16)
   float scale_log2;        // scale * log2(e): scores kept in the log2 domain
   uint32_t window;         // 0 = none
-  uint32_t local_merge;    // f32 decode: split rows merge inside their workgroup (slots LOCAL_SLOT | ...)
+  uint32_t local_merge;    // decode: 0, or split rows merge inside workgroups of this many waves (slots LOCAL_SLOT | ...)
 };
 
 struct PrefillGeom {
@@ -172,6 +172,9 @@ bool decode_tiles_supported(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 uint32_t decode_rows_max_heads();
 // f32 decode: the calls whose split rows may merge inside their workgroup (tile layout instances).
 bool decode_local_merge_ok(uint32_t hd, uint32_t hdv, uint32_t group);
+// matrix-core decode (f16 / bf16 / q8_0 pages): an instance whose split rows (up to 4 items, the
+// waves of one workgroup) merge inside their workgroup
+bool decode_mfma_local_ok(uint32_t kv_type, uint32_t hd, uint32_t hdv);
 
 // Prefill (multi-token segments on matrix cores): n_wg workgroups, workgroup b runs the units
 // items[b * per_wg ..] up to the first with n_tok == 0. `max_pages` bounds the key pages of any unit.

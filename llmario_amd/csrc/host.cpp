@@ -1394,6 +1394,7 @@ static void fill_kernel_facts(PlanIn& in, uint32_t kv_type, uint32_t hd, uint32_
   in.lds_limit = 160 * 1024;
   in.rows_max_heads = decode_rows_max_heads();
   in.local_merge_ok = decode_local_merge_ok(hd, hdv, group);
+  in.mfma_local_ok = decode_mfma_local_ok(kv_type, hd, hdv);
 }
 
 // lmh_attend and lmh_attend_noalloc. noalloc: split-K partials and the merge list go to the
@@ -1459,7 +1460,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   PlanOut& pl = kv->plan;
   plan_attend(pin, pl);
   const uint32_t ng = pl.ng, slots = pl.slots, pf_wg = pl.pf_wg, pf_per_wg = pl.pf_per_wg, max_pages = pl.max_pages;
-  const bool local = pl.local;
+  const bool local = pl.local != 0;
   const size_t slot_bytes = (size_t)ng * (y.hdv + 4) * 4;
   if ((rc = kv->flush(st)) != LMH_OK) return rc;
   const size_t items_bytes = kv->plan.items.size() * sizeof(DecodeItem);
@@ -1507,7 +1508,7 @@ static int32_t attend_impl(lmh_kv* kv, uint32_t layer, const lmh_seg* segs, uint
   r.ng = ng;
   r.scale_log2 = scale * 1.4426950408889634f;
   r.window = (uint32_t)std::min<uint64_t>(window, 0xffffffffull);
-  r.local_merge = local ? 1u : 0u;
+  r.local_merge = pl.local;   // 0, or the waves per workgroup of a local-merge launch
   PrefillGeom pg{};
   pg.n_head = y.n_head;
   pg.group = group;
@@ -1689,7 +1690,7 @@ int32_t lmh_plan_attend(const lmh_plan_desc* d, const lmh_seg* segs, uint64_t n_
   counts->pf_wg = o.pf_wg;
   counts->pf_per_wg = o.pf_per_wg;
   counts->max_pages = o.max_pages;
-  counts->local = o.local ? 1u : 0u;
+  counts->local = o.local;
   counts->layout = in.layout;
   counts->chunk = o.chunk;
   if (o.items.size() > items_cap || o.merges.size() > merges_cap || o.pitems.size() > units_cap)

@@ -113,7 +113,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   o.merges.clear();
   o.pitems.clear();
   o.slots = o.pf_wg = o.pf_per_wg = o.max_pages = 0;
-  o.local = false;
+  o.local = 0;
   auto blk_at = [&](uint64_t seq, uint64_t p) {   // block id of the tile holding key p
     return (uint32_t)in.table[seq * in.bps + (((p >> 4) << 4) >> in.bt_shift)];
   };
@@ -394,16 +394,32 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   uint64_t chunk = std::min<uint64_t>(64, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / target));
   while (chunk < 64 && n_items_for(chunk) > target) chunk++;
   o.chunk = (uint32_t)chunk;
-  // f32 pages, short rows (at most 16 tiles): a row's split items are consecutive waves of one
-  // 8-wave workgroup and merge there (no merge launch). A row splits into 1, 2, 4 or 8 items of
-  // at most 2 tiles (the f32 kernel's smallest chunk); groups of 8 go first, then 4, 2 and single
-  // items, so no group crosses a workgroup. Not with explicit split settings.
-  if (in.layout == LAYOUT_TILES && in.kv_type == LMH_KV_F32 && in.local_merge_ok && !in.decode_target_items &&
-      !in.decode_min_tiles) {
+  // Split rows that merge inside their workgroup (no partials in HBM, no merge launch). A row's
+  // split count n is 1, 2, 4 or 8 and its items are consecutive waves of one workgroup: groups of
+  // 8 go first, then 4, 2 and single items, so no group crosses a workgroup. Not with explicit
+  // split settings.
+  //  - f32 pages, short rows (at most 16 tiles): 8-wave workgroups; a row splits into items of at
+  //    most 2 tiles (the f32 kernel's smallest chunk).
+  //  - matrix-core pages, a call of decode rows alone whose rows split at most 4 ways at the
+  //    chunk above: the kernel's 4-wave workgroups; a row's split count rounded up to 1, 2 or 4
+  //    (items of (chunk/2, chunk] tiles; every item still resident in one round: at most 4/3 of
+  //    the target of half the capacity).
+  uint64_t (*split_of)(uint64_t n_t, uint64_t chunk) = nullptr;
+  if (in.layout == LAYOUT_TILES && !in.decode_target_items && !in.decode_min_tiles) {
     uint64_t max_nt = 0;
     for (uint64_t t = 0; t < n_rows; t++)
       if (o.decode_row[t]) max_nt = std::max<uint64_t>(max_nt, row_tiles(t));
-    o.local = max_nt > 2 && max_nt <= 16;
+    if (in.kv_type == LMH_KV_F32 && in.local_merge_ok && max_nt > 2 && max_nt <= 16) {
+      o.local = LOCAL_WAVES;
+      split_of = [](uint64_t n_t, uint64_t) -> uint64_t { return n_t <= 2 ? 1 : n_t <= 4 ? 2 : n_t <= 8 ? 4 : 8; };
+    } else if (mfma_decode && in.mfma_local_ok && o.pitems.empty() && max_nt > chunk &&
+               (max_nt + chunk - 1) / chunk <= (uint64_t)MFMA_LOCAL_WAVES) {
+      o.local = MFMA_LOCAL_WAVES;
+      split_of = [](uint64_t n_t, uint64_t c) -> uint64_t {
+        const uint64_t k = (n_t + c - 1) / c;
+        return k <= 1 ? 1 : k <= 2 ? 2 : 4;
+      };
+    }
   }
   if (o.local) {
     std::vector<DecodeItem> by_size[4];   // groups of 8, 4, 2, single items
@@ -412,7 +428,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
       const uint64_t pos = (uint64_t)in.row_pos[t];
       const uint64_t lo = key_lo(pos, window), hi = pos + 1;
       const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
-      const uint32_t n = n_t <= 2 ? 1 : n_t <= 4 ? 2 : n_t <= 8 ? 4 : 8;
+      const uint32_t n = (uint32_t)split_of(n_t, chunk);
       std::vector<DecodeItem>& dst = by_size[n == 8 ? 0 : n == 4 ? 1 : n == 2 ? 2 : 3];
       const uint32_t seq = (uint32_t)in.row_seq[t];
       for (uint32_t kvh = 0; kvh < in.n_kv; kvh++) {

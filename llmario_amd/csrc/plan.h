@@ -47,6 +47,7 @@ struct PlanIn {
   size_t lds_limit = 160 * 1024;
   uint32_t rows_max_heads = 4;      // query heads per item of the row-layout kernel
   bool local_merge_ok = false;      // f32 decode: split rows may merge inside their workgroup
+  bool mfma_local_ok = false;       // matrix-core decode: the same, for rows split at most 4 ways
 };
 
 struct PlanOut {
@@ -58,7 +59,7 @@ struct PlanOut {
   uint32_t slots = 0;                 // split-K partial slots
   uint32_t pf_wg = 0, pf_per_wg = 0, max_pages = 0;
   uint32_t chunk = 0;                 // decode split chunk (16-key tiles)
-  bool local = false;                 // decode items merge inside their workgroups
+  uint32_t local = 0;                 // decode items merge inside workgroups of this many waves (0: no)
 };
 
 // Segments of at least this many rows run on the matrix-core prefill kernel by default (Metal's

@@ -22,12 +22,17 @@ struct DecodeItem {
   uint32_t blk0;  // block id of the first tile p0 >> 4 (the first fetch skips the block-table read)
 };
 constexpr uint32_t NO_SLOT = 0xffffffffu;
-// A split item merged inside its workgroup (f32 decode of short rows): LOCAL_SLOT | (its index in
-// the row's group << 8) | the group's size; the group's items are consecutive waves of one
-// workgroup, and the first merges their partials from LDS, so the call needs no merge launch.
+// A split item merged inside its workgroup (f32 decode of short rows; matrix-core decode whose rows
+// split at most MFMA_LOCAL_WAVES ways): LOCAL_SLOT | (its index in the row's group << 8) | the
+// group's size; the group's items are consecutive waves of one workgroup, which merges their
+// partials from LDS, so the call needs no merge launch.
 constexpr uint32_t LOCAL_SLOT = 0x80000000u;
 constexpr uint32_t LOCAL_MERGE_MAX = 1024;   // heads x hdv of an item whose partials a wave keeps in LDS
-constexpr int LOCAL_WAVES = 8;               // waves per workgroup of a local-merge call (its largest group)
+constexpr int LOCAL_WAVES = 8;               // waves per workgroup of an f32 local-merge call (its largest group)
+// The same for the matrix-core decode kernel (its own 4-wave workgroups). Not 8-wave ones for rows
+// of up to 8 splits: c2 (rows of 512-4,096 keys) ran its 1,328 items on 166 such workgroups, the
+// CUs left idle slowed the kernel from 50.0 to 62.8 us, more than the merge launch costs.
+constexpr int MFMA_LOCAL_WAVES = 4;
 
 // Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, heads h0 ..
 // h0 + nh - 1). nh = 0 (a decode row's merge): up to the item's head count ng, head h0 + i at

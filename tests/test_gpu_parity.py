@@ -218,6 +218,44 @@ def test_attend_small(cuda, kv, layer, prior, new, window, bt, split):
     assert err <= TOL[kv], err
 
 
+# Matrix-core decode rows that split at most 4 ways (at the 8-tile chunk) merge inside their 4-wave
+# workgroup: rows of 1, 2, 3 (run as 4) and 4 splits in one decode launch and no merge launch,
+# against the oracle and against the same rows at the same chunk merged by the merge launch
+# (explicit split settings keep it). A group of 20 heads (two head blocks per KV head), hd 64,
+# q8_0, windows.
+LOCAL = [
+    ("f16", Layer(32, 8, 128, 128), [100, 200, 300, 500], 0),
+    ("bf16", Layer(40, 2, 128, 128), [500, 100, 300, 200, 0], 0),
+    ("q8_0", Layer(16, 4, 64, 64), [300, 450, 20], 0),
+    ("q8_0", Layer(32, 8, 128, 128), [250, 500], 0),
+    ("f16", Layer(16, 4, 64, 64), [900, 700, 60], 400),
+    ("bf16", Layer(16, 4, 64, 64), [1300, 700, 60, 0], 450),
+]
+
+
+@pytest.mark.parametrize("kv,layer,prior,window", LOCAL)
+def test_decode_split_rows_merge_in_workgroup(cuda, kv, layer, prior, window):
+    w = small("loc", kv, layer, prior, [1] * len(prior), window=window, seed=41)
+    hc, oc, q = pair(w)
+    hc.kernel_times()
+    hc.set_timing(True)
+    got = run_gpu(hc, w, q)
+    kt_local = hc.kernel_times()
+    hc.set_tuning(decode_min_tiles=8, decode_target_items=100000)
+    glob = run_gpu(hc, w, q)
+    kt_glob = hc.kernel_times()
+    hc.set_timing(False)
+    assert kt_local["decode"][1] == 1 and kt_local["merge"][1] == 0, kt_local
+    assert kt_glob["decode"][1] == 1 and kt_glob["merge"][1] == 1, kt_glob
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    assert np.isfinite(got).all()
+    err, err_glob, diff = row_rel_err(got, ref), row_rel_err(glob, ref), row_rel_err(got, glob)
+    print(f"{kv} {layer} prior={prior} window={window}: local {err:.3e} merge launch {err_glob:.3e} "
+          f"local vs merge launch {diff:.3e}")
+    assert err <= TOL[kv] and err_glob <= TOL[kv], (err, err_glob)
+    assert diff <= 2e-5, diff
+
+
 # Prompt units streamed through few workgroups: each workgroup runs many units (and two passes
 # per unit when Q has bits below the cache's 16-bit type) back to back, reusing its LDS stages,
 # block-id list and Q registers from one to the next. Segments of different lengths give units

@@ -100,13 +100,15 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
                 slots_seen.add(x)
     if c.local:
         assert len(merges) == 0
-        # a row's group is consecutive items within one 8-wave workgroup
+        # a row's group is consecutive items within one workgroup (c.local waves: 8 for f32
+        # pages, 4 for the matrix-core kernel)
+        assert c.local == (8 if kv == "f32" else 4)
         for i, it in enumerate(items):
             slot = int(it[5])
             if slot != NO_SLOT:
                 idx, n = (slot >> 8) & 0x7F, slot & 0xFF
                 first = i - idx
-                assert first // 8 == (first + n - 1) // 8
+                assert n <= c.local and first // c.local == (first + n - 1) // c.local
     dec_merges = set()
     for m in merges:
         row, kvh, h0, slot0, n_split, nh = (int(x) for x in m[:6])
@@ -225,8 +227,8 @@ def test_random_calls_plan_a_partition_of_the_work(seed):
 
 def test_configuration_shapes():
     """The benchmark configurations' calls plan as intended: c2's rows split into items of whole
-    tiles with merges; c3's prompts become prefill units only; c5 holds both kinds; chunk32k's eight
-    long units are cut into key pieces."""
+    tiles with merges (up to 8 per row: more than a workgroup merges); c3's prompts become prefill
+    units only; c5 holds both kinds; chunk32k's eight long units are cut into key pieces."""
     from llmario_amd.workloads import Generator, config
     for name in ["c1", "c2", "c3", "c4", "c5", "c5w", "chunk32k"]:
         w = config(name)
@@ -248,11 +250,44 @@ def test_configuration_shapes():
         if name in ("c5", "c5w"):
             assert len(items) > 0 and live_units > 0
         if name == "c2":
-            assert live_units == 0 and len(merges) > 0
+            assert live_units == 0 and c.local == 0 and len(merges) > 0
         cut = bool(len(units)) and bool((units[units[:, 4] != 0][:, 9] != NO_SLOT).any())
         # only the long-prefix chunk's few units are cut into key pieces (c5's are whole: cutting them
         # measured slower)
         assert cut == (name == "chunk32k"), name
+
+
+def test_decode_rows_of_few_splits_merge_in_their_workgroup():
+    """Matrix-core decode rows that split at most 4 ways at the chunk (8 tiles here) run as groups of
+    1, 2 or 4 items (3 splits run as 4), groups of 4 first, then 2, then single items, so none
+    crosses a 4-wave workgroup, and the call has no merges. Not beside prompt units (one mixed
+    launch), not with explicit split settings, not when a row needs more than 4 splits."""
+    prior = [100, 200, 300, 500]                       # 7, 13, 19, 32 tiles: 1, 2, 3, 4 splits
+    segs = [(s, s, 1, p) for s, p in enumerate(prior)]
+    table = contiguous_table([p + 1 for p in prior], 16)
+    items, merges, units, c = plan("f16", 32, 8, 128, 128, 16, table, segs)
+    check_plan("f16", 32, 8, 128, 128, 16, table, segs, 0, items, merges, units, c)
+    assert c.local == 4 and len(merges) == 0 and c.chunk == 8
+    sizes = [1 if int(x) == NO_SLOT else int(x) & 0xFF for x in items[:, 5]]
+    assert sizes == [4] * 64 + [2] * 16 + [1] * 8
+    assert [int(r) for r in items[:64:4, 0]] == [2] * 8 + [3] * 8   # rows 2 and 3 as groups of 4
+    # the same rows with explicit split settings: the merge launch, 3 splits for row 2
+    items, merges, units, c = plan("f16", 32, 8, 128, 128, 16, table, segs, decode_min_tiles=8,
+                                   decode_target_items=1000)
+    check_plan("f16", 32, 8, 128, 128, 16, table, segs, 0, items, merges, units, c)
+    assert c.local == 0 and len(items) == 80 and len(merges) == 24
+    # beside a prompt segment (one mixed launch): the merge launch
+    segs2 = segs + [(4, 4, 40, 0)]
+    table2 = contiguous_table([p + 1 for p in prior] + [40], 16)
+    items, merges, units, c = plan("f16", 32, 8, 128, 128, 16, table2, segs2)
+    check_plan("f16", 32, 8, 128, 128, 16, table2, segs2, 0, items, merges, units, c)
+    assert c.local == 0 and len(merges) > 0 and c.pf_wg > 0
+    # a row of 5 splits: the merge launch for all
+    segs3 = segs + [(4, 4, 1, 600)]                    # 38 tiles
+    table3 = contiguous_table([p + 1 for p in prior] + [601], 16)
+    items, merges, units, c = plan("f16", 32, 8, 128, 128, 16, table3, segs3)
+    check_plan("f16", 32, 8, 128, 128, 16, table3, segs3, 0, items, merges, units, c)
+    assert c.local == 0 and len(merges) > 0
 
 
 # Few long prompt units on many CUs: their key ranges are cut into pieces (stream-K), whose
