@@ -14,9 +14,11 @@ the same 297 MB) is reported beside it as `c2_warm`.
 Also reported (extra keys, each in isolation: a failing leg is recorded under `errors` and the
 headline line still prints): every other configuration's throughput and its launch roofline
 (max(bytes / HBM peak, FLOPs / MFMA peak) against the kernel time, with the decode and prefill
-parts of a mixed launch), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), c3's
+parts of a mixed launch), c2's geometry with every row at 2,048 keys, cold, whose rows split 4 ways
+and merge inside their workgroups (`c2u_cold`) and the same split merged by the merge launch
+(`c2u_merge_cold`), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), c3's
 prompts on q8_0 pages (`c3_q8`; `c3_q8_rows`: the same with every row sent to the decode kernels), c3
-with Q keeping all f32 bits (`c3_q_f32`: the prefill's two-pass path; every other leg's Q is rounded
+with Q keeping all f32 bits (`c3_q_f32`: Q as f16 hi + lo parts; every other leg's Q is rounded
 to the cache's 16-bit type), a 64-token prompt chunk on a 32k prefix with its prefill units cut into
 key pieces across the device (`chunk32k`) and kept whole (`chunk32k_whole`), the
 fused producer kernel (QK-norm + RoPE + K/V store, `rope_c3`) on c3's rows, snapshot write/read
@@ -44,6 +46,10 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0  # dense fp16/bf16
 FP32_PEAK_TFLOPS = 157.3
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_c2_traffic.json")
 COLD_LAYERS = 5   # c2_cold: 5 x 297 MB of K/V in rotation
+# The decode split target a 256-CU MI355X picks by itself for f16 / hd 128 (half of 8 items per CU),
+# set explicitly: the same chunks, but explicit split settings keep the merge launch (the A side of
+# the in-workgroup merge)
+MERGE_LAUNCH_TUNING = {"decode_target_items": 1024}
 
 
 def log(*a):
@@ -541,18 +547,19 @@ def main():
     # ~0.2 s of c2 steps: the clock needs tens of milliseconds of load to settle (10 warm-up steps
     # left the cold decode kernel at 52.7 us against 50.3 us settled)
     ap.add_argument("--warmup", type=int, default=3000)
-    ap.add_argument("--extra", default="c1,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c5,c5w,chunk32k,chunk32k_whole,"
-                                       "rope_c3,snapshot_c4,sched_c5,window_c5w",
+    ap.add_argument("--extra", default="c1,c2u_cold,c2u_merge_cold,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c5,c5w,"
+                                       "chunk32k,chunk32k_whole,rope_c3,snapshot_c4,sched_c5,window_c5w",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU baseline budget (c2 on all threads and on 1, c1 on both)")
     ap.add_argument("--layers", type=int, default=0,
-                    help="with --profile-config: layers in rotation (0 = 1, or COLD_LAYERS for c2_cold)")
+                    help="with --profile-config: layers in rotation (0 = 1, or COLD_LAYERS for a *_cold config)")
     ap.add_argument("--extra-warmup-s", type=float, default=0.2,
                     help="minimum warm-up time of the headline and of each extra configuration (clock ramp)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-config", default="",
-                    help="only time this one config (c1..c5, c5w, chunk32k; suffixes _q_f32, _p_f16, _rows, _whole) and print its result dict: the "
+                    help="only time this one config (c1..c5, c2u, c5w, chunk32k; suffixes _q_f32, _p_f16, _rows, _whole, "
+                         "_merge, and _cold last: layers in rotation) and print its result dict: the "
                          "command the rocprofv3 summaries under profiles/ were taken with")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run a plain device copy of this many MiB (20 launches): the known-size "
@@ -591,8 +598,10 @@ def main():
         return
     if args.profile_config:
         name, tuning, layers = args.profile_config, None, args.layers or 1
-        if name == "c2_cold":
-            name, layers = "c2", args.layers or COLD_LAYERS
+        if name.endswith("_cold"):
+            name, layers = name[:-len("_cold")], args.layers or COLD_LAYERS
+        if name.endswith("_merge"):
+            name, tuning = name[:-len("_merge")], MERGE_LAUNCH_TUNING
         elif name.endswith("_p_f16"):
             name, tuning = name[:-len("_p_f16")], {"prefill_p_f16": True}
         elif name.endswith("_rows"):
@@ -633,6 +642,12 @@ def main():
         # (units cut into key pieces across the device, partials merged)
         "chunk32k_whole": lambda: time_config("chunk32k", short, 3, warmup_s=args.extra_warmup_s,
                                               tuning={"prefill_whole_units": True}, label="chunk32k_whole"),
+        # rows of 2,048 keys, cold: each row's 4 split items merge inside their workgroup; beside
+        # it the same split at the same chunk merged by the merge launch
+        "c2u_cold": lambda: time_config("c2u", args.steps, 20, n_layers=COLD_LAYERS, label="c2u_cold",
+                                        warmup_s=args.extra_warmup_s),
+        "c2u_merge_cold": lambda: time_config("c2u", args.steps, 20, n_layers=COLD_LAYERS, label="c2u_merge_cold",
+                                              warmup_s=args.extra_warmup_s, tuning=MERGE_LAUNCH_TUNING),
         # c3 with Q keeping all f32 bits (the prefill's two passes: Q as f16 hi + lo)
         "c3_q_f32": lambda: time_config("c3", short, 3, warmup_s=args.extra_warmup_s, q_f32=True,
                                         label="c3_q_f32"),

@@ -117,7 +117,9 @@ class Workload:
 
 def config(name: str) -> Workload:
     """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096); c3_q8 is c3 on q8_0 pages;
-    chunk32k is a long-prefix prompt chunk (few, long prefill units: the key-piece case)."""
+    chunk32k is a long-prefix prompt chunk (few, long prefill units: the key-piece case); c2u is
+    c2's geometry with every row at 2,048 keys (rows that split 4 ways: the decode kernel's
+    in-workgroup merge)."""
     if name == "c1":
         return Workload("c1", "f32", Layer(8, 8, 64, 64), prior=[255], new=[1], seed=1)
     if name == "c2":
@@ -125,6 +127,8 @@ def config(name: str) -> Workload:
         ctx = rng.integers(512, 4096, size=32, endpoint=True)
         return Workload("c2", "f16", Layer(32, 8, 128, 128), prior=[int(c) - 1 for c in ctx], new=[1] * 32,
                         seed=2)
+    if name == "c2u":
+        return Workload("c2u", "f16", Layer(32, 8, 128, 128), prior=[2047] * 32, new=[1] * 32, seed=2)
     if name == "c3":
         return Workload("c3", "bf16", Layer(32, 8, 128, 128), prior=[0] * 4, new=[2048] * 4, seed=3)
     if name == "c3_q8":   # c3's prompts on a q8_0 cache (the planner's degraded KV type)

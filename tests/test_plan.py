@@ -227,10 +227,11 @@ def test_random_calls_plan_a_partition_of_the_work(seed):
 
 def test_configuration_shapes():
     """The benchmark configurations' calls plan as intended: c2's rows split into items of whole
-    tiles with merges (up to 8 per row: more than a workgroup merges); c3's prompts become prefill
-    units only; c5 holds both kinds; chunk32k's eight long units are cut into key pieces."""
+    tiles with merges (up to 8 per row: more than a workgroup merges); c2u's rows into 4 items each,
+    merged inside their workgroups; c3's prompts become prefill units only; c5 holds both kinds;
+    chunk32k's eight long units are cut into key pieces."""
     from llmario_amd.workloads import Generator, config
-    for name in ["c1", "c2", "c3", "c4", "c5", "c5w", "chunk32k"]:
+    for name in ["c1", "c2", "c2u", "c3", "c4", "c5", "c5w", "chunk32k"]:
         w = config(name)
         gen = Generator(w)
         bps = max(len(t) for t in gen.tables)
@@ -251,6 +252,8 @@ def test_configuration_shapes():
             assert len(items) > 0 and live_units > 0
         if name == "c2":
             assert live_units == 0 and c.local == 0 and len(merges) > 0
+        if name == "c2u":   # every row 4 items, merged inside its workgroup
+            assert live_units == 0 and c.local == 4 and len(merges) == 0 and len(items) == 32 * 8 * 4
         cut = bool(len(units)) and bool((units[units[:, 4] != 0][:, 9] != NO_SLOT).any())
         # only the long-prefix chunk's few units are cut into key pieces (c5's are whole: cutting them
         # measured slower)
