@@ -254,46 +254,12 @@ template <int KVT, int HD, int HDV>
 __global__ __launch_bounds__(64 * WAVES) __attribute__((amdgpu_waves_per_eu(waves_per_eu<HD, HDV>(), waves_per_eu<HD, HDV>())))
 void decode_mfma_local_kernel(PageGeom g, RowGeom r, const DecodeItem* items, uint32_t n_items, const float* q,
                               float* out, float* part, MergeCopy mc) {
-  constexpr int NJ = HDV / 16, LF = local_partial_floats<HDV>();
-  __shared__ __align__(16) float lp[WAVES * LF];
-  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-  const uint32_t wi = blockIdx.x * WAVES + w;
+  __shared__ __align__(16) float lp[WAVES * local_partial_floats<HDV>()];
+  const uint32_t wi = blockIdx.x * WAVES + (threadIdx.x >> 6);
   copy_merges(mc, blockIdx.x, gridDim.x);
   if (wi < n_items) decode_item<KVT, HD, HDV, true>(g, r, items, wi, q, out, part, lp);
   __syncthreads();   // every wave of the workgroup, with an item or not
-  if (wi >= n_items) return;
-  const uint32_t slot = __builtin_amdgcn_readfirstlane(items[wi].slot);
-  if (slot == NO_SLOT || (slot & LOCAL_SLOT) == 0) return;
-  const uint32_t row = __builtin_amdgcn_readfirstlane(items[wi].row);
-  const uint32_t kvh = __builtin_amdgcn_readfirstlane(items[wi].kvh);
-  const uint32_t h0 = __builtin_amdgcn_readfirstlane(items[wi].h0);
-  const uint32_t s = (slot >> 8) & 0x7fu, n = slot & 0xffu;
-  if (s >= n || s > w || w - s + n > (uint32_t)WAVES) return;   // a group inside the workgroup (the planner's)
-  const float* grp0 = lp + (w - s) * LF;   // the group's first wave
-  const uint32_t hq = lane & 15u, grp = lane >> 4;
-  float M = -INFINITY;
-  for (uint32_t k = 0; k < n; k++) M = fmaxf(M, grp0[k * LF + NJ * 256 + hq]);
-  float c[WAVES], L = 0.f;
-#pragma unroll
-  for (int k = 0; k < WAVES; k++) {
-    c[k] = 0.f;
-    if ((uint32_t)k < n) {
-      const float ms = grp0[k * LF + NJ * 256 + hq];
-      c[k] = ms == -INFINITY ? 0.f : exp2_fast(ms - M);
-      L = fmaf(c[k], grp0[k * LF + NJ * 256 + 16 + hq], L);
-    }
-  }
-  const float inv = L > 0.f ? 1.0f / L : 0.f;
-  if (hq >= r.ng || h0 + hq >= r.group) return;
-  float* op = out + ((size_t)row * r.n_head + kvh * r.group + h0 + hq) * HDV + 4 * grp;
-  for (uint32_t j = s; j < (uint32_t)NJ; j += n) {
-    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int k = 0; k < WAVES; k++)
-      if ((uint32_t)k < n) acc += c[k] * *(const f4*)(grp0 + k * LF + (j * 64 + lane) * 4);
-    acc *= inv;
-    *(float4*)(op + 16 * j) = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  }
+  if (wi < n_items) local_merge<HDV, WAVES>(r, items, wi, lp, out);
 }
 
 // ---- f32 pages: VALU path ----------------------------------------------------------------------

@@ -453,5 +453,48 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   }
 }
 
+// The workgroup-local merge (forward.rs:772-806's log-sum-exp merge) after decode_item<.., true>
+// and a barrier: a row's split items are consecutive waves of one W-wave workgroup (their slots
+// LOCAL_SLOT | index << 8 | count), each of which left its partial in its share of `lds`; wave s of
+// a group of n folds the group's partials for the O blocks j = s, s + n, .. and writes them.
+template <int HDV, int W>
+__device__ __forceinline__ void local_merge(const RowGeom& r, const DecodeItem* items, uint32_t wi, const float* lds,
+                                            float* out) {
+  constexpr int NJ = HDV / 16, LF = local_partial_floats<HDV>();
+  const uint32_t w = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+  const uint32_t slot = __builtin_amdgcn_readfirstlane(items[wi].slot);
+  if (slot == NO_SLOT || (slot & LOCAL_SLOT) == 0) return;
+  const uint32_t row = __builtin_amdgcn_readfirstlane(items[wi].row);
+  const uint32_t kvh = __builtin_amdgcn_readfirstlane(items[wi].kvh);
+  const uint32_t h0 = __builtin_amdgcn_readfirstlane(items[wi].h0);
+  const uint32_t s = (slot >> 8) & 0x7fu, n = slot & 0xffu;
+  if (s >= n || s > w || w - s + n > (uint32_t)W) return;   // a group inside the workgroup (the planner's)
+  const float* grp0 = lds + (w - s) * LF;   // the group's first wave
+  const uint32_t hq = lane & 15u, grp = lane >> 4;
+  float M = -INFINITY;
+  for (uint32_t k = 0; k < n; k++) M = fmaxf(M, grp0[k * LF + NJ * 256 + hq]);
+  float c[W], L = 0.f;
+#pragma unroll
+  for (int k = 0; k < W; k++) {
+    c[k] = 0.f;
+    if ((uint32_t)k < n) {
+      const float ms = grp0[k * LF + NJ * 256 + hq];
+      c[k] = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+      L = fmaf(c[k], grp0[k * LF + NJ * 256 + 16 + hq], L);
+    }
+  }
+  const float inv = L > 0.f ? 1.0f / L : 0.f;
+  if (hq >= r.ng || h0 + hq >= r.group) return;
+  float* op = out + ((size_t)row * r.n_head + kvh * r.group + h0 + hq) * HDV + 4 * grp;
+  for (uint32_t j = s; j < (uint32_t)NJ; j += n) {
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < W; k++)
+      if ((uint32_t)k < n) acc += c[k] * *(const f4*)(grp0 + k * LF + (j * 64 + lane) * 4);
+    acc *= inv;
+    *(float4*)(op + 16 * j) = make_float4(acc[0], acc[1], acc[2], acc[3]);
+  }
+}
+
 }  // namespace dtile
 }  // namespace lmh

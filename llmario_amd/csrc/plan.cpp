@@ -28,6 +28,12 @@ constexpr uint32_t PF_MIN_PIECE = LMH_PF_MIN_PIECE;
 // such tiles in ~50 us on 256 CUs, 0.34 CU-us each, at a 2.2-us tile: 0.16; CUs that share HBM
 // with prefill work stream faster each).
 constexpr double DECODE_TILE_COST = 0.1;
+// A decode item's own time per 16-key tile, in the same units: a wave streams a tile in ~1.2 us
+// (8 KiB per 16-key tile at the ~7 GB/s one wave's two-deep prefetch sustains).
+constexpr double DECODE_WAVE_TILE = 0.5;
+// A mixed launch's decode chunk may grow (so split rows merge inside their workgroups) while its
+// longest item stays within this fraction of the prefill part's largest workgroup load.
+constexpr double MIXED_DECODE_SLACK = 0.75;
 
 struct PfUnit {
   PrefillItem it;   // page0 / n_pages: the whole unit's key pages
@@ -122,6 +128,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   // Per segment and KV head, the (token, query head) columns are packed token-major in units of
   // unit_cols (a unit may start mid-token, so no unit is a remnant of a few columns); a unit's keys
   // are the pages from its first token's range start to its last token.
+  double pf_load = 0.0;   // the prefill part's largest workgroup load (estimate)
   const uint64_t pf_min = in.prefill_min_rows ? in.prefill_min_rows : DEFAULT_PREFILL_MIN_ROWS;
   const bool pf_ok = in.scale > 0.f && in.layout == LAYOUT_TILES && in.prefill_supported;
   if (pf_ok) {
@@ -191,6 +198,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
     // plus the merge's estimate is below PF_CUT_GAIN of the whole units' largest load; a first
     // bound on its load is the tiles shared evenly with about one more piece per workgroup.
     const double whole = assign_whole_units(units, slots, lists);
+    pf_load = whole;
     double w_cut = 0.0;
     for (const PfUnit& u : units) w_cut += u.tiles * u.cpt;
     const double cap = (w_cut + PF_UNIT_COST * ((double)units.size() + slots)) / std::max<uint32_t>(slots, 1);
@@ -320,6 +328,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
                            (decode_tiles == 0 && partials > 0 ? PF_MERGE_LAUNCH : 0.0);
       const double cut_load = *std::max_element(load.begin(), load.end()) + merge;
       if (fits && cut_load < PF_CUT_GAIN * whole) {
+        pf_load = cut_load;
         lists.reset(n_wg, units.size() + n_wg);
         for (size_t ui = 0; ui < units.size(); ui++) emit_pieces(units[ui], cuts[ui]);
         lists.n_wg = 0;   // workgroups past the last one given a piece stay unlaunched
@@ -404,6 +413,11 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   //    chunk above: the kernel's 4-wave workgroups; a row's split count rounded up to 1, 2 or 4
   //    (items of (chunk/2, chunk] tiles; every item still resident in one round: at most 4/3 of
   //    the target of half the capacity).
+  //  - matrix-core pages beside prefill units (one mixed launch): its 8-wave decode workgroups,
+  //    split counts rounded up to 1, 2, 4 or 8, the chunk grown (to at most 64 tiles) until no row
+  //    splits more than 8 ways, as long as the longest item's estimate stays well within the
+  //    prefill part's (c5: 992 items of up to 36 tiles and 128 merges in a merge launch become
+  //    items of up to 64 tiles merged in place; the decode part finishes long before the prefill).
   uint64_t (*split_of)(uint64_t n_t, uint64_t chunk) = nullptr;
   if (in.layout == LAYOUT_TILES && !in.decode_target_items && !in.decode_min_tiles) {
     uint64_t max_nt = 0;
@@ -419,6 +433,17 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
         const uint64_t k = (n_t + c - 1) / c;
         return k <= 1 ? 1 : k <= 2 ? 2 : 4;
       };
+    } else if (mfma_decode && in.mfma_local_ok && !o.pitems.empty() && max_nt > chunk) {
+      const uint64_t c8 = std::max<uint64_t>(chunk, (max_nt + MIXED_LOCAL_WAVES - 1) / MIXED_LOCAL_WAVES);
+      if (c8 <= 64 && (double)c8 * DECODE_WAVE_TILE <= MIXED_DECODE_SLACK * pf_load) {
+        chunk = c8;
+        o.chunk = (uint32_t)c8;
+        o.local = MIXED_LOCAL_WAVES;
+        split_of = [](uint64_t n_t, uint64_t c) -> uint64_t {
+          const uint64_t k = (n_t + c - 1) / c;
+          return k <= 1 ? 1 : k <= 2 ? 2 : k <= 4 ? 4 : 8;
+        };
+      }
     }
   }
   if (o.local) {

@@ -49,6 +49,7 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 constexpr int PW = 8;          // waves per workgroup
 constexpr int NT = 64 * PW;    // threads per workgroup
+static_assert(PW == MIXED_LOCAL_WAVES, "a mixed launch's decode workgroups hold the planner's local groups");
 constexpr int COLS = 32;       // columns per wave (two 16-column MFMA blocks)
 constexpr int NCB = COLS / 16;
 constexpr int BK = 64;         // keys per tile (4 page tiles of 16)
@@ -923,7 +924,9 @@ void prefill_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* items, uint32
 // release. The decode waves fit the same register budget (two waves per SIMD) and each
 // workgroup carries the prefill LDS allocation, so a CU holds one workgroup of either kind: the
 // same eight waves per CU the decode kernel runs at. One launch instead of a decode launch on a
-// second stream saves the two cross-stream waits and their idle gaps.
+// second stream saves the two cross-stream waits and their idle gaps. r.local_merge (= PW): a
+// split row's items are waves of one decode workgroup and merge there, in the workgroup's LDS
+// (no merge launch).
 template <int KVT, int HD, bool PLO, bool QS>
 __global__ __launch_bounds__(NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_t per_wg, uint32_t pf_wg, RowGeom r,
@@ -935,6 +938,14 @@ void mixed_kernel(PageGeom g, PrefillGeom pg, const PrefillItem* pitems, uint32_
   }
   const uint32_t b = blockIdx.x - pf_wg;
   const uint32_t wi = b * PW + (threadIdx.x >> 6);
+  if (r.local_merge) {   // uniform over the launch
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    float* lp = (float*)smem;   // PW partials: within the prefill allocation every workgroup carries
+    if (wi < n_items) dtile::decode_item<KVT, HD, HD, true>(g, r, items, wi, q, out, part, lp);
+    __syncthreads();   // every wave of the workgroup, with an item or not
+    if (wi < n_items) dtile::local_merge<HD, PW>(r, items, wi, lp, out);
+    return;
+  }
   if (wi < n_items) dtile::decode_item<KVT, HD, HD>(g, r, items, wi, q, out, part);
 }
 
@@ -967,6 +978,8 @@ hipError_t launch_mixed_t(const PageGeom& g, const PrefillGeom& pg, const Prefil
                           hipStream_t s, const LaunchEv& ev) {
   const uint32_t lds = (uint32_t)prefill_lds_bytes(KVT, HD, max_pages, per_wg);
   const uint32_t n_wg = pf_wg + (n_items + PW - 1) / PW;
+  if (r.local_merge && (r.local_merge != (uint32_t)PW || lds < PW * dtile::local_partial_floats<HD>() * sizeof(float)))
+    return hipErrorInvalidValue;
 #define LMH_MIXED_LAUNCH(P, S)                                                                               \
   LMH_LAUNCH(ev, (mixed_kernel<KVT, HD, P, S>), dim3(n_wg), dim3(NT), lds, s, g, pg, pitems, per_wg, pf_wg, r, items, \
              n_items, q, out, part, mc)

@@ -33,6 +33,8 @@ constexpr int LOCAL_WAVES = 8;               // waves per workgroup of an f32 lo
 // of up to 8 splits: c2 (rows of 512-4,096 keys) ran its 1,328 items on 166 such workgroups, the
 // CUs left idle slowed the kernel from 50.0 to 62.8 us, more than the merge launch costs.
 constexpr int MFMA_LOCAL_WAVES = 4;
+// The decode workgroups of a mixed launch (prefill units beside decode rows) have 8 waves.
+constexpr int MIXED_LOCAL_WAVES = 8;
 
 // Merge of `n_split` consecutive partial slots starting at `slot0` for (row, kvh, heads h0 ..
 // h0 + nh - 1). nh = 0 (a decode row's merge): up to the item's head count ng, head h0 + i at

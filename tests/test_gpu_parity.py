@@ -256,6 +256,45 @@ def test_decode_split_rows_merge_in_workgroup(cuda, kv, layer, prior, window):
     assert diff <= 2e-5, diff
 
 
+# Mixed launches (prefill units beside decode rows): split decode rows merge inside the launch's
+# 8-wave decode workgroups (groups of 8, 4, 2 and single items, the chunk grown until no row splits
+# more than 8 ways), beside prompt key pieces that the merge launch still combines, or with whole
+# units and no merge launch at all; against the oracle and against explicit split settings (the
+# decode rows' merges in the merge launch). f16, q8_0, hd 64 with a window, bf16.
+MIXED_LOCAL = [
+    ("f16", Layer(40, 8, 128, 128), [4096, 2000, 3000, 500], [512, 1, 1, 1], 0, {}),
+    ("q8_0", Layer(32, 8, 128, 128), [1000, 2500, 900], [200, 1, 1], 0, {}),
+    ("f16", Layer(16, 4, 64, 64), [2000, 1200, 3000], [100, 1, 1], 1000, {}),
+    ("bf16", Layer(32, 8, 128, 128), [3000, 1500, 700], [64, 1, 1], 0, {"prefill_whole_units": 1}),
+]
+
+
+@pytest.mark.parametrize("kv,layer,prior,new,window,tuning", MIXED_LOCAL)
+def test_mixed_launch_merges_decode_rows_in_workgroup(cuda, kv, layer, prior, new, window, tuning):
+    w = small("mloc", kv, layer, prior, new, window=window, seed=43)
+    hc, oc, q = pair(w)
+    if tuning:
+        hc.set_tuning(**tuning)
+    hc.kernel_times()
+    hc.set_timing(True)
+    got = run_gpu(hc, w, q)
+    kt_local = hc.kernel_times()
+    hc.set_tuning(decode_min_tiles=8, decode_target_items=4096)
+    glob = run_gpu(hc, w, q)
+    kt_glob = hc.kernel_times()
+    hc.set_timing(False)
+    assert kt_local["mixed"][1] == 1 and kt_glob["mixed"][1] == 1 and kt_glob["merge"][1] == 1, (kt_local, kt_glob)
+    if tuning.get("prefill_whole_units"):
+        assert kt_local["merge"][1] == 0, kt_local
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    assert np.isfinite(got).all()
+    err, err_glob, diff = row_rel_err(got, ref), row_rel_err(glob, ref), row_rel_err(got, glob)
+    print(f"{kv} {layer} prior={prior} new={new} window={window} {tuning}: local {err:.3e} merge launch "
+          f"{err_glob:.3e} local vs merge launch {diff:.3e}")
+    assert err <= TOL[kv] and err_glob <= TOL[kv], (err, err_glob)
+    assert diff <= 2e-5, diff
+
+
 # Prompt units streamed through few workgroups: each workgroup runs many units (and two passes
 # per unit when Q has bits below the cache's 16-bit type) back to back, reusing its LDS stages,
 # block-id list and Q registers from one to the next. Segments of different lengths give units
