@@ -353,7 +353,10 @@ typedef struct lmh_plan_desc {
 typedef struct lmh_plan_counts {
   uint64_t n_items, n_merges, n_units;
   uint32_t item_words, merge_words, unit_words;
-  uint32_t ng, slots, pf_wg, pf_per_wg, max_pages, local, layout;
+  uint32_t ng, slots, pf_wg, pf_per_wg, max_pages;
+  uint32_t local;   /* 0, or the waves per workgroup inside which split decode rows merge (8 for f32
+                       pages and beside prefill units, 4 for the matrix-core decode launch) */
+  uint32_t layout;
   uint32_t chunk;   /* decode split chunk in 16-key tiles */
 } lmh_plan_counts;
 int32_t lmh_plan_attend(const lmh_plan_desc* d, const lmh_seg* segs, uint64_t n_segs, uint32_t* items,
