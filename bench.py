@@ -16,7 +16,8 @@ headline line still prints): every other configuration's throughput and its laun
 (max(bytes / HBM peak, FLOPs / MFMA peak) against the kernel time, with the decode and prefill
 parts of a mixed launch), c2's geometry with every row at 2,048 keys, cold, whose rows split 4 ways
 and merge inside their workgroups (`c2u_cold`) and the same split merged by the merge launch
-(`c2u_merge_cold`), c3 with P rounded to f16 (`c3_p_f16`, Metal's prefill precision), c3's
+(`c2u_merge_cold`), c4's rows on f16 pages (`c4_f16`), c3 with P rounded to f16 (`c3_p_f16`,
+Metal's prefill precision), c3's
 prompts on q8_0 pages (`c3_q8`; `c3_q8_rows`: the same with every row sent to the decode kernels), c3
 with Q keeping all f32 bits (`c3_q_f32`: Q as f16 hi + lo parts; every other leg's Q is rounded
 to the cache's 16-bit type), a 64-token prompt chunk on a 32k prefix with its prefill units cut into
@@ -547,7 +548,7 @@ def main():
     # ~0.2 s of c2 steps: the clock needs tens of milliseconds of load to settle (10 warm-up steps
     # left the cold decode kernel at 52.7 us against 50.3 us settled)
     ap.add_argument("--warmup", type=int, default=3000)
-    ap.add_argument("--extra", default="c1,c2u_cold,c2u_merge_cold,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c5,c5w,"
+    ap.add_argument("--extra", default="c1,c2u_cold,c2u_merge_cold,c3,c3_p_f16,c3_q_f32,c3_q8,c3_q8_rows,c4,c4_f16,c5,c5w,"
                                        "chunk32k,chunk32k_whole,rope_c3,snapshot_c4,sched_c5,window_c5w",
                     help="other configs to report ('' = none)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,

@@ -237,16 +237,20 @@ __device__ __forceinline__ void decode_item(const PageGeom& g, const RowGeom& r,
   f4 O[NJ];
   bool checked = false;   // q8_0: every tile's V scales checked (the pass after an overflow)
 
-  // The item's tiles t0..t1 (at most 64, the host caps chunks): lane i holds the block id of
-  // tile t0 + i, so the loop reads ids with readlane instead of a dependent memory load.
+  // The item's tiles t0..t1 (at most MFMA_ITEM_TILES = 128, the host caps chunks): lane i holds
+  // the block ids of tiles t0 + i and t0 + 64 + i, so the loop reads ids with readlane instead of
+  // a dependent memory load.
   const uint32_t t0 = it.p0 >> 4, t1 = (it.p1 - 1) >> 4;
   const uint32_t bt_mask = (1u << g.bt_shift) - 1u;
-  int my_blk = 0;
+  int my_blk = 0, my_blk_hi = 0;
   if (t0 + lane <= t1) my_blk = tab[((t0 + lane) << 4) >> g.bt_shift];
+  if (t0 + 64 + lane <= t1) my_blk_hi = tab[((t0 + 64 + lane) << 4) >> g.bt_shift];
   auto ptrs = [&](uint32_t t, const uint8_t*& kb, const uint8_t*& vb, const uint8_t*& ksb, const uint8_t*& vsb,
                   bool first = false) {
     const uint32_t pos = t << 4;
-    const int blk = first ? (int)it.blk0 : __builtin_amdgcn_readlane(my_blk, (int)(t - t0));
+    const uint32_t d = t - t0;   // wave-uniform
+    const int blk = first ? (int)it.blk0
+                          : d < 64 ? __builtin_amdgcn_readlane(my_blk, (int)d) : __builtin_amdgcn_readlane(my_blk_hi, (int)(d - 64));
     const uint32_t sub = (pos & bt_mask) >> 4;
     const uint8_t* base = g.pool + (size_t)blk * g.block_bytes;
     const uint8_t* kh = base + g.k_off + it.kvh * g.k_head;

@@ -392,16 +392,21 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   // more, shorter items hide it better); 4 for the row layout.
   const uint64_t min_chunk = in.decode_min_tiles ? in.decode_min_tiles
                                                  : (in.layout == LAYOUT_ROWS ? 4 : in.kv_type == LMH_KV_F32 ? 2 : 8);
-  // chunks of whole tiles; at most 64 per item (the decode kernel keeps one block id per lane);
-  // grown until the rows' rounded-up split counts fit the target
+  // chunks of whole tiles, grown until the rows' rounded-up split counts fit the target; at most
+  // 128 per item on the matrix-core kernel for f16 / bf16 pages (two block ids per lane), 64 on the
+  // others (one). Long rows reach the cap: at 128 their items halve to one wave per SIMD (8 rows x
+  // 32 K keys, f16: step 172.5 -> 164.6 us; bf16 170.9 -> 165.3; 16 x 16 K 169.5 -> 163.1), while
+  // q8_0, whose tiles carry ~4x the VALU work, needs two waves per SIMD to hide its loads (c4 97.3
+  // -> 103.3 us at 128).
+  const uint64_t max_chunk = mfma_decode && in.kv_type != LMH_KV_Q8_0 ? MFMA_ITEM_TILES : ITEM_TILES;
   auto n_items_for = [&](uint64_t c) {
     uint64_t n = 0;
     for (uint64_t t = 0; t < n_rows; t++)
       if (o.decode_row[t]) n += (row_tiles(t) + c - 1) / c;
     return n * in.n_kv * head_blocks;
   };
-  uint64_t chunk = std::min<uint64_t>(64, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / target));
-  while (chunk < 64 && n_items_for(chunk) > target) chunk++;
+  uint64_t chunk = std::min<uint64_t>(max_chunk, std::max<uint64_t>(min_chunk, (total_tiles + target - 1) / target));
+  while (chunk < max_chunk && n_items_for(chunk) > target) chunk++;
   o.chunk = (uint32_t)chunk;
   // Split rows that merge inside their workgroup (no partials in HBM, no merge launch). A row's
   // split count n is 1, 2, 4 or 8 and its items are consecutive waves of one workgroup: groups of
@@ -414,7 +419,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   //    (items of (chunk/2, chunk] tiles; every item still resident in one round: at most 4/3 of
   //    the target of half the capacity).
   //  - matrix-core pages beside prefill units (one mixed launch): its 8-wave decode workgroups,
-  //    split counts rounded up to 1, 2, 4 or 8, the chunk grown (to at most 64 tiles) until no row
+  //    split counts rounded up to 1, 2, 4 or 8, the chunk grown (within the item cap) until no row
   //    splits more than 8 ways, as long as the longest item's estimate stays well within the
   //    prefill part's (c5: 992 items of up to 36 tiles and 128 merges in a merge launch become
   //    items of up to 64 tiles merged in place; the decode part finishes long before the prefill).
@@ -435,7 +440,7 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
       };
     } else if (mfma_decode && in.mfma_local_ok && !o.pitems.empty() && max_nt > chunk) {
       const uint64_t c8 = std::max<uint64_t>(chunk, (max_nt + MIXED_LOCAL_WAVES - 1) / MIXED_LOCAL_WAVES);
-      if (c8 <= 64 && (double)c8 * DECODE_WAVE_TILE <= MIXED_DECODE_SLACK * pf_load) {
+      if (c8 <= max_chunk && (double)c8 * DECODE_WAVE_TILE <= MIXED_DECODE_SLACK * pf_load) {
         chunk = c8;
         o.chunk = (uint32_t)c8;
         o.local = MIXED_LOCAL_WAVES;

@@ -22,6 +22,10 @@ struct DecodeItem {
   uint32_t blk0;  // block id of the first tile p0 >> 4 (the first fetch skips the block-table read)
 };
 constexpr uint32_t NO_SLOT = 0xffffffffu;
+// Tiles per decode item: the matrix-core kernel keeps two block ids per lane (the planner uses the
+// second for f16 / bf16 pages), the f32 and row-layout kernels one.
+constexpr uint32_t MFMA_ITEM_TILES = 128;
+constexpr uint32_t ITEM_TILES = 64;
 // A split item merged inside its workgroup (f32 decode of short rows; matrix-core decode whose rows
 // split at most MFMA_LOCAL_WAVES ways): LOCAL_SLOT | (its index in the row's group << 8) | the
 // group's size; the group's items are consecutive waves of one workgroup, which merges their

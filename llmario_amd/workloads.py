@@ -119,7 +119,7 @@ def config(name: str) -> Workload:
     """The BASELINE.json configurations by name: c1 .. c5, c5w (window 4096); c3_q8 is c3 on q8_0 pages;
     chunk32k is a long-prefix prompt chunk (few, long prefill units: the key-piece case); c2u is
     c2's geometry with every row at 2,048 keys (rows that split 4 ways: the decode kernel's
-    in-workgroup merge)."""
+    in-workgroup merge); c4_f16 is c4 on f16 pages."""
     if name == "c1":
         return Workload("c1", "f32", Layer(8, 8, 64, 64), prior=[255], new=[1], seed=1)
     if name == "c2":
@@ -135,6 +135,8 @@ def config(name: str) -> Workload:
         return Workload("c3_q8", "q8_0", Layer(32, 8, 128, 128), prior=[0] * 4, new=[2048] * 4, seed=3)
     if name == "c4":
         return Workload("c4", "q8_0", Layer(64, 8, 128, 128), prior=[32767] * 8, new=[1] * 8, seed=4)
+    if name == "c4_f16":   # c4's rows on f16 pages (items of up to 128 tiles, one wave per SIMD)
+        return Workload("c4_f16", "f16", Layer(64, 8, 128, 128), prior=[32767] * 8, new=[1] * 8, seed=4)
     if name in ("c5", "c5w"):
         rng = np.random.default_rng(5)
         ctx = rng.integers(1024, 8192, size=16, endpoint=True)

@@ -377,7 +377,7 @@ def test_prefill_key_pieces(cuda, kv, geo, prior, new, window, bt, q_kind):
     assert err <= TOL[kv] and err_w <= TOL[kv], (err, err_w)
 
 
-@pytest.mark.parametrize("name", ["c1", "c2", "c2u", "c4"])
+@pytest.mark.parametrize("name", ["c1", "c2", "c2u", "c4", "c4_f16"])
 def test_attend_config_all_rows(cuda, name):
     w = config(name)
     hc, oc, q = pair(w)

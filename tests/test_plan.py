@@ -63,6 +63,7 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
     n_rows = len(rows)
     blk = lambda s, p: int(table[s, p // bt])
     covered = np.zeros((n_rows, n_head), np.int32)
+    item_tiles = 128 if kv in ("f16", "bf16") and c.layout == 0 else 64
     # ---- decode items
     slots_seen = set()
     by_key = {}
@@ -73,7 +74,7 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
         assert seq == s
         lo, hi = key_lo(pos, window), pos + 1
         assert lo <= p0 < p1 <= hi, (p0, p1, lo, hi)
-        assert (p1 - 1) // 16 - p0 // 16 + 1 <= 64           # one block id per lane
+        assert (p1 - 1) // 16 - p0 // 16 + 1 <= item_tiles   # block ids per lane: two (matrix cores), one
         assert blk0 == blk(s, p0 // 16 * 16)   # the block of the 16-key tile holding p0
         by_key.setdefault((row, kvh, h0), []).append((p0, p1, slot))
     for (row, kvh, h0), parts in by_key.items():
@@ -120,10 +121,10 @@ def check_plan(kv, n_head, n_kv, hd, hdv, bt, table, segs, window, items, merges
     assert len(dec_merges) == sum(1 for p in by_key.values() if len(p) > 1) or c.local
     if noalloc and c.slots:
         # the split target is capped to what the no-allocation scratch holds; a call whose rows
-        # still need more (chunks at their 64-tile maximum) is refused by lmh_attend_noalloc
+        # still need more (chunks at their maximum) is refused by lmh_attend_noalloc
         slot_bytes = c.ng * (hdv + 4) * 4
         fits = ((c.slots * slot_bytes + 255) // 256 * 256 + len(merges) * 24) <= 32 << 20
-        assert fits or c.chunk == 64
+        assert fits or c.chunk == item_tiles
     # ---- prefill units: pf_wg lists of pf_per_wg, empty units only at a list's end
     assert len(units) == c.pf_wg * c.pf_per_wg
     for wgi in range(c.pf_wg):

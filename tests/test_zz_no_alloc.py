@@ -78,10 +78,10 @@ def test_noalloc_prompt_key_pieces(cuda, prior):
 
 def test_noalloc_refuses_a_call_beyond_its_scratch(cuda):
     import torch
-    # group 16 (16 heads per item) and 32 rows x 8 KV heads x 16 splits of 1024 keys: 4096 split
-    # slots of 8448 bytes, more than the 32 MiB scratch
+    # group 16 (16 heads per item) and 32 rows x 8 KV heads x 16 splits of 2048 keys (items of at
+    # most 128 tiles): 4096 split slots of 8448 bytes, more than the 32 MiB scratch
     L = Layer(128, 8, 128, 128)
-    ctx = 16384
+    ctx = 32768
     hc = HipKvCache([L], max_ctx=ctx, n_seqs=32, kv_type="f16", block_tokens=16)
     segs_l, n = hc.prepare_batch([(s, ctx) for s in range(32)])
     hc.commit_batch(segs_l)
