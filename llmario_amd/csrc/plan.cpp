@@ -451,23 +451,47 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
       }
     }
   }
+  // A row's key range cut into k pieces of whole tiles, [tlo + floor(s n_t / k), tlo +
+  // floor((s + 1) n_t / k)) clipped to [lo, pos], with the block id of each piece's first tile:
+  // computed once per row (its KV heads and head blocks share them), the floors by increments
+  // (q = n_t / k whole tiles each, the remainders carried) instead of two divisions per item.
+  struct Piece {
+    uint32_t p0, p1, blk0;
+  };
+  std::vector<Piece> pieces;
+  auto cut_row = [&](uint64_t t, uint64_t k) {
+    const uint64_t pos = (uint64_t)in.row_pos[t];
+    const uint64_t lo = key_lo(pos, window), hi = pos + 1;
+    const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
+    const uint64_t seq = (uint64_t)in.row_seq[t];
+    const uint64_t q = n_t / k, r = n_t % k;
+    pieces.clear();
+    uint64_t a = tlo, carry = 0;
+    for (uint64_t s = 0; s < k; s++) {
+      uint64_t b = a + q;
+      carry += r;
+      if (carry >= k) {
+        carry -= k;
+        b++;
+      }
+      const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
+      pieces.push_back(Piece{(uint32_t)p0, (uint32_t)p1, blk_at(seq, p0)});
+      a = b;
+    }
+  };
   if (o.local) {
     std::vector<DecodeItem> by_size[4];   // groups of 8, 4, 2, single items
     for (uint64_t t = 0; t < n_rows; t++) {
       if (!o.decode_row[t]) continue;
-      const uint64_t pos = (uint64_t)in.row_pos[t];
-      const uint64_t lo = key_lo(pos, window), hi = pos + 1;
-      const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
-      const uint32_t n = (uint32_t)split_of(n_t, chunk);
+      const uint32_t n = (uint32_t)split_of(row_tiles(t), chunk);
+      cut_row(t, n);
       std::vector<DecodeItem>& dst = by_size[n == 8 ? 0 : n == 4 ? 1 : n == 2 ? 2 : 3];
       const uint32_t seq = (uint32_t)in.row_seq[t];
       for (uint32_t kvh = 0; kvh < in.n_kv; kvh++) {
         for (uint32_t hb = 0; hb < head_blocks; hb++) {
           for (uint32_t s = 0; s < n; s++) {
-            const uint64_t a = tlo + s * n_t / n, b = tlo + (s + 1) * n_t / n;
-            const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
             const uint32_t slot = n == 1 ? NO_SLOT : LOCAL_SLOT | (s << 8) | n;
-            dst.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, slot, seq, blk_at(seq, p0)});
+            dst.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, pieces[s].p0, pieces[s].p1, slot, seq, pieces[s].blk0});
           }
         }
       }
@@ -477,23 +501,18 @@ void plan_attend(const PlanIn& in, PlanOut& o) {
   }
   for (uint64_t t = 0; t < n_rows; t++) {
     if (!o.decode_row[t]) continue;
-    const uint64_t pos = (uint64_t)in.row_pos[t];
-    const uint64_t lo = key_lo(pos, window), hi = pos + 1;
-    const uint64_t tlo = lo / 16, n_t = pos / 16 - tlo + 1;
-    const uint64_t n_split = (n_t + chunk - 1) / chunk;
+    const uint64_t n_split = (row_tiles(t) + chunk - 1) / chunk;
+    cut_row(t, n_split);
     const uint32_t seq = (uint32_t)in.row_seq[t];
     for (uint32_t kvh = 0; kvh < in.n_kv; kvh++) {
       for (uint32_t hb = 0; hb < head_blocks; hb++) {
         if (n_split == 1) {
-          o.items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)lo, (uint32_t)hi, NO_SLOT, seq, blk_at(seq, lo)});
+          o.items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, pieces[0].p0, pieces[0].p1, NO_SLOT, seq, pieces[0].blk0});
           continue;
         }
         o.merges.push_back(MergeItem{(uint32_t)t, kvh, hb * ng, o.slots, (uint32_t)n_split, 0});   // nh 0: ng heads
-        for (uint64_t s = 0; s < n_split; s++) {
-          const uint64_t a = tlo + s * n_t / n_split, b = tlo + (s + 1) * n_t / n_split;
-          const uint64_t p0 = std::max(lo, a * 16), p1 = std::min(hi, b * 16);
-          o.items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, (uint32_t)p0, (uint32_t)p1, o.slots++, seq, blk_at(seq, p0)});
-        }
+        for (uint64_t s = 0; s < n_split; s++)
+          o.items.push_back(DecodeItem{(uint32_t)t, kvh, hb * ng, pieces[s].p0, pieces[s].p1, o.slots++, seq, pieces[s].blk0});
       }
     }
   }
