@@ -295,6 +295,25 @@ def test_mixed_launch_merges_decode_rows_in_workgroup(cuda, kv, layer, prior, ne
     assert diff <= 2e-5, diff
 
 
+# Rows long enough that decode items reach the 128-tile cap of f16 / bf16 pages (each lane keeps two
+# block ids): 32 rows x 32 K keys over 2 KV heads (group 8), against the oracle on every row; the
+# planner's chunk is checked on the CPU for the same geometry.
+@pytest.mark.parametrize("kv", ["f16", "bf16"])
+def test_decode_items_of_128_tiles(cuda, kv):
+    from test_plan import contiguous_table, plan
+    prior = [32767 - 97 * i for i in range(32)]
+    segs = [(s, s, 1, p) for s, p in enumerate(prior)]
+    _, _, _, c = plan(kv, 16, 2, 128, 128, 16, contiguous_table([p + 1 for p in prior], 16), segs)
+    assert c.chunk > 64, c.chunk
+    w = small("i128", kv, Layer(16, 2, 128, 128), prior, [1] * 32, seed=47)
+    hc, oc, q = pair(w)
+    got = run_gpu(hc, w, q)
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    err = row_rel_err(got, ref)
+    print(f"{kv}: items of up to {c.chunk} tiles, max row rel err {err:.3e}")
+    assert np.isfinite(got).all() and err <= TOL[kv], err
+
+
 # Prompt units streamed through few workgroups: each workgroup runs many units (and two passes
 # per unit when Q has bits below the cache's 16-bit type) back to back, reusing its LDS stages,
 # block-id list and Q registers from one to the next. Segments of different lengths give units
