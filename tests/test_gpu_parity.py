@@ -314,6 +314,26 @@ def test_decode_items_of_128_tiles(cuda, kv):
     assert np.isfinite(got).all() and err <= TOL[kv], err
 
 
+# Split-K partial slots reused from call to call: a first call whose rows split up to 15 ways fills
+# more slots than the next call on the same handle (the same sequences at earlier positions, rows
+# split at most 8 ways) writes, so the partial buffer holds the first call's partials past the
+# second's; each merge reads only its own call's. Both calls against the oracle.
+def test_merges_after_a_larger_call(cuda):
+    w = small("strided", "f16", Layer(32, 8, 128, 128), prior=[1900, 1500, 1200, 900, 400, 1800, 100, 1000],
+              new=[1] * 8, seed=51)
+    hc, oc, q = pair(w)
+    got = run_gpu(hc, w, q)
+    ref = oc.attend(0, w.segments(), q, w.scale, w.window, THREADS)
+    err = row_rel_err(got, ref)
+    segs2 = [(s, start, n, p // 2) for (s, start, n, p) in w.segments()]
+    got2 = run_gpu(hc, w, q, segs2)
+    ref2 = oc.attend(0, segs2, q, w.scale, w.window, THREADS)
+    err2 = row_rel_err(got2, ref2)
+    print(f"first call {err:.3e}, second call {err2:.3e}")
+    assert np.isfinite(got).all() and np.isfinite(got2).all()
+    assert err <= TOL["f16"] and err2 <= TOL["f16"], (err, err2)
+
+
 # Prompt units streamed through few workgroups: each workgroup runs many units (and two passes
 # per unit when Q has bits below the cache's 16-bit type) back to back, reusing its LDS stages,
 # block-id list and Q registers from one to the next. Segments of different lengths give units
