@@ -264,11 +264,12 @@ class Pool:
 
     def __init__(self, n_blocks=0, block_tokens=16, block_bytes=0, handle=None):
         self._own = handle is None
+        self._free = lib().orc_pool_free   # held here: at interpreter exit the module's globals may be gone
         self.h = lib().orc_pool_new(n_blocks, block_tokens, block_bytes) if handle is None else handle
 
     def __del__(self):
         if getattr(self, "_own", False) and self.h:
-            lib().orc_pool_free(self.h)
+            self._free(self.h)
             self.h = None
 
     def free_blocks(self) -> int:
@@ -326,12 +327,13 @@ class Cache:
         self.layers = [tuple(int(v) for v in g) for g in layers]  # (n_head, n_kv, hd, hdv)
         geo = (LayerGeom * len(layers))(*[LayerGeom(*g) for g in self.layers])
         o = Options(max_ctx, n_seqs, block_tokens, pool_tokens, kv_type)
+        self._free = lib().orc_cache_free   # held here: at interpreter exit the module's globals may be gone
         self.h = lib().orc_cache_new(C.byref(o), geo, len(layers))
         self.pool = Pool(handle=lib().orc_cache_pool(self.h))
 
     def __del__(self):
         if getattr(self, "h", None):
-            lib().orc_cache_free(self.h)
+            self._free(self.h)
             self.h = None
 
     def layout(self) -> dict:
