@@ -155,7 +155,10 @@ class Scheduler:
     def __del__(self):
         h = getattr(self, "h", None)
         if h:
-            N.lib().lmh_sched_destroy(h)
+            lib = getattr(N, "lib", None)
+            if lib is None:  # interpreter shutdown: the module is already torn down
+                return
+            lib().lmh_sched_destroy(h)
             self.h = None
 
     def _check(self, rc: int, what: str):
