@@ -1305,12 +1305,13 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
                                 hipStream_t s, const LaunchEv& ev) {
   if (n_rows == 0) return hipSuccess;
   // register path: hd == hdv = 64*VPL; Normal pairs are always in-lane (VPL >= 2) or one lane
-  // apart; Neox partners are half_rot/VPL lanes apart, which must be a whole power of two
+  // apart; Neox partners are half_rot/VPL lanes apart, which must be a whole power of two. The
+  // tile layout's widths stop at 256, so VPL is 1, 2 or 4.
   const uint32_t vpl = g.hd / 64, half = r.half_rot;
   const bool neox = (r.flags & ROPE_NEOX) != 0;
   const bool pairs_ok = half == 0 || !neox || (half % vpl == 0 && ((half / vpl) & (half / vpl - 1)) == 0);
   const bool reg = g.layout == LAYOUT_TILES && g.hd == g.hdv && g.hd % 64 == 0 &&
-                   (vpl == 1 || vpl == 2 || vpl == 4 || vpl == 8) && pairs_ok;
+                   (vpl == 1 || vpl == 2 || vpl == 4) && pairs_ok;
   if (reg) {
     // aligned runs of 4 f16 / bf16 rows (when the caller found any) with the other rows, or a
     // short call of any type (decode rows), go to the split kernel: one launch, each row's heads
@@ -1362,8 +1363,7 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
       switch (vpl) {
         case 1: LMH_QUAD(1); break;
         case 2: LMH_QUAD(2); break;
-        case 4: LMH_QUAD(4); break;
-        default: LMH_QUAD(8); break;
+        default: LMH_QUAD(4); break;
       }
 #undef LMH_QUAD
       return hipGetLastError();
@@ -1371,8 +1371,7 @@ hipError_t launch_qk_rope_store(const PageGeom& g, const RopeGeom& r, const int3
     switch (vpl) {
       case 1: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<1>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
       case 2: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<2>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      case 4: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
-      default: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<8>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
+      default: LMH_LAUNCH(ev, qk_rope_store_reg_kernel<4>, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out); break;
     }
   } else {
     LMH_LAUNCH(ev, qk_rope_store_kernel, dim3(n_rows), dim3(256), 0, s, g, r, row_seq, row_pos, q, k, v, q_out);

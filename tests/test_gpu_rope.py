@@ -63,22 +63,40 @@ CASES = [
     ("f16", 6, 2, 64, 64, 64, True, True, False, True, 0, True, 1e4),
     ("f16", 9, 3, 128, 128, 128, True, True, True, True, 0, False, 1e4),
     ("bf16", 4, 1, 128, 128, 128, False, True, True, False, 256, False, 1e4),
+    ("f16", 4, 2, 256, 256, 256, False, True, True, False, 0, False, 1e4),
 ]
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"{c[0]}-h{c[1]}x{c[2]}-hd{c[3]}-rot{c[5]}-{'neox' if c[6] else 'norm'}")
 def test_qk_rope_store_matches_oracle(cuda, case):
+    # three sequences: one row at a large position, a 37-row chunk, a 5-row chunk mid-context
+    check_case(case, 100 + CASES.index(case), [32760, 0, 1000], [(0, 1), (1, 37), (2, 5)], 40000)
+
+
+# Calls of 1,024 rows or more with no aligned runs of 4 f16 / bf16 rows (q8_0 and f32 pages) take
+# the row kernel of the register path (each row's heads in one workgroup), at each of its widths.
+LONG = [
+    ("q8_0", 8, 2, 64, 64, 64, True, True, True, False, 0, False, 1e4),
+    ("f32", 8, 2, 128, 128, 128, False, True, False, True, 0, True, 1e6),
+    ("q8_0", 4, 2, 256, 256, 256, True, False, True, False, 0, False, 1e6),
+]
+
+
+@pytest.mark.parametrize("case", LONG, ids=lambda c: f"{c[0]}-hd{c[3]}")
+def test_qk_rope_store_long_calls_match_oracle(cuda, case):
+    check_case(case, 200 + LONG.index(case), [0, 500, 0], [(0, 1030), (1, 3), (2, 1)], 2048)
+
+
+def check_case(case, seed, prior, batch, max_ctx):
     import torch
     kv_type, nh, nk, hd, hdv, rot, neox, qn, kn, vn, q_stride, div, theta = case
-    rng = np.random.default_rng(100 + CASES.index(case))
-    hc = HipKvCache([Layer(nh, nk, hd, hdv)], max_ctx=40000, n_seqs=3, kv_type=kv_type, block_tokens=16)
-    # three sequences: one row at a large position, a 37-row chunk, a 5-row chunk mid-context
-    prior = [32760, 0, 1000]
+    rng = np.random.default_rng(seed)
+    hc = HipKvCache([Layer(nh, nk, hd, hdv)], max_ctx=max_ctx, n_seqs=len(prior), kv_type=kv_type, block_tokens=16)
     for s, p in enumerate(prior):
         if p:
             hc.reserve(s, p)
             hc.set_len(s, p)
-    segs, n = hc.prepare_batch([(0, 1), (1, 37), (2, 5)])
+    segs, n = hc.prepare_batch(batch)
     pos = np.concatenate([np.arange(p0, p0 + m) for (_, _, m, p0) in segs]).astype(np.uint32)
     qs = q_stride or hd
     q = (rng.standard_normal((n, nh, qs)) * 2).astype(np.float32)

@@ -17,20 +17,20 @@ pytestmark = pytest.mark.gpu
 LAYERS = [(8, 2, 128, 128), (4, 4, 64, 64)]
 
 
-def twin(kv_type, n_seqs=3, max_ctx=512, pool_tokens=0, bt=16):
-    hc = HipKvCache([Layer(*g) for g in LAYERS], max_ctx=max_ctx, n_seqs=n_seqs, kv_type=kv_type,
+def twin(kv_type, n_seqs=3, max_ctx=512, pool_tokens=0, bt=16, layers=LAYERS):
+    hc = HipKvCache([Layer(*g) for g in layers], max_ctx=max_ctx, n_seqs=n_seqs, kv_type=kv_type,
                     block_tokens=bt, pool_tokens=pool_tokens)
-    oc = O.Cache(LAYERS, max_ctx=max_ctx, n_seqs=n_seqs, kv_type=kv_type, block_tokens=bt, pool_tokens=pool_tokens)
+    oc = O.Cache(layers, max_ctx=max_ctx, n_seqs=n_seqs, kv_type=kv_type, block_tokens=bt, pool_tokens=pool_tokens)
     return hc, oc
 
 
-def step(hc, oc, batch, rng):
+def step(hc, oc, batch, rng, layers=LAYERS):
     """One batch on both caches: the same rows stored through each cache's own store path."""
     import torch
     segs_h, n = hc.prepare_batch(batch)
     segs_o, n_o = oc.prepare_batch(batch)
     assert segs_h == segs_o and n == n_o
-    for l, (nh, nk, hd, hdv) in enumerate(LAYERS):
+    for l, (nh, nk, hd, hdv) in enumerate(layers):
         k = (rng.standard_normal((n, nk * hd)) * 2).astype(np.float32)
         v = rng.standard_normal((n, nk * hdv)).astype(np.float32)
         hc.store(l, segs_h, torch.from_numpy(k).cuda(), torch.from_numpy(v).cuda())
@@ -97,3 +97,42 @@ def test_read_seq_without_room_changes_nothing(cuda):
     with pytest.raises(LmhError):
         hc.read_seq(0, 61, snap)                                    # size does not match the length
     assert hc.snapshot_bytes(0) == 0 and hc.write_seq(0).numel() == 0
+
+
+# Each snapshot launch, written and read: the side kernel (tile layout, f16 / bf16 / q8_0 at hd 64,
+# 128, 256) at the widths and types the cases above leave out, the tiles kernel (tile layout at
+# other widths, f32 pages), and the row kernels (the row layout: a width without a tile instance,
+# blocks of 8 positions).
+ROUND_TRIP = [
+    ("f16", [(8, 2, 256, 256)], 16),
+    ("bf16", [(8, 2, 64, 64), (8, 2, 128, 128), (4, 2, 256, 256)], 16),
+    ("q8_0", [(8, 2, 256, 256)], 16),
+    ("f16", [(12, 4, 96, 96)], 16),
+    ("f32", [(8, 2, 128, 128)], 16),
+    ("f16", [(8, 2, 80, 80)], 16),
+    ("bf16", [(8, 2, 64, 64)], 8),
+]
+
+
+@pytest.mark.parametrize("kv_type,layers,bt", ROUND_TRIP,
+                         ids=[f"{k}-{'-'.join(str(g[2]) for g in ls)}-bt{b}" for k, ls, b in ROUND_TRIP])
+def test_snapshot_round_trip_every_launch(cuda, kv_type, layers, bt):
+    """write_seq equals the reference-format snapshot byte for byte; read_seq of that snapshot into
+    another sequence restores every encoded row, and writing it again gives the same bytes."""
+    import torch
+    rng = np.random.default_rng(13)
+    hc, oc = twin(kv_type, bt=bt, layers=layers)
+    step(hc, oc, [(0, 70), (1, 33)], rng, layers)
+    for s, n in ((0, 70), (1, 33)):
+        snap = oc.write_seq(s)
+        assert np.array_equal(hc.write_seq(s).cpu().numpy(), snap), f"write seq {s}"
+        hc.read_seq(2, n, torch.from_numpy(snap).cuda())
+        assert hc.len(2) == n
+        assert np.array_equal(hc.write_seq(2).cpu().numpy(), snap), f"read seq {s}"
+        for l in range(len(layers)):
+            kr = torch.empty((n, oc.layer(l)["k_row"]), dtype=torch.uint8, device="cuda")
+            vr = torch.empty((n, oc.layer(l)["v_row"]), dtype=torch.uint8, device="cuda")
+            hc.gather_encoded(l, [(2, 0, n, 0)], kr, vr)
+            torch.cuda.synchronize()
+            ko, vo = oc.load_rows_raw(s, l, 0, n)
+            assert np.array_equal(kr.cpu().numpy(), ko) and np.array_equal(vr.cpu().numpy(), vo), (s, l)
